@@ -1,0 +1,184 @@
+/*
+ * HIP (gfx950 / MI355X) backend slot for TinyEngine's attention step.
+ *
+ * This header takes the place of the reference GPU backend contract
+ * c/src/metal_backend.h for the attention step only, with the same
+ * conventions (metal_backend.h:13-347, metal_backend_layers.mm.inc:529-556,
+ * :670-720):
+ *   - every entry point is extern "C" and returns te_status;
+ *   - NULL / zero / inconsistent arguments  -> TE_STATUS_INVALID_ARGUMENT;
+ *   - a shape, cap or device the kernels do not handle -> TE_STATUS_UNSUPPORTED
+ *     (callers read it as "take another path");
+ *   - a failed HIP call or launch -> TE_STATUS_RUNTIME_ERROR;
+ *   - a failed device allocation -> TE_STATUS_OUT_OF_MEMORY.
+ *
+ * Two kinds of entry points:
+ *   - te_hip_* taking DEVICE pointers and a stream (`void *stream`, a
+ *     hipStream_t; NULL = the null stream).  They only enqueue work and return;
+ *     they are the fast path the benchmark measures.
+ *   - te_hip_attention_*_mma_f32 taking HOST pointers: synchronous twins of the
+ *     reference's MMA attention test entry points (metal_backend.h:104-142),
+ *     serialized by the library's process-wide mutex.
+ *
+ * Data layout in HBM (all row-major, innermost dimension last):
+ *   query/out  fp32  [seqs][layers][tokens][heads][head_dim]
+ *   k, v (new) fp32  [seqs][layers][tokens][kv_heads][head_dim]
+ *   q_bias     fp32  [layers][heads*head_dim]      (NULL = no bias)
+ *   k/v_bias   fp32  [layers][kv_heads*head_dim]   (NULL = no bias)
+ *   rope_cos/sin fp32 [context_tokens][head_dim/2] (row = absolute position)
+ *   key/value_cache fp16 (IEEE binary16 bits, uint16_t)
+ *                    [seqs][layers][context_tokens][kv_heads][head_dim]
+ * The cache slot of (seq, layer, position, kv_head, i) is
+ *   (((seq*layers + layer)*context_tokens + position)*kv_heads + kv_head)*head_dim + i,
+ * i.e. the reference slot formula (layer*context_tokens + position)*kv_dim
+ * (qwen.c:805, :1034) with a leading sequence index.
+ */
+#ifndef TE_HIP_BACKEND_H
+#define TE_HIP_BACKEND_H
+
+#include "tinyengine.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Largest number of independent sequences one call accepts (positions are
+ * passed by value to the kernels). */
+#define TE_HIP_MAX_SEQS 64u
+
+/* 1 when a gfx950 device is visible and the kernels in this library can run
+ * on it, else 0.  Never aborts. */
+TE_API int te_hip_available(void);
+
+/* Writes the device name (e.g. "AMD Instinct MI355X (gfx950)") and compute-unit
+ * count.  TE_STATUS_UNSUPPORTED without a usable device. */
+TE_API te_status te_hip_device_info(char *name, size_t name_capacity, uint32_t *compute_units);
+
+/*
+ * RoPE cos/sin tables.  Replaces the table build of te_qwen_state_init
+ * (reference qwen.c:531-539): row p, column i holds cosf/sinf of
+ * (float)p * powf(theta, -(2.0f*i)/(float)head_dim), computed with the host
+ * libm exactly as the reference does, then copied to the device tables
+ * `cos_table` / `sin_table` ([context_tokens][head_dim/2] fp32, device).
+ * Synchronous.
+ */
+TE_API te_status te_hip_rope_table_f32(float *cos_table, float *sin_table, size_t context_tokens,
+                                       size_t head_dim, float theta);
+
+/*
+ * Bias + RoPE + fp16 KV append, for `tokens` tokens of each (seq, layer).
+ * Replaces te_qkv_bias_rope_cache_batch_f32 / _h_f32
+ * (metal_kernels.metal.inc:2172-2252, :2344-2429) and the CPU sequence
+ * bias-add -> te_qwen_rope_cached(q), (k) -> memcpy append
+ * (qwen.c:774-808, :998-1036).
+ *
+ * Token b of sequence s sits at position base_positions[s] + b (or
+ * base_position + b when base_positions is NULL); every position must be
+ * < context_tokens.  In place: q and k become bias-added and rotated, v becomes
+ * bias-added.  The rotated k and the biased v are rounded to fp16 (IEEE
+ * round-to-nearest-even) into the cache slot above.  When q_half is non-NULL the
+ * rotated q is also written there as fp16 (layout of `query`), the operand of
+ * te_hip_attention_prefill_f16.
+ * head_dim must be even and <= 256.  base_positions is a HOST array of `seqs`
+ * entries (seqs <= TE_HIP_MAX_SEQS).
+ */
+TE_API te_status te_hip_rope_kv_append_f16(
+    float *q, float *k, float *v,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *q_half,
+    size_t seqs, size_t layers, size_t tokens,
+    const size_t *base_positions, size_t base_position,
+    size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+    void *stream);
+
+/*
+ * GQA decode attention over the fp16 cache, one query token per (seq, layer).
+ * Replaces te_attention_decode_f32_kernel (metal_kernels.metal.inc:2431-2500)
+ * and, numerically, te_attention_decode_f32 (ops.c:323-395) fed the fp16 cache
+ * upcast to fp32.  Query token of sequence s attends cache positions
+ * 0..positions[s] inclusive (positions NULL -> `position` for all sequences;
+ * positions is a HOST array, seqs <= TE_HIP_MAX_SEQS, every position
+ * < context_tokens).
+ *
+ * Split-K ("flash-decoding"): the positions are cut into chunks, each chunk of
+ * each (seq, layer, kv_head) is one workgroup that produces an unnormalized
+ * partial (running max m, sum l, accumulator o[heads/kv_heads][head_dim]), and
+ * a combine kernel merges the partials.  Softmax and all accumulation are fp32.
+ * head_dim in {64, 128}; heads/kv_heads <= 16.
+ *
+ * workspace: device scratch of at least te_hip_attention_decode_workspace_bytes
+ * bytes, or NULL to use a buffer the library owns (grown on demand, guarded by
+ * the library mutex).  Calls sharing one workspace must be stream-ordered.
+ */
+TE_API size_t te_hip_attention_decode_workspace_bytes(size_t seqs, size_t layers, size_t max_position,
+                                                      size_t heads, size_t kv_heads, size_t head_dim);
+
+TE_API te_status te_hip_attention_decode_f16(
+    const float *query, const uint16_t *key_cache, const uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The two stages of te_hip_attention_decode_f16 as separate launches, so a
+ * caller (the benchmark) can time the split-K kernel on its own.  Same
+ * arguments; the workspace must be supplied and be the same for both calls. */
+TE_API te_status te_hip_attention_decode_splitk_f16(
+    const float *query, const uint16_t *key_cache, const uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    void *workspace, size_t workspace_bytes, void *stream);
+TE_API te_status te_hip_attention_decode_combine(
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, const void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Batched-prefill causal attention over the fp16 cache.  Replaces the CPU
+ * per-token loop (qwen.c:810-824: row t = decode at position t) and the MMA
+ * prefill kernel te_attention_flash_mma_t_f32_kernel
+ * (metal_kernels.metal.inc:2693-2836), whose mask
+ * `past <= base_position + row` defines chunked prefill.  Row t of (seq, layer)
+ * attends cache positions 0..base_position+t inclusive; the cache must already
+ * hold those positions (te_hip_rope_kv_append_f16 writes them).
+ *
+ * q_half: fp16 rotated queries [seqs][layers][tokens][heads][head_dim];
+ * out: fp32, same layout.  QK^T and PV run on fp16 MFMA with fp32 accumulation;
+ * softmax is fp32.  head_dim in {64, 128}; heads % kv_heads == 0;
+ * base_position + tokens <= context_tokens.
+ */
+TE_API te_status te_hip_attention_prefill_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *stream);
+
+/*
+ * Host-pointer twins of the reference MMA attention entry points
+ * (metal_backend.h:104-142, metal_backend.mm:30-373), same signatures and the
+ * same shape guards (q_rows == 8, head_dim == 64; k_cols == 8 for qk/tile,
+ * k_cols % 8 == 0 for stream/causal, q_base <= k_cols for causal).
+ * key_t is [head_dim][k_cols], value is [k_cols][head_dim], all fp32.  They run
+ * fp32 MFMA (v_mfma_f32_16x16x4_f32) on the GPU.
+ *   qk:     out[q][k]  = sum_d query[q][d]*key_t[d][k]
+ *   tile:   out[q][:]  = softmax_k(scale*scores) @ value, k_cols == 8
+ *   stream: same, k_cols any multiple of 8
+ *   causal: same, keys k > q_base + q masked
+ */
+TE_API te_status te_hip_attention_qk_mma_f32(const float *query, const float *key_t, size_t q_rows,
+                                             size_t k_cols, size_t head_dim, float *out);
+TE_API te_status te_hip_attention_tile_mma_f32(const float *query, const float *key_t, const float *value,
+                                               size_t q_rows, size_t k_cols, size_t head_dim, float *out);
+TE_API te_status te_hip_attention_stream_mma_f32(const float *query, const float *key_t, const float *value,
+                                                 size_t q_rows, size_t k_cols, size_t head_dim, float *out);
+TE_API te_status te_hip_attention_causal_mma_f32(const float *query, const float *key_t, const float *value,
+                                                 size_t q_rows, size_t k_cols, size_t head_dim, size_t q_base,
+                                                 float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TE_HIP_BACKEND_H */

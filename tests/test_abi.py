@@ -1,0 +1,145 @@
+"""CPU checks of the C-ABI boundary: the library loads, exports every symbol the
+headers declare and every symbol the reference ctypes binding binds, and
+honours the reference's status conventions on argument errors (no compute
+calls: these run without a GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+# python/tinyengine/runtime.py:271-378 of the reference binds these 22 symbols.
+REFERENCE_BINDING_SYMBOLS = [
+    "te_strerror", "te_detect_arch", "te_get_capabilities", "te_make_kernel_plan",
+    "te_kernel_plan_supports_quant", "te_kernel_plan_optimizes_quant", "te_kernel_plan_supports_op",
+    "te_model_load_gguf", "te_model_get_info", "te_model_get_tokenizer_info", "te_model_get_tensor_info",
+    "te_format_qwen_chat_prompt", "te_model_tokenize", "te_model_detokenize", "te_model_read_f32_tensor",
+    "te_model_dequantize_row_f32", "te_model_matvec_f32", "te_model_free", "te_context_create",
+    "te_context_free", "te_generate", "te_generate_raw",
+]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from tinymetalagent_amd import runtime
+
+    return runtime.load_library()
+
+
+def declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        for m in re.finditer(r"TE_API\s+[^;(]*?\b(te_\w+)\s*\(", text, re.S):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_every_header_symbol_is_exported(lib):
+    names = declared_symbols()
+    assert len(names) >= 45
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_reference_binding_symbols_resolve(lib):
+    for n in REFERENCE_BINDING_SYMBOLS:
+        assert hasattr(lib, n), n
+
+
+def test_status_strings(lib):
+    want = {0: "ok", 1: "invalid argument", 2: "I/O error", 3: "unsupported", 4: "out of memory",
+            5: "runtime error", 99: "unknown error"}
+    for k, v in want.items():
+        assert lib.te_strerror(k).decode() == v
+
+
+def test_defaults_and_capabilities():
+    from tinymetalagent_amd import runtime
+
+    lib = runtime.load_library()
+    opts = lib.te_default_options()
+    assert (opts.abi_version, opts.context_tokens, opts.batch_tokens) == (3, 512, 128)
+    caps = runtime.capabilities()
+    assert caps.abi_version == 3 and caps.backend_name == "hip-gfx950"
+    for op in (runtime.TE_OP_ROPE, runtime.TE_OP_CAUSAL_ATTENTION, runtime.TE_OP_KV_CACHE):
+        assert caps.vector_op_mask >> op & 1
+    plan = runtime._KernelPlan()
+    o = runtime._RuntimeOptions(abi_version=3, context_tokens=8192)
+    runtime.check(lib.te_make_kernel_plan(ctypes.byref(o), ctypes.byref(plan)))
+    assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), runtime.TE_OP_CAUSAL_ATTENTION) == 1
+    assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), 0) == 0
+    assert plan.max_context_tokens == 8192
+    o.abi_version = 2
+    assert lib.te_make_kernel_plan(ctypes.byref(o), ctypes.byref(plan)) == runtime.TE_STATUS_UNSUPPORTED
+
+
+def test_public_attention_argument_checks(lib):
+    f = np.ones(64, np.float32)
+    p = f.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    # te_rope_f32: reference ops.c:302-304
+    assert lib.te_rope_f32(None, 1, 8, 0, ctypes.c_float(1e6)) == 1
+    assert lib.te_rope_f32(p, 0, 8, 0, ctypes.c_float(1e6)) == 1
+    assert lib.te_rope_f32(p, 1, 7, 0, ctypes.c_float(1e6)) == 1
+    assert lib.te_rope_f32(p, 1, 8, 0, ctypes.c_float(0.0)) == 1
+    # te_attention_decode_f32: reference ops.c:333-339
+    assert lib.te_attention_decode_f32(p, p, p, 0, 3, 2, 4, p) == 1
+    assert lib.te_attention_decode_f32(None, p, p, 0, 2, 1, 4, p) == 1
+    assert lib.te_attention_decode_f32(p, p, p, 2 ** 64 - 1, 2, 1, 4, p) == 3
+
+
+def test_backend_guard_conventions(lib):
+    """NULL first argument -> INVALID_ARGUMENT or UNSUPPORTED; unsupported shape -> UNSUPPORTED
+    (the convention of reference c/tests/generate_metal_guard_tests.py:68-79)."""
+    from tinymetalagent_amd import runtime
+
+    buf = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its checks first
+    ws = ctypes.c_void_p(0x2000)
+    ok = (runtime.TE_STATUS_INVALID_ARGUMENT, runtime.TE_STATUS_UNSUPPORTED)
+    assert lib.te_hip_rope_kv_append_f16(None, buf, buf, None, None, None, buf, buf, buf, buf, None,
+                                         1, 1, 1, None, 0, 8, 2, 1, 4, None) in ok
+    assert lib.te_hip_rope_kv_append_f16(buf, buf, buf, None, None, None, buf, buf, buf, buf, None,
+                                         1, 1, 1, None, 0, 8, 2, 1, 3, None) == 1  # odd head_dim
+    assert lib.te_hip_rope_kv_append_f16(buf, buf, buf, None, None, None, buf, buf, buf, buf, None,
+                                         1, 1, 4, None, 6, 8, 2, 1, 4, None) == 1  # positions past the cache
+    assert lib.te_hip_attention_decode_splitk_f16(None, buf, buf, None, 0, 1, 1, 8, 2, 1, 128, ws, 1 << 20,
+                                                  None) in ok
+    assert lib.te_hip_attention_decode_splitk_f16(buf, buf, buf, None, 0, 1, 1, 8, 2, 1, 96, ws, 1 << 20,
+                                                  None) == 3  # head_dim 96
+    assert lib.te_hip_attention_decode_splitk_f16(buf, buf, buf, None, 0, 1, 1, 8, 34, 2, 128, ws, 1 << 20,
+                                                  None) == 3  # group of 17 heads
+    assert lib.te_hip_attention_decode_splitk_f16(buf, buf, buf, None, 8, 1, 1, 8, 2, 1, 128, ws, 1 << 20,
+                                                  None) == 1  # position >= context
+    assert lib.te_hip_attention_decode_splitk_f16(buf, buf, buf, None, 0, 1, 1, 8, 2, 1, 128, ws, 16,
+                                                  None) == 1  # workspace too small
+    assert lib.te_hip_attention_prefill_f16(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None) in ok
+    assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 6, 8, 2, 1, 128, buf, None) == 1
+    assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None) == 3
+    q = np.ones(8 * 64, np.float32).ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    assert lib.te_hip_attention_qk_mma_f32(None, q, 8, 8, 64, q) in ok
+    assert lib.te_hip_attention_qk_mma_f32(q, q, 4, 8, 64, q) == 3
+    assert lib.te_hip_attention_stream_mma_f32(q, q, q, 8, 12, 64, q) == 3
+    assert lib.te_hip_attention_causal_mma_f32(q, q, q, 8, 24, 64, 25, q) == 3
+
+
+def test_workspace_query(lib):
+    n = lib.te_hip_attention_decode_workspace_bytes(1, 36, 8192, 16, 2, 128)
+    assert n > 0
+    assert lib.te_hip_attention_decode_workspace_bytes(0, 36, 8192, 16, 2, 128) == 0
+
+
+def test_out_of_scope_entry_points_report_unsupported():
+    from tinymetalagent_amd import runtime
+
+    lib = runtime.load_library()
+    model = ctypes.c_void_p()
+    status = lib.te_model_load_gguf(b"/nonexistent.gguf", None, ctypes.byref(model))
+    assert status == runtime.TE_STATUS_UNSUPPORTED and model.value is None
+    with pytest.raises(runtime.TinyEngineError, match="^unsupported$"):
+        runtime.check(status)
+    assert lib.te_context_create(None, None, ctypes.byref(model)) == 1
+    cb = runtime._TOKEN_CALLBACK(lambda *a: None)
+    assert lib.te_generate(None, b"hi", 4, cb, None) == 1

@@ -1,0 +1,394 @@
+"""GPU parity tests: the HIP kernels (through the C-ABI of libtinyengine.so)
+against the CPU oracle, the reference's golden vectors and known-answer tests.
+
+Bars: bit-exact for RoPE'd values, cache slot indexing,
+fp16 cache contents and positions; max-abs error <= 2e-3 for attention outputs
+(fp32 softmax and accumulation).  Shapes: the BASELINE configs, reduced where
+the single-threaded oracle must finish in seconds, plus full-size checks
+through size-independent properties (sampled rows/layers against the oracle,
+constant-V, prefill row t == decode at base+t).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import _synth as S
+import cases as C
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from tinymetalagent_amd import attention as A  # noqa: E402
+from tinymetalagent_amd import runtime as R  # noqa: E402
+
+TOL = 2e-3  # max-abs error bar for attention outputs (north_star)
+DEV = "cuda"
+
+
+def bits32(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def to_dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.to(DEV)
+
+
+def f16_dev(bits_u16):
+    return torch.from_numpy(np.ascontiguousarray(bits_u16).view(np.int16)).to(DEV).view(torch.float16)
+
+
+def f16_host_bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def maxabs(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+# ------------------------------------------------------------------ device ---
+
+def test_hip_path_is_live():
+    assert R.hip_available(), "libtinyengine.so found no gfx950 device"
+    name, cus = R.device_info()
+    assert "gfx950" in name and cus >= 1
+    print(f"device: {name}, {cus} CUs, library {R.library_path()}")
+
+
+# -------------------------------------------------------------- public ABI ---
+
+def test_rope_f32_public_matches_reference_bits(golden):
+    data, meta = golden
+    for name, heads, d, pos, theta in C.ROPE_CASES:
+        x = C.rope_input(name, heads, d)
+        got = R.rope_f32(x, heads, d, pos, theta)
+        assert np.array_equal(bits32(got), bits32(data[f"rope/{name}"])), name
+
+
+def test_rope_table_device_matches_reference_bits(golden):
+    data, meta = golden
+    positions = meta["rope_rows"]["positions"]
+    for d in (64, 128):
+        cos, sin = A.rope_table(max(positions) + 1, d, 1e6)
+        cos, sin = cos.cpu().numpy(), sin.cpu().numpy()
+        rows = data[f"rope_rows/d{d}"]
+        for i, p in enumerate(positions):
+            assert np.array_equal(bits32(cos[p]), bits32(rows[i, : d // 2])), (d, p)
+            assert np.array_equal(bits32(sin[p]), bits32(rows[i, d // 2:])), (d, p)
+
+
+def test_attention_decode_f32_public_kat():
+    # reference c/tests/kernel_ops.c:341-356
+    out = R.attention_decode_f32(np.array([1, 0, 0, 1], np.float32), np.array([1, 0, 0, 1], np.float32),
+                                 np.array([10, 20, 30, 40], np.float32), 1, 2, 1, 2)
+    sc = 1 / math.sqrt(2)
+    hi = math.exp(sc)
+    wh, wl = hi / (hi + 1), 1 / (hi + 1)
+    want = [wh * 10 + wl * 30, wh * 20 + wl * 40, wl * 10 + wh * 30, wl * 20 + wh * 40]
+    np.testing.assert_allclose(out, want, atol=1e-5, rtol=0)
+
+
+def test_attention_decode_f32_public_golden(golden):
+    data, meta = golden
+    for case in C.DECODE_CASES:
+        q, kb, vb = C.decode_inputs(case)
+        assert S.digest(q, kb, vb) == meta["decode"][case["name"]]["input_sha256"]
+        got = R.attention_decode_f32(q, S.f16_bits_to_f32(kb), S.f16_bits_to_f32(vb), case["pos"], case["heads"],
+                                     case["kv"], case["d"])
+        err = maxabs(got, data[f"decode/{case['name']}"])
+        print(f"te_attention_decode_f32 {case['name']}: max abs err {err:.3e}")
+        assert err <= 5e-5, case["name"]
+
+
+def _kat_inputs(k_cols, kscale, vscale):
+    # formulas of reference c/tests/kernel_ops.c:522-741
+    q = np.array([[(q + 1) * ((d % 7) + 1) * 0.0078125 for d in range(64)] for q in range(8)], np.float32)
+    kt = np.array([[((d % 5) + 1) * (k + 2) * kscale for k in range(k_cols)] for d in range(64)], np.float32)
+    v = np.array([[(k + 3) * ((d % 11) + 1) * vscale for d in range(64)] for k in range(k_cols)], np.float32)
+    return q, kt, v
+
+
+def _kat_expected(q, kt, v, q_base=None):
+    s = q.astype(np.float32) @ kt.astype(np.float32) / np.float32(8.0)
+    if q_base is not None:
+        for r in range(8):
+            s[r, q_base + r + 1:] = -np.inf
+    w = np.exp(s - s.max(1, keepdims=True))
+    return (w / w.sum(1, keepdims=True)) @ v
+
+
+def test_mma_twins_reference_kats():
+    q, kt, _ = _kat_inputs(8, 0.015625, 0)
+    got = R.attention_qk_mma_f32(q, kt, 8, 8, 64).reshape(8, 8)
+    np.testing.assert_allclose(got, q @ kt, atol=1e-4, rtol=0)
+    q, kt, v = _kat_inputs(8, 0.015625, 0.00390625)
+    got = R.attention_tile_mma_f32(q, kt, v, 8, 8, 64).reshape(8, 64)
+    np.testing.assert_allclose(got, _kat_expected(q, kt, v), atol=1e-4, rtol=0)
+    q, kt, v = _kat_inputs(24, 0.00390625, 0.001953125)
+    got = R.attention_stream_mma_f32(q, kt, v, 8, 24, 64).reshape(8, 64)
+    np.testing.assert_allclose(got, _kat_expected(q, kt, v), atol=1e-4, rtol=0)
+    got = R.attention_causal_mma_f32(q, kt, v, 8, 24, 64, 8).reshape(8, 64)
+    np.testing.assert_allclose(got, _kat_expected(q, kt, v, q_base=8), atol=1e-4, rtol=0)
+
+
+# ---------------------------------------------------------- RoPE + append ---
+
+def test_rope_kv_append_bit_exact(oracle_mod):
+    seqs, layers, tokens, ctx, h, kv, d = 3, 2, 5, 48, 16, 2, 128
+    bases = [0, 17, 43]
+    q = S.normal(20, "gq", (seqs, layers, tokens, h, d))
+    k = S.normal(20, "gk", (seqs, layers, tokens, kv, d))
+    v = S.normal(20, "gv", (seqs, layers, tokens, kv, d))
+    qb = S.normal(20, "gqb", (layers, h * d), 0.1)
+    kb = S.normal(20, "gkb", (layers, kv * d), 0.1)
+    vb = S.normal(20, "gvb", (layers, kv * d), 0.1)
+    cos, sin = oracle_mod.rope_table(ctx, d, 1e6)
+    sentinel = np.full((seqs, layers, ctx, kv, d), 0x7E01, np.uint16)
+    # oracle
+    q_o, k_o, v_o = q.copy(), k.copy(), v.copy()
+    kc_o, vc_o = sentinel.copy(), sentinel.copy()
+    oracle_mod.rope_kv_append_f16(q_o, k_o, v_o, qb, kb, vb, cos, sin, kc_o, vc_o, seqs, layers, tokens, bases, 0,
+                                  ctx, h, kv, d)
+    # GPU
+    tq, tk, tv = to_dev(q), to_dev(k), to_dev(v)
+    dcos, dsin = A.rope_table(ctx, d, 1e6)
+    kc, vc = f16_dev(sentinel), f16_dev(sentinel)
+    qh = torch.empty(q.shape, dtype=torch.float16, device=DEV)
+    A.rope_kv_append(tq, tk, tv, dcos, dsin, kc, vc, base_positions=bases, q_bias=to_dev(qb), k_bias=to_dev(kb),
+                     v_bias=to_dev(vb), q_half=qh)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits32(tq.cpu().numpy()), bits32(q_o))
+    assert np.array_equal(bits32(tk.cpu().numpy()), bits32(k_o))
+    assert np.array_equal(bits32(tv.cpu().numpy()), bits32(v_o))
+    assert np.array_equal(f16_host_bits(kc), kc_o)
+    assert np.array_equal(f16_host_bits(vc), vc_o)
+    assert np.array_equal(f16_host_bits(qh), S.to_f16_bits(q_o))
+
+
+def test_rope_kv_append_no_bias_decode_all_layers(oracle_mod):
+    seqs, layers, ctx, h, kv, d = 1, 36, 9000, 16, 2, 128
+    pos = 8192
+    q = S.normal(21, "dq", (seqs, layers, 1, h, d), 1 / math.sqrt(d))
+    k = S.normal(21, "dk", (seqs, layers, 1, kv, d))
+    v = S.normal(21, "dv", (seqs, layers, 1, kv, d))
+    cos, sin = oracle_mod.rope_table(ctx, d, 1e6)
+    kc_o = np.zeros((seqs, layers, ctx, kv, d), np.uint16)
+    vc_o = kc_o.copy()
+    q_o, k_o, v_o = q.copy(), k.copy(), v.copy()
+    oracle_mod.rope_kv_append_f16(q_o, k_o, v_o, None, None, None, cos, sin, kc_o, vc_o, seqs, layers, 1, None, pos,
+                                  ctx, h, kv, d)
+    tq, tk, tv = to_dev(q), to_dev(k), to_dev(v)
+    dcos, dsin = A.rope_table(ctx, d, 1e6)
+    kc = torch.zeros((seqs, layers, ctx, kv, d), dtype=torch.float16, device=DEV)
+    vc = torch.zeros_like(kc)
+    A.rope_kv_append(tq, tk, tv, dcos, dsin, kc, vc, base_position=pos)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits32(tq.cpu().numpy()), bits32(q_o))
+    assert np.array_equal(f16_host_bits(kc[:, :, pos]), kc_o[:, :, pos])
+    assert np.array_equal(f16_host_bits(vc[:, :, pos]), vc_o[:, :, pos])
+    assert int(torch.count_nonzero(kc[:, :, :pos])) == 0 and int(torch.count_nonzero(kc[:, :, pos + 1:])) == 0
+
+
+# ------------------------------------------------------------------ decode ---
+
+def _decode_gpu(q, kc_bits, vc_bits, positions, seqs, layers, ctx, h, kv, d):
+    tq = to_dev(q.reshape(seqs, layers, h, d))
+    kc = f16_dev(kc_bits.reshape(seqs, layers, ctx, kv, d))
+    vc = f16_dev(vc_bits.reshape(seqs, layers, ctx, kv, d))
+    out = A.attention_decode(tq, kc, vc, positions=positions)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_decode_f16_golden(golden):
+    data, meta = golden
+    for case in C.DECODE_CASES:
+        q, kb, vb = C.decode_inputs(case)
+        assert S.digest(q, kb, vb) == meta["decode"][case["name"]]["input_sha256"]
+        n = case["pos"] + 1
+        ctx = n + 5  # cache capacity beyond the attended range
+        kc = np.zeros((ctx, case["kv"], case["d"]), np.uint16)
+        vc = np.zeros_like(kc)
+        kc[:n] = kb.reshape(n, case["kv"], case["d"])
+        vc[:n] = vb.reshape(n, case["kv"], case["d"])
+        kc[n:] = 0x7C00  # +inf past the end: must never be read
+        vc[n:] = 0x7E00  # NaN past the end
+        got = _decode_gpu(q, kc, vc, [case["pos"]], 1, 1, ctx, case["heads"], case["kv"], case["d"])
+        err = maxabs(got.reshape(-1), data[f"decode/{case['name']}"])
+        print(f"decode_f16 {case['name']}: max abs err {err:.3e}")
+        assert err <= TOL, case["name"]
+
+
+@pytest.mark.parametrize("shape", [
+    # heads, kv, d, layers, positions (per sequence)
+    (14, 2, 64, 1, [0, 1, 31, 32, 127, 128, 129, 255, 256, 512, 1000]),
+    (16, 2, 128, 3, [2047]),
+    (28, 4, 128, 2, "ragged8"),
+    (12, 2, 128, 1, [4096]),
+    (16, 16, 128, 1, [300]),
+    (8, 1, 64, 2, [5000, 3]),
+])
+def test_decode_f16_vs_oracle(oracle_mod, shape):
+    h, kv, d, layers, positions = shape
+    if positions == "ragged8":
+        positions = [int(x) for x in S.rng(S.SEED, "ragged").integers(1, 3000, size=8)]
+    outliers = h == 12
+    seqs = len(positions)
+    ctx = max(positions) + 3
+    tag = f"dec{h}{kv}{d}{layers}{seqs}"
+    q = S.normal(22, tag + "q", (seqs, layers, h, d), 1 / math.sqrt(d))
+    shape_kv = (seqs, layers, ctx, kv, d)
+    kf = S.outlier_keys(22, tag + "k", shape_kv) if outliers else S.normal(22, tag + "k", shape_kv)
+    kc = S.to_f16_bits(kf)
+    vc = S.to_f16_bits(S.normal(22, tag + "v", shape_kv))
+    want = oracle_mod.attention_decode_f16kv(q, kc, vc, positions, 0, seqs, layers, ctx, h, kv, d)
+    got = _decode_gpu(q, kc, vc, positions, seqs, layers, ctx, h, kv, d)
+    err = maxabs(got, want)
+    print(f"decode_f16 {shape[:4]} positions={positions}: max abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_sharp_softmax(oracle_mod):
+    # large-magnitude queries: near one-hot attention stresses P rounding
+    h, kv, d, ctx = 16, 2, 128, 1500
+    q = S.normal(23, "sq", (1, 1, h, d), 1.5)
+    kc = S.to_f16_bits(S.normal(23, "sk", (1, 1, ctx, kv, d)))
+    vc = S.to_f16_bits(S.normal(23, "sv", (1, 1, ctx, kv, d)))
+    want = oracle_mod.attention_decode_f16kv(q, kc, vc, [ctx - 1], 0, 1, 1, ctx, h, kv, d)
+    got = _decode_gpu(q, kc, vc, [ctx - 1], 1, 1, ctx, h, kv, d)
+    err = maxabs(got, want)
+    print(f"decode_f16 sharp softmax: max abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_config1_step(oracle_mod):
+    """BASELINE config 1 end to end: RoPE + fp16 append of 512 cached tokens,
+    then one decode step at position 512 (append + attention)."""
+    h, kv, d, theta, pos = 14, 2, 64, 1e6, 512
+    ctx = pos + 1
+    scale = 1 / math.sqrt(d)
+    qs = S.normal(24, "c1q", (1, 1, pos + 1, h, d), scale)
+    ks = S.normal(24, "c1k", (1, 1, pos + 1, kv, d), scale)
+    vs = S.normal(24, "c1v", (1, 1, pos + 1, kv, d), scale)
+    cos, sin = oracle_mod.rope_table(ctx, d, theta)
+    kc_o = np.zeros((1, 1, ctx, kv, d), np.uint16)
+    vc_o = kc_o.copy()
+    q_o, k_o, v_o = qs.copy(), ks.copy(), vs.copy()
+    oracle_mod.rope_kv_append_f16(q_o, k_o, v_o, None, None, None, cos, sin, kc_o, vc_o, 1, 1, pos + 1, None, 0, ctx,
+                                  h, kv, d)
+    want = oracle_mod.attention_decode_f16kv(q_o[:, :, pos].copy(), kc_o, vc_o, None, pos, 1, 1, ctx, h, kv, d)
+
+    dcos, dsin = A.rope_table(ctx, d, theta)
+    kc = torch.zeros((1, 1, ctx, kv, d), dtype=torch.float16, device=DEV)
+    vc = torch.zeros_like(kc)
+    tq, tk, tv = to_dev(qs[:, :, :pos].copy()), to_dev(ks[:, :, :pos].copy()), to_dev(vs[:, :, :pos].copy())
+    A.rope_kv_append(tq, tk, tv, dcos, dsin, kc, vc, base_position=0)          # cached prefix 0..511
+    sq, sk, sv = to_dev(qs[:, :, pos:].copy()), to_dev(ks[:, :, pos:].copy()), to_dev(vs[:, :, pos:].copy())
+    A.rope_kv_append(sq, sk, sv, dcos, dsin, kc, vc, base_position=pos)        # the decode token
+    out = A.attention_decode(sq, kc, vc, position=pos)
+    torch.cuda.synchronize()
+    assert np.array_equal(f16_host_bits(kc), kc_o) and np.array_equal(f16_host_bits(vc), vc_o)
+    err = maxabs(out.cpu().numpy().reshape(-1), want.reshape(-1))
+    print(f"config-1 decode step: max abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_full_size_3b_8k_sampled_layers(oracle_mod):
+    """BASELINE config 2 at 8K, all 36 layers on the GPU; layers 0, 17, 35 against the oracle."""
+    h, kv, d, layers, pos = 16, 2, 128, 36, 8192
+    ctx = pos + 1
+    g = torch.Generator(device=DEV).manual_seed(S.SEED)
+    kc = torch.randn((1, layers, ctx, kv, d), generator=g, device=DEV).half()
+    vc = torch.randn((1, layers, ctx, kv, d), generator=g, device=DEV).half()
+    q = torch.randn((1, layers, h, d), generator=g, device=DEV) / math.sqrt(d)
+    out = A.attention_decode(q, kc, vc, position=pos).cpu().numpy()
+    for layer in (0, 17, 35):
+        want = oracle_mod.attention_decode_f16kv(q[:, layer].cpu().numpy().copy(), f16_host_bits(kc[:, layer]),
+                                                 f16_host_bits(vc[:, layer]), None, pos, 1, 1, ctx, h, kv, d)
+        err = maxabs(out[:, layer], want)
+        print(f"3B 8K layer {layer}: max abs err {err:.3e}")
+        assert err <= TOL
+
+
+def test_decode_constant_values_32k():
+    """Size-independent property at 32K: V constant over positions -> output == that constant."""
+    h, kv, d, layers, pos = 16, 2, 128, 2, 32767
+    ctx = pos + 1
+    g = torch.Generator(device=DEV).manual_seed(7)
+    kc = torch.randn((1, layers, ctx, kv, d), generator=g, device=DEV).half()
+    row = torch.randn((1, layers, 1, kv, d), generator=g, device=DEV).half()
+    vc = row.expand(1, layers, ctx, kv, d).contiguous()
+    q = torch.randn((1, layers, h, d), generator=g, device=DEV)
+    out = A.attention_decode(q, kc, vc, position=pos)
+    want = row[:, :, 0].float().repeat_interleave(h // kv, dim=2)
+    err = float((out - want).abs().max())
+    print(f"constant-V 32K: max abs err {err:.3e}")
+    assert err <= 1e-4
+
+
+# ----------------------------------------------------------------- prefill ---
+
+def _prefill_case(oracle_mod, h, kv, d, tokens, base, seed):
+    ctx = base + tokens
+    tag = f"pf{h}{kv}{d}{tokens}{base}"
+    # cached prefix (base positions) + the chunk's own K/V, all fp16 in the cache
+    kc = S.to_f16_bits(S.normal(seed, tag + "k", (1, 1, ctx, kv, d)))
+    vc = S.to_f16_bits(S.normal(seed, tag + "v", (1, 1, ctx, kv, d)))
+    q32 = S.normal(seed, tag + "q", (1, 1, tokens, h, d))
+    q16 = S.to_f16_bits(q32)
+    want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q16).reshape(tokens, h, d), kc[0, 0], vc[0, 0], tokens,
+                                        base, ctx, h, kv, d)
+    out = A.attention_prefill(f16_dev(q16), f16_dev(kc), f16_dev(vc), base_position=base)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().reshape(tokens, h, d), want
+
+
+@pytest.mark.parametrize("h,kv,d,tokens,base", [
+    (16, 2, 128, 300, 0),
+    (16, 2, 128, 130, 200),
+    (16, 2, 128, 1, 0),
+    (16, 2, 128, 64, 0),
+    (14, 2, 64, 200, 37),
+    (28, 4, 128, 257, 0),
+    (12, 2, 128, 129, 1000),
+])
+def test_prefill_vs_oracle(oracle_mod, h, kv, d, tokens, base):
+    got, want = _prefill_case(oracle_mod, h, kv, d, tokens, base, 25)
+    err = maxabs(got, want)
+    print(f"prefill H{h} KV{kv} d{d} L{tokens} base{base}: max abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_full_size_4k_rows(oracle_mod):
+    """BASELINE config 3 at L=4096 (fp16 Q/K/V ~ N(0,1), RoPE at 0..L-1, causal):
+    strided rows against the oracle, plus row t == the decode kernel at position t."""
+    h, kv, d, L, theta = 16, 2, 128, 4096, 1e6
+    g = torch.Generator(device=DEV).manual_seed(S.SEED)
+    q = torch.randn((1, 1, L, h, d), generator=g, device=DEV).half().float()
+    k = torch.randn((1, 1, L, kv, d), generator=g, device=DEV).half().float()
+    v = torch.randn((1, 1, L, kv, d), generator=g, device=DEV).half().float()
+    dcos, dsin = A.rope_table(L, d, theta)
+    kc = torch.zeros((1, 1, L, kv, d), dtype=torch.float16, device=DEV)
+    vc = torch.zeros_like(kc)
+    qh = torch.empty((1, 1, L, h, d), dtype=torch.float16, device=DEV)
+    A.rope_kv_append(q, k, v, dcos, dsin, kc, vc, base_position=0, q_half=qh)
+    out = A.attention_prefill(qh, kc, vc, base_position=0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(L, h, d)
+    rows = list(range(0, L, 257)) + [L - 1]
+    want = oracle_mod.attention_prefill(q.cpu().numpy().reshape(L, h, d), f16_host_bits(kc[0, 0]),
+                                        f16_host_bits(vc[0, 0]), L, 0, L, h, kv, d, 0, L, 257)
+    want[L - 1] = oracle_mod.attention_prefill(q.cpu().numpy().reshape(L, h, d), f16_host_bits(kc[0, 0]),
+                                               f16_host_bits(vc[0, 0]), L, 0, L, h, kv, d, L - 1, L, 1)[L - 1]
+    err = max(maxabs(got[r], want[r]) for r in rows)
+    print(f"prefill 3B L=4096 sampled rows: max abs err vs oracle (fp32 q) {err:.3e}")
+    assert err <= TOL
+    # row t of prefill == decode at position t (same fp16 cache; decode takes the fp32 q)
+    for t in (0, 1, 100, 2048, 4095):
+        dec = A.attention_decode(q[:, :, t].contiguous(), kc, vc, position=t)
+        e = float((dec[0, 0] - out[0, 0, t]).abs().max())
+        assert e <= TOL, (t, e)

@@ -1,0 +1,142 @@
+"""Device-level attention step on torch tensors (HBM-resident inputs).
+
+Thin wrappers over the te_hip_* C-ABI entry points of libtinyengine.so.  torch
+only provides device memory and the current HIP stream; every arithmetic step
+runs in the library's hand-written gfx950 kernels.  Tensors must be contiguous,
+on the GPU, with the dtypes and layouts of include/te_hip_backend.h:
+
+    q, out        float32  [seqs, layers, tokens, heads, head_dim]
+    k, v          float32  [seqs, layers, tokens, kv_heads, head_dim]
+    key/value     float16  [seqs, layers, context_tokens, kv_heads, head_dim]
+    rope cos/sin  float32  [context_tokens, head_dim // 2]
+
+A missing library or GPU raises TinyEngineError; nothing falls back to the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import torch
+
+from .runtime import TE_HIP_MAX_SEQS, TinyEngineError, check, load_library
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise TinyEngineError("invalid argument: tensor is not on the GPU")
+    if not t.is_contiguous():
+        raise TinyEngineError("invalid argument: tensor is not contiguous")
+    return t.data_ptr()
+
+
+def _dtype(t: torch.Tensor | None, dtype: torch.dtype, name: str) -> None:
+    if t is not None and t.dtype != dtype:
+        raise TinyEngineError(f"invalid argument: {name} must be {dtype}, got {t.dtype}")
+
+
+def _stream(stream: torch.cuda.Stream | None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _positions(positions: Sequence[int] | None):
+    if positions is None:
+        return None
+    if len(positions) > TE_HIP_MAX_SEQS:
+        raise TinyEngineError("unsupported")
+    arr = (ctypes.c_size_t * len(positions))(*[int(p) for p in positions])
+    return arr
+
+
+def rope_table(context_tokens: int, head_dim: int, theta: float, device="cuda"):
+    """Device cos/sin tables built with the reference formula (host libm)."""
+    cos = torch.empty((context_tokens, head_dim // 2), dtype=torch.float32, device=device)
+    sin = torch.empty_like(cos)
+    check(load_library().te_hip_rope_table_f32(_ptr(cos), _ptr(sin), context_tokens, head_dim,
+                                               ctypes.c_float(theta)))
+    return cos, sin
+
+
+def rope_kv_append(q, k, v, rope_cos, rope_sin, key_cache, value_cache, *, base_position: int = 0,
+                   base_positions: Sequence[int] | None = None, q_bias=None, k_bias=None, v_bias=None,
+                   q_half: torch.Tensor | None = None, stream=None) -> None:
+    """In place: bias + RoPE on q/k (and bias on v), fp16 append of k/v to the cache."""
+    seqs, layers, tokens, heads, head_dim = q.shape
+    kv_heads = k.shape[3]
+    ctx = key_cache.shape[2]
+    for t, dt, n in ((q, torch.float32, "q"), (k, torch.float32, "k"), (v, torch.float32, "v"),
+                     (key_cache, torch.float16, "key_cache"), (value_cache, torch.float16, "value_cache"),
+                     (q_half, torch.float16, "q_half"), (rope_cos, torch.float32, "rope_cos"),
+                     (rope_sin, torch.float32, "rope_sin")):
+        _dtype(t, dt, n)
+    bp = _positions(base_positions)
+    check(load_library().te_hip_rope_kv_append_f16(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(rope_cos), _ptr(rope_sin),
+        _ptr(key_cache), _ptr(value_cache), _ptr(q_half), seqs, layers, tokens, bp, base_position, ctx, heads,
+        kv_heads, head_dim, _stream(stream)))
+
+
+def decode_workspace(seqs: int, layers: int, max_position: int, heads: int, kv_heads: int, head_dim: int,
+                     device="cuda") -> torch.Tensor:
+    n = load_library().te_hip_attention_decode_workspace_bytes(seqs, layers, max_position, heads, kv_heads,
+                                                                head_dim)
+    if n == 0:
+        raise TinyEngineError("invalid argument")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def attention_decode(query, key_cache, value_cache, *, position: int = 0, positions: Sequence[int] | None = None,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, stream=None,
+                     stage: str = "both") -> torch.Tensor:
+    """Split-K GQA decode: query [seqs, layers, heads, d] (or with a tokens=1 axis).
+
+    stage: "both" (split-K + combine), "splitk" or "combine" -- the last two let
+    a caller time the split-K kernel alone (the workspace must be given).
+    """
+    q = query if query.dim() == 4 else query.reshape(query.shape[0], query.shape[1], query.shape[-2],
+                                                     query.shape[-1])
+    seqs, layers, heads, head_dim = q.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    _dtype(q, torch.float32, "query")
+    _dtype(key_cache, torch.float16, "key_cache")
+    _dtype(value_cache, torch.float16, "value_cache")
+    if out is None:
+        out = torch.empty_like(q)
+    pp = _positions(positions)
+    lib = load_library()
+    ws_ptr = _ptr(workspace)
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    s = _stream(stream)
+    if stage == "both":
+        check(lib.te_hip_attention_decode_f16(_ptr(q), _ptr(key_cache), _ptr(value_cache), pp, position, seqs,
+                                              layers, ctx, heads, kv_heads, head_dim, _ptr(out), ws_ptr, ws_bytes,
+                                              s))
+    elif stage == "splitk":
+        check(lib.te_hip_attention_decode_splitk_f16(_ptr(q), _ptr(key_cache), _ptr(value_cache), pp, position,
+                                                     seqs, layers, ctx, heads, kv_heads, head_dim, ws_ptr,
+                                                     ws_bytes, s))
+    elif stage == "combine":
+        check(lib.te_hip_attention_decode_combine(pp, position, seqs, layers, heads, kv_heads, head_dim, _ptr(out),
+                                                  ws_ptr, ws_bytes, s))
+    else:
+        raise ValueError(stage)
+    return out
+
+
+def attention_prefill(q_half, key_cache, value_cache, *, base_position: int = 0, out: torch.Tensor | None = None,
+                      stream=None) -> torch.Tensor:
+    """Causal prefill: q_half fp16 [seqs, layers, tokens, heads, d] -> out fp32, same shape."""
+    seqs, layers, tokens, heads, head_dim = q_half.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    _dtype(q_half, torch.float16, "q_half")
+    _dtype(key_cache, torch.float16, "key_cache")
+    _dtype(value_cache, torch.float16, "value_cache")
+    if out is None:
+        out = torch.empty(q_half.shape, dtype=torch.float32, device=q_half.device)
+    check(load_library().te_hip_attention_prefill_f16(_ptr(q_half), _ptr(key_cache), _ptr(value_cache), seqs,
+                                                      layers, tokens, base_position, ctx, heads, kv_heads, head_dim,
+                                                      _ptr(out), _stream(stream)))
+    return out

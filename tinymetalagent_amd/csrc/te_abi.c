@@ -1,0 +1,357 @@
+/*
+ * ABI plumbing of libtinyengine.so (reference c/src/tinyengine.c:13-440):
+ * version and status strings, option defaults, capability and kernel-plan
+ * reports, context handling and the generate entry points.
+ *
+ * The status strings are part of the contract (reference tinyengine.c:17-34):
+ * the agent layer matches the exact text "unsupported"
+ * (python/tinyagent/engine.py:46, :62).
+ *
+ * Entry points outside the attention step (GGUF model loading, tokenizer,
+ * quantized matvec, element-wise ops, full generation) keep the reference's
+ * argument checks and then return TE_STATUS_UNSUPPORTED, the reference's
+ * "path not available here" status (qwen.c:1162-1165).  They exist so that an
+ * unchanged ctypes binding resolves all of its symbols
+ * (python/tinyengine/runtime.py:271-378).
+ */
+#include "tinyengine.h"
+#include "te_hip_backend.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+static const char *const TE_VERSION_STRING = "0.1.0-c-abi-hip-gfx950";
+
+struct te_context {
+    te_model *model;
+    te_runtime_options options;
+};
+
+const char *te_version(void) {
+    return TE_VERSION_STRING;
+}
+
+const char *te_strerror(te_status status) {
+    switch (status) {
+        case TE_STATUS_OK:
+            return "ok";
+        case TE_STATUS_INVALID_ARGUMENT:
+            return "invalid argument";
+        case TE_STATUS_IO_ERROR:
+            return "I/O error";
+        case TE_STATUS_UNSUPPORTED:
+            return "unsupported";
+        case TE_STATUS_OUT_OF_MEMORY:
+            return "out of memory";
+        case TE_STATUS_RUNTIME_ERROR:
+            return "runtime error";
+        default:
+            return "unknown error";
+    }
+}
+
+const char *te_quant_name(te_quant_kind quant) {
+    static const char *const names[TE_QUANT_COUNT] = {
+        "unknown", "F32", "F16", "BF16", "Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q2_K", "Q3_K",
+        "Q4_K", "Q5_K", "Q6_K", "Q8_K", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS", "MXFP4"};
+    if ((int)quant < 0 || quant >= TE_QUANT_COUNT) {
+        return "unknown";
+    }
+    return names[quant];
+}
+
+const char *te_vector_op_name(te_vector_op op) {
+    static const char *const names[TE_OP_COUNT] = {
+        "matvec", "matmul", "batched-prefill", "decode-token", "rmsnorm", "rope", "causal-attention",
+        "swiglu", "residual-add", "argmax", "sampling", "kv-cache", "tokenize"};
+    if ((int)op < 0 || op >= TE_OP_COUNT) {
+        return "unknown";
+    }
+    return names[op];
+}
+
+/* Defaults: reference tinyengine.c:121-132 (context 512, batch 128). */
+te_runtime_options te_default_options(void) {
+    te_runtime_options options;
+    memset(&options, 0, sizeof(options));
+    options.abi_version = TE_ABI_VERSION;
+    options.target_arch = TE_ARCH_AUTO;
+    options.context_tokens = 512u;
+    options.batch_tokens = 128u;
+    return options;
+}
+
+/* The attention-step operations this build implements on the GPU. */
+static uint64_t te_hip_op_mask(void) {
+    return (1ull << TE_OP_ROPE) | (1ull << TE_OP_CAUSAL_ATTENTION) | (1ull << TE_OP_KV_CACHE) |
+           (1ull << TE_OP_BATCHED_PREFILL);
+}
+
+te_status te_detect_arch(te_arch_info *out_info) {
+    if (out_info == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    memset(out_info, 0, sizeof(*out_info));
+    long cores = sysconf(_SC_NPROCESSORS_ONLN);
+    out_info->cpu_cores = cores > 0 ? (uint32_t)cores : 0u;
+    uint32_t cus = 0;
+    if (te_hip_device_info(out_info->name, sizeof(out_info->name), &cus) == TE_STATUS_OK) {
+        out_info->kind = TE_ARCH_AMD_GFX950;
+        out_info->gpu_cores = cus;
+        out_info->recommended_max_context = 131072u;
+    } else {
+        out_info->kind = TE_ARCH_AUTO;
+        snprintf(out_info->name, sizeof(out_info->name), "%s", "no gfx950 device");
+    }
+    return TE_STATUS_OK;
+}
+
+te_status te_get_capabilities(te_capabilities *out_capabilities) {
+    if (out_capabilities == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    memset(out_capabilities, 0, sizeof(*out_capabilities));
+    out_capabilities->abi_version = TE_ABI_VERSION;
+    out_capabilities->known_quant_mask[0] = (1ull << TE_QUANT_F32) | (1ull << TE_QUANT_F16);
+    out_capabilities->optimized_quant_mask[0] = 1ull << TE_QUANT_F16;
+    out_capabilities->vector_op_mask = te_hip_op_mask();
+    out_capabilities->optimization_flags = TE_OPT_ARCH_SPECIALIZED | TE_OPT_GPU_RESIDENT_KV | TE_OPT_BATCHED_PREFILL;
+    out_capabilities->preferred_alignment_bytes = 256u;
+    snprintf(out_capabilities->backend_name, sizeof(out_capabilities->backend_name), "%s", "hip-gfx950");
+    snprintf(out_capabilities->notes, sizeof(out_capabilities->notes), "%s",
+             "attention step on MI355X: RoPE, fp16 KV append, split-K GQA decode, MFMA causal prefill");
+    return TE_STATUS_OK;
+}
+
+te_status te_make_kernel_plan(const te_runtime_options *options, te_kernel_plan *out_plan) {
+    if (options == NULL || out_plan == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (options->abi_version != TE_ABI_VERSION) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    memset(out_plan, 0, sizeof(*out_plan));
+    out_plan->abi_version = TE_ABI_VERSION;
+    out_plan->target_arch = TE_ARCH_AMD_GFX950;
+    out_plan->quant_mask[0] = (1ull << TE_QUANT_F32) | (1ull << TE_QUANT_F16);
+    out_plan->optimized_quant_mask[0] = 1ull << TE_QUANT_F16;
+    out_plan->vector_op_mask = te_hip_op_mask();
+    out_plan->optimization_flags = TE_OPT_ARCH_SPECIALIZED | TE_OPT_GPU_RESIDENT_KV | TE_OPT_BATCHED_PREFILL;
+    out_plan->dot_threads = 64u; /* wavefront width */
+    out_plan->preferred_alignment_bytes = 256u;
+    out_plan->max_context_tokens = options->context_tokens != 0u ? options->context_tokens : 512u;
+    out_plan->memory_budget_bytes = options->memory_limit_bytes;
+    snprintf(out_plan->metal_function_suffix, sizeof(out_plan->metal_function_suffix), "%s", "_gfx950");
+    return TE_STATUS_OK;
+}
+
+te_status te_compile_kernels(const te_runtime_options *options, const te_kernel_plan *plan) {
+    if (options == NULL || plan == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    /* Kernels are compiled ahead of time for gfx950. */
+    return te_hip_available() ? TE_STATUS_OK : TE_STATUS_UNSUPPORTED;
+}
+
+static int te_mask_has(const uint64_t *mask, unsigned bit) {
+    return (mask[bit / 64u] >> (bit % 64u)) & 1u;
+}
+
+int te_kernel_plan_supports_quant(const te_kernel_plan *plan, te_quant_kind quant) {
+    if (plan == NULL || (int)quant < 0 || quant >= TE_QUANT_COUNT) {
+        return 0;
+    }
+    return te_mask_has(plan->quant_mask, (unsigned)quant);
+}
+
+int te_kernel_plan_optimizes_quant(const te_kernel_plan *plan, te_quant_kind quant) {
+    if (plan == NULL || (int)quant < 0 || quant >= TE_QUANT_COUNT) {
+        return 0;
+    }
+    return te_mask_has(plan->optimized_quant_mask, (unsigned)quant);
+}
+
+int te_kernel_plan_supports_op(const te_kernel_plan *plan, te_vector_op op) {
+    if (plan == NULL || (int)op < 0 || op >= TE_OP_COUNT) {
+        return 0;
+    }
+    return (int)((plan->vector_op_mask >> (unsigned)op) & 1u);
+}
+
+/* ---- outside the attention step: argument checks, then UNSUPPORTED ---- */
+
+te_status te_model_load_gguf(const char *path, const te_runtime_options *options, te_model **out_model) {
+    (void)options;
+    if (path == NULL || out_model == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_model = NULL;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_get_info(const te_model *model, te_model_info *out_info) {
+    return (model == NULL || out_info == NULL) ? TE_STATUS_INVALID_ARGUMENT : TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_get_tokenizer_info(const te_model *model, te_tokenizer_info *out_info) {
+    return (model == NULL || out_info == NULL) ? TE_STATUS_INVALID_ARGUMENT : TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_get_tensor_info(const te_model *model, const char *name, te_tensor_info *out_info) {
+    return (model == NULL || name == NULL || out_info == NULL) ? TE_STATUS_INVALID_ARGUMENT
+                                                                : TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_format_qwen_chat_prompt(const char *prompt, char *out, size_t out_capacity, size_t *out_written) {
+    (void)out;
+    (void)out_capacity;
+    if (prompt == NULL || out_written == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_written = 0;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_tokenize(const te_model *model, const char *text, int parse_special, uint32_t *out_tokens,
+                            size_t out_capacity, size_t *out_written) {
+    (void)parse_special;
+    (void)out_tokens;
+    (void)out_capacity;
+    if (model == NULL || text == NULL || out_written == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_written = 0;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_detokenize(const te_model *model, const uint32_t *tokens, size_t token_count,
+                              int skip_special, char *out, size_t out_capacity, size_t *out_written) {
+    (void)skip_special;
+    (void)out;
+    (void)out_capacity;
+    if (model == NULL || (tokens == NULL && token_count != 0u) || out_written == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_written = 0;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_read_f32_tensor(const te_model *model, const char *name, float *out, size_t out_capacity,
+                                   size_t *out_written) {
+    (void)out;
+    (void)out_capacity;
+    if (model == NULL || name == NULL || out_written == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_written = 0;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_dequantize_row_f32(const te_model *model, const char *name, uint64_t row_index, float *out,
+                                      size_t out_capacity, size_t *out_written) {
+    (void)row_index;
+    (void)out;
+    (void)out_capacity;
+    if (model == NULL || name == NULL || out_written == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_written = 0;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_model_matvec_f32(const te_model *model, const char *name, const float *input, size_t input_len,
+                              float *out, size_t out_capacity, size_t *out_written) {
+    (void)input_len;
+    (void)out;
+    (void)out_capacity;
+    if (model == NULL || name == NULL || input == NULL || out_written == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    *out_written = 0;
+    return TE_STATUS_UNSUPPORTED;
+}
+
+void te_model_free(te_model *model) {
+    (void)model; /* no model can be created by this build */
+}
+
+te_status te_rmsnorm_f32(const float *input, const float *weight, size_t len, float epsilon, float *out) {
+    (void)epsilon;
+    return (input == NULL || weight == NULL || out == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
+                                                                         : TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_swiglu_f32(const float *gate, const float *up, size_t len, float *out) {
+    return (gate == NULL || up == NULL || out == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
+                                                                    : TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_add_f32(const float *lhs, const float *rhs, size_t len, float *out) {
+    return (lhs == NULL || rhs == NULL || out == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
+                                                                    : TE_STATUS_UNSUPPORTED;
+}
+
+te_status te_argmax_f32(const float *values, size_t len, uint32_t *out_index) {
+    return (values == NULL || out_index == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
+                                                              : TE_STATUS_UNSUPPORTED;
+}
+
+/* ---- context and generation: reference tinyengine.c:374-440 ---- */
+
+te_status te_context_create(te_model *model, const te_runtime_options *options, te_context **out_context) {
+    if (model == NULL || out_context == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_context *context = (te_context *)calloc(1, sizeof(*context));
+    if (context == NULL) {
+        return TE_STATUS_OUT_OF_MEMORY;
+    }
+    context->model = model;
+    context->options = options != NULL ? *options : te_default_options();
+    *out_context = context;
+    return TE_STATUS_OK;
+}
+
+void te_context_free(te_context *context) {
+    free(context);
+}
+
+/* Stub generation mode kept from the reference (tinyengine.c:410-423): with
+ * TINYENGINE_GENERATION=stub the fixed four-piece reply is streamed. */
+te_status te_generate(te_context *context, const char *prompt, uint32_t max_tokens, te_token_callback callback,
+                      void *userdata) {
+    if (context == NULL || prompt == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (max_tokens == 0u) {
+        return TE_STATUS_OK;
+    }
+    const char *mode = getenv("TINYENGINE_GENERATION");
+    if (mode == NULL || strcmp(mode, "stub") != 0) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    static const char *const pieces[] = {"Mi", " ch", "iamo", " Alex"};
+    static const uint32_t ids[] = {41887u, 521u, 34214u, 8515u};
+    const uint32_t count = max_tokens < 4u ? max_tokens : 4u;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (callback != NULL) {
+            callback(pieces[i], ids[i], userdata);
+        }
+    }
+    return TE_STATUS_OK;
+}
+
+te_status te_generate_raw(te_context *context, const char *prompt, uint32_t max_tokens, te_token_callback callback,
+                          void *userdata) {
+    (void)callback;
+    (void)userdata;
+    if (context == NULL || prompt == NULL) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (max_tokens == 0u) {
+        return TE_STATUS_OK;
+    }
+    return TE_STATUS_UNSUPPORTED;
+}

@@ -1,0 +1,557 @@
+// GQA decode attention over the fp16 KV cache: split-K ("flash-decoding")
+// kernel + combine kernel, and the fp32-cache variant behind te_attention_decode_f32.
+//
+// Numerical contract: the reference te_attention_decode_f32 (ops.c:323-395)
+// -- scores q.k/sqrt(d) over positions 0..pos, softmax, PV -- in fp32.  Here
+// the softmax is online (base-2, exp2 of log2e-prescaled scores) per chunk and
+// merged exactly by the combine kernel; every accumulation is fp32.
+//
+// Split-K kernel, one workgroup (4 waves) per (chunk of positions, kv_head,
+// seq*layer).  Each wave streams its share of the chunk 32 positions at a time
+// for all `group` (= heads/kv_heads <= 16) query heads of its KV head at once,
+// so every K/V element is read from HBM exactly once per query token (the GQA
+// sharing of te_attention_flash_gqa_f32_kernel, metal_kernels.metal.inc:3209-3372):
+//
+//   S^T[32 pos x 16 heads] = K[32 x D] . Q^T[D x 16]          (fp16 MFMA 16x16x32)
+//   O^T[D x 16 heads]     += V^T[D x 32 pos] . P^T[32 x 16]    (fp16 MFMA 16x16x32)
+//
+// q and P are fp32 values split into hi+lo fp16 pairs (two MFMAs each), so the
+// only rounding relative to an fp32 computation is the fp16 cache itself.
+// Lane mapping (l = lane, g = l/16, c = l%16):
+//   K operand : lane reads K[p0 + 16h + c][8g + 32kk .. +7]          (16 B loads)
+//   V operand : lane reads V[p0 + kmap(g,j)][NT*c .. NT*c+NT-1]       (16 B loads,
+//               a 256-byte cache row per 16 lanes), kmap(g,j) = 16(j/4)+4g+(j%4),
+//               then an in-register 8 x NT transpose gives the A operand of
+//               output tile t = dims {NT*m + t}.
+//   S^T result: lane holds head c at positions 4g+r (+16h) -- exactly the
+//               P^T B-operand layout of the PV MFMA for kmap, so P never moves.
+//   O^T result: lane holds head c, dims 4NT*g .. 4NT*g + 4NT - 1.
+// K and V go from HBM straight into MFMA operand registers; no LDS staging
+// is needed on this path (LDS is used only for the in-workgroup merge).
+//
+// HBM bytes per (seq, layer), the roofline unit: 2*(pos+1)*kv_heads*D*2 B of
+// K/V + heads*D*4 B of q; partials add (chunks*heads*(D+2)*4 B) x2.
+#include "te_hip_common.h"
+
+#include <math.h>
+#include <stdlib.h>
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kTile = 32;                   // positions per MFMA step
+constexpr int kMinChunk = kWaves * kTile;   // 128
+constexpr int kMaxCombineChunks = 4096;
+
+struct DecodeArgs {
+    const float *query;
+    const f16 *key_cache;
+    const f16 *value_cache;
+    float *part_o;   // [SL][heads][max_chunks][D]
+    float *part_ml;  // [SL][heads][max_chunks][2]  (m in log2 units, l)
+    int layers;
+    int ctx;
+    int heads;
+    int kv_heads;
+    int group;
+    int chunk;
+    int max_chunks;
+    float qscale;    // log2(e)/sqrt(D)
+    int positions[TE_HIP_MAX_SEQS];
+};
+
+template <int D>
+struct VRow;
+template <>
+struct VRow<128> {
+    typedef f16x8 type;
+};
+template <>
+struct VRow<64> {
+    typedef f16x4 type;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_splitk_f16_kernel(DecodeArgs a) {
+    constexpr int NT = D / 16;  // output tiles over head_dim; also dims per lane in V loads
+    constexpr int KK = D / 32;  // MFMA K-steps over head_dim for QK^T
+    typedef typename VRow<D>::type vrow_t;
+
+    const int chunk_id = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int sl = blockIdx.z;
+    const int s = sl / a.layers;
+    const int pos = a.positions[s];
+    const int c0 = chunk_id * a.chunk;
+    if (c0 > pos) {
+        return;  // uniform for the whole workgroup: this sequence has fewer chunks
+    }
+    const int c1 = min(c0 + a.chunk, pos + 1);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int span = a.chunk / kWaves;
+    const int w0 = c0 + wave * span;
+    const int w1 = min(w0 + span, c1);
+
+    const size_t row_stride = (size_t)a.kv_heads * D;
+    const size_t sl_base = (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
+    const f16 *kbase = a.key_cache + sl_base;
+    const f16 *vbase = a.value_cache + sl_base;
+
+    // Q^T operand, hi/lo split, pre-scaled into the log2 domain.
+    f16x8 qh[KK], ql[KK];
+    {
+        const bool head_ok = c < a.group;
+        const float *qrow = a.query + ((size_t)sl * a.heads + (size_t)kvh * a.group + (head_ok ? c : 0)) * D;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk + 4);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = head_ok ? xs[j] * a.qscale : 0.0f;
+                f16 hi, lo;
+                split_f16(x, hi, lo);
+                qh[kk][j] = hi;
+                ql[kk][j] = lo;
+            }
+        }
+    }
+
+    float m = -INFINITY;
+    float l = 0.0f;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    for (int p0 = w0; p0 < w1; p0 += kTile) {
+        // ---- loads (positions past `pos` are clamped to `pos`, then masked) ----
+        f16x8 kf[2][KK];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pr = min(p0 + 16 * h + c, pos);
+            const f16 *kr = kbase + (size_t)pr * row_stride;
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                kf[h][kk] = *reinterpret_cast<const f16x8 *>(kr + 8 * g + 32 * kk);
+            }
+        }
+        vrow_t vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int pr = min(p0 + 16 * (j >> 2) + 4 * g + (j & 3), pos);
+            vr[j] = *reinterpret_cast<const vrow_t *>(vbase + (size_t)pr * row_stride + NT * c);
+        }
+
+        // ---- S^T = K Q^T ----
+        f32x4 sacc[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            sacc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                sacc[h] = mfma16x16x32(kf[h][kk], qh[kk], sacc[h]);
+                sacc[h] = mfma16x16x32(kf[h][kk], ql[kk], sacc[h]);
+            }
+        }
+
+        // ---- online softmax (per head = per lane column c) ----
+        float sv[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int p = p0 + 16 * (j >> 2) + 4 * g + (j & 3);
+            const float x = sacc[j >> 2][j & 3];
+            sv[j] = p <= pos ? x : -INFINITY;
+            mx = fmaxf(mx, sv[j]);
+        }
+        mx = wave_xor_max16_32(mx);
+        const float m_new = fmaxf(m, mx);
+        const float alpha = fast_exp2(m - m_new);
+        m = m_new;
+        f16x8 ph, pl;
+        float psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = fast_exp2(sv[j] - m_new);
+            psum += p;
+            f16 hi, lo;
+            split_f16(p, hi, lo);
+            ph[j] = hi;
+            pl[j] = lo;
+        }
+        l = l * alpha + psum;
+
+        // ---- O^T = alpha*O^T + V^T P^T ----
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            f16x8 va;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                va[j] = vr[j][t];
+            }
+            acc[t] = acc[t] * alpha;
+            acc[t] = mfma16x16x32(va, ph, acc[t]);
+            acc[t] = mfma16x16x32(va, pl, acc[t]);
+        }
+    }
+
+    l = wave_xor_sum16_32(l);
+
+    // ---- merge the 4 waves of this chunk in LDS, write one partial ----
+    __shared__ float sm_m[kWaves][16];
+    __shared__ float sm_l[kWaves][16];
+    __shared__ float sm_o[kWaves][16][D + 4];
+    if (g == 0) {
+        sm_m[wave][c] = m;
+        sm_l[wave][c] = l;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sm_o[wave][c][NT * (4 * g + r) + t] = acc[t][r];
+        }
+    }
+    __syncthreads();
+
+    const int n_items = a.group * D;
+    for (int item = threadIdx.x; item < n_items; item += blockDim.x) {
+        const int hh = item / D;
+        const int dd = item - hh * D;
+        float M = sm_m[0][hh];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            M = fmaxf(M, sm_m[w][hh]);
+        }
+        float L = 0.0f;
+        float O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float wt = fast_exp2(sm_m[w][hh] - M);  // exp2(-inf) = 0 for idle waves
+            L += sm_l[w][hh] * wt;
+            O += sm_o[w][hh][dd] * wt;
+        }
+        const size_t pidx = ((size_t)sl * a.heads + (size_t)kvh * a.group + hh) * a.max_chunks + chunk_id;
+        a.part_o[pidx * D + dd] = O;
+        if (dd == 0) {
+            a.part_ml[pidx * 2] = M;
+            a.part_ml[pidx * 2 + 1] = L;
+        }
+    }
+}
+
+struct CombineArgs {
+    const float *part_o;
+    const float *part_ml;
+    float *out;  // [SL][heads][D]
+    int layers;
+    int heads;
+    int head_dim;
+    int chunk;
+    int max_chunks;
+    int positions[TE_HIP_MAX_SEQS];
+};
+
+// One workgroup per (head, seq*layer): out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c.
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+    const int h = blockIdx.x;
+    const int sl = blockIdx.y;
+    const int s = sl / a.layers;
+    const int n_chunks = (a.positions[s] + a.chunk) / a.chunk;  // ceil((pos+1)/chunk)
+    const size_t base = ((size_t)sl * a.heads + h) * a.max_chunks;
+    const float *ml = a.part_ml + base * 2;
+    const int tid = threadIdx.x;
+
+    __shared__ float red[256];
+    __shared__ float wts[kMaxCombineChunks];
+
+    float mx = -INFINITY;
+    for (int i = tid; i < n_chunks; i += 256) {
+        mx = fmaxf(mx, ml[2 * i]);
+    }
+    red[tid] = mx;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) {
+            red[tid] = fmaxf(red[tid], red[tid + w]);
+        }
+        __syncthreads();
+    }
+    const float M = red[0];
+    __syncthreads();
+    float ls = 0.0f;
+    for (int i = tid; i < n_chunks; i += 256) {
+        const float w = fast_exp2(ml[2 * i] - M);
+        wts[i] = w;
+        ls += w * ml[2 * i + 1];
+    }
+    red[tid] = ls;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) {
+            red[tid] += red[tid + w];
+        }
+        __syncthreads();
+    }
+    const float L = red[0];
+    const float inv = L > 0.0f ? 1.0f / L : 1.0f;
+    const float *po = a.part_o + base * a.head_dim;
+    float *o = a.out + ((size_t)sl * a.heads + h) * a.head_dim;
+    for (int d = tid; d < a.head_dim; d += 256) {
+        float acc = 0.0f;
+        for (int i = 0; i < n_chunks; ++i) {
+            acc += wts[i] * po[(size_t)i * a.head_dim + d];
+        }
+        o[d] = acc * inv;
+    }
+}
+
+// fp32-cache decode for te_attention_decode_f32 (host-pointer API, any head_dim):
+// one wave per (chunk of 64*8 positions, head); scores in LDS, two-pass softmax
+// within the chunk, partial written for decode_combine_kernel.
+constexpr int kF32Chunk = 512;
+
+__global__ __launch_bounds__(64) void decode_f32_chunk_kernel(const float *query, const float *key_cache,
+                                                              const float *value_cache, int pos, int heads,
+                                                              int kv_heads, int head_dim, float qscale,
+                                                              int max_chunks, float *part_o, float *part_ml) {
+    const int chunk_id = blockIdx.x;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int c0 = chunk_id * kF32Chunk;
+    const int c1 = min(c0 + kF32Chunk, pos + 1);
+    const int kvh = h / (heads / kv_heads);
+    const float *q = query + (size_t)h * head_dim;
+    __shared__ float sc[kF32Chunk];
+
+    float mx = -INFINITY;
+    for (int p = c0 + lane; p < c1; p += 64) {
+        const float *kr = key_cache + ((size_t)p * kv_heads + kvh) * head_dim;
+        float dot = 0.0f;
+        for (int i = 0; i < head_dim; ++i) {
+            dot = fmaf(q[i], kr[i], dot);
+        }
+        const float x = dot * qscale;
+        sc[p - c0] = x;
+        mx = fmaxf(mx, x);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    }
+    float ls = 0.0f;
+    for (int p = c0 + lane; p < c1; p += 64) {
+        const float e = fast_exp2(sc[p - c0] - mx);
+        sc[p - c0] = e;
+        ls += e;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        ls += __shfl_xor(ls, off, 64);
+    }
+    __syncthreads();
+    const size_t pidx = (size_t)h * max_chunks + chunk_id;
+    for (int d = lane; d < head_dim; d += 64) {
+        float acc = 0.0f;
+        for (int p = c0; p < c1; ++p) {
+            acc = fmaf(sc[p - c0], value_cache[((size_t)p * kv_heads + kvh) * head_dim + d], acc);
+        }
+        part_o[pidx * head_dim + d] = acc;
+    }
+    if (lane == 0) {
+        part_ml[pidx * 2] = mx;
+        part_ml[pidx * 2 + 1] = ls;
+    }
+}
+
+bool valid_positions(const size_t *positions, size_t position, size_t seqs, size_t context_tokens,
+                     size_t *max_position) {
+    size_t mx = 0;
+    for (size_t s = 0; s < seqs; ++s) {
+        const size_t p = positions != nullptr ? positions[s] : position;
+        if (p >= context_tokens) {
+            return false;
+        }
+        if (p > mx) {
+            mx = p;
+        }
+    }
+    *max_position = mx;
+    return true;
+}
+
+te_status check_decode_args(const size_t *positions, size_t position, size_t seqs, size_t layers,
+                            size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+                            size_t *max_position) {
+    if (seqs == 0 || layers == 0 || context_tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 ||
+        (heads % kv_heads) != 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (seqs > TE_HIP_MAX_SEQS || (head_dim != 64 && head_dim != 128) || heads / kv_heads > 16 ||
+        seqs * layers > 65535 || context_tokens > (1u << 30) || kv_heads > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    if (!valid_positions(positions, position, seqs, context_tokens, max_position)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    return TE_STATUS_OK;
+}
+
+}  // namespace
+
+namespace te_hip {
+
+DecodeGeometry decode_geometry(size_t seqs, size_t layers, size_t max_position, size_t kv_heads) {
+    // Aim for ~8 workgroups per CU over the whole launch (256 CUs): enough to
+    // fill the machine and balance ragged sequences, few enough that the
+    // partials stay a small fraction of the KV bytes.  TE_HIP_DECODE_CHUNK
+    // (a multiple of 128) overrides the choice.
+    DecodeGeometry g;
+    const size_t n = max_position + 1;
+    const size_t streams = seqs * layers * kv_heads;
+    size_t chunk = kMinChunk;
+    while (chunk < 2048 && streams * ((n + chunk * 2 - 1) / (chunk * 2)) >= 2048) {
+        chunk *= 2;
+    }
+    const char *env = getenv("TE_HIP_DECODE_CHUNK");
+    if (env != nullptr) {
+        const long v = strtol(env, nullptr, 10);
+        if (v >= kMinChunk && v % kMinChunk == 0 && v <= (1 << 20)) {
+            chunk = (size_t)v;
+        }
+    }
+    while ((n + chunk - 1) / chunk > (size_t)kMaxCombineChunks) {
+        chunk *= 2;
+    }
+    g.chunk = (int)chunk;
+    g.max_chunks = (int)((n + chunk - 1) / chunk);
+    return g;
+}
+
+size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layers, size_t heads,
+                              size_t head_dim) {
+    const size_t parts = seqs * layers * heads * (size_t)g.max_chunks;
+    return parts * head_dim * sizeof(float) + parts * 2 * sizeof(float);
+}
+
+te_status launch_decode_f32(const float *query, const float *key_cache, const float *value_cache,
+                            size_t position, size_t heads, size_t kv_heads, size_t head_dim, float *out,
+                            float *part_o, float *part_ml, hipStream_t stream) {
+    const int max_chunks = (int)((position + 1 + kF32Chunk - 1) / kF32Chunk);
+    const float qscale = TE_LOG2E / sqrtf((float)head_dim);
+    decode_f32_chunk_kernel<<<dim3(max_chunks, (unsigned)heads), 64, 0, stream>>>(
+        query, key_cache, value_cache, (int)position, (int)heads, (int)kv_heads, (int)head_dim, qscale,
+        max_chunks, part_o, part_ml);
+    te_status st = launch_status();
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    CombineArgs c;
+    c.part_o = part_o;
+    c.part_ml = part_ml;
+    c.out = out;
+    c.layers = 1;
+    c.heads = (int)heads;
+    c.head_dim = (int)head_dim;
+    c.chunk = kF32Chunk;
+    c.max_chunks = max_chunks;
+    c.positions[0] = (int)position;
+    decode_combine_kernel<<<dim3((unsigned)heads, 1), 256, 0, stream>>>(c);
+    return launch_status();
+}
+
+}  // namespace te_hip
+
+extern "C" size_t te_hip_attention_decode_workspace_bytes(size_t seqs, size_t layers, size_t max_position,
+                                                          size_t heads, size_t kv_heads, size_t head_dim) {
+    if (seqs == 0 || layers == 0 || heads == 0 || kv_heads == 0 || head_dim == 0) {
+        return 0;
+    }
+    const te_hip::DecodeGeometry g = te_hip::decode_geometry(seqs, layers, max_position, kv_heads);
+    return te_hip::decode_workspace_bytes(g, seqs, layers, heads, head_dim);
+}
+
+extern "C" te_status te_hip_attention_decode_splitk_f16(
+    const float *query, const uint16_t *key_cache, const uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    if (query == nullptr || key_cache == nullptr || value_cache == nullptr || workspace == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    size_t max_position = 0;
+    te_status st = check_decode_args(positions, position, seqs, layers, context_tokens, heads, kv_heads,
+                                     head_dim, &max_position);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(seqs, layers, max_position, kv_heads);
+    if (workspace_bytes < te_hip::decode_workspace_bytes(geo, seqs, layers, heads, head_dim)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    DecodeArgs a;
+    a.query = query;
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
+    const size_t parts = seqs * layers * heads * (size_t)geo.max_chunks;
+    a.part_o = static_cast<float *>(workspace);
+    a.part_ml = a.part_o + parts * head_dim;
+    a.layers = (int)layers;
+    a.ctx = (int)context_tokens;
+    a.heads = (int)heads;
+    a.kv_heads = (int)kv_heads;
+    a.group = (int)(heads / kv_heads);
+    a.chunk = geo.chunk;
+    a.max_chunks = geo.max_chunks;
+    a.qscale = TE_LOG2E / sqrtf((float)head_dim);
+    for (size_t s = 0; s < seqs; ++s) {
+        a.positions[s] = (int)(positions != nullptr ? positions[s] : position);
+    }
+    const dim3 grid((unsigned)geo.max_chunks, (unsigned)kv_heads, (unsigned)(seqs * layers));
+    hipStream_t strm = te_hip::as_stream(stream);
+    if (head_dim == 128) {
+        decode_splitk_f16_kernel<128><<<grid, 256, 0, strm>>>(a);
+    } else {
+        decode_splitk_f16_kernel<64><<<grid, 256, 0, strm>>>(a);
+    }
+    return te_hip::launch_status();
+}
+
+extern "C" te_status te_hip_attention_decode_combine(
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, const void *workspace, size_t workspace_bytes, void *stream) {
+    if (out == nullptr || workspace == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    size_t max_position = 0;
+    te_status st = check_decode_args(positions, position, seqs, layers, (size_t)1 << 30, heads, kv_heads,
+                                     head_dim, &max_position);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(seqs, layers, max_position, kv_heads);
+    if (workspace_bytes < te_hip::decode_workspace_bytes(geo, seqs, layers, heads, head_dim)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    CombineArgs c;
+    const size_t parts = seqs * layers * heads * (size_t)geo.max_chunks;
+    c.part_o = static_cast<const float *>(workspace);
+    c.part_ml = c.part_o + parts * head_dim;
+    c.out = out;
+    c.layers = (int)layers;
+    c.heads = (int)heads;
+    c.head_dim = (int)head_dim;
+    c.chunk = geo.chunk;
+    c.max_chunks = geo.max_chunks;
+    for (size_t s = 0; s < seqs; ++s) {
+        c.positions[s] = (int)(positions != nullptr ? positions[s] : position);
+    }
+    decode_combine_kernel<<<dim3((unsigned)heads, (unsigned)(seqs * layers)), 256, 0, te_hip::as_stream(stream)>>>(c);
+    return te_hip::launch_status();
+}

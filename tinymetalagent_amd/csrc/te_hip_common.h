@@ -1,0 +1,84 @@
+// Shared device types, MFMA wrappers and launch helpers for the gfx950
+// attention kernels.  CDNA4 only: wave64, v_mfma_f32_16x16x32_f16 (gfx950),
+// v_mfma_f32_16x16x4_f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "te_hip_backend.h"
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// log2(e): softmax runs in the base-2 domain, exp(x) == exp2(x * log2(e)).
+#define TE_LOG2E 1.4426950408889634f
+
+// D = A(16 x 32) * B(32 x 16) + C, fp16 operands, fp32 accumulation.
+// Lane l holds A row (l % 16) and B column (l % 16), eight K-elements each
+// (the same K-subset for A and B, selected by l / 16); D lane l holds column
+// (l % 16), rows 4*(l / 16) + {0,1,2,3}.
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// fp32 MFMA: A(16 x 4) * B(4 x 16); lane l holds A[l%16][l/16], B[l/16][l%16].
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_xor_max16_32(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_xor_sum16_32(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Split x into hi + lo fp16 parts (hi = RNE(x), lo = RNE(x - hi)) so that a
+// pair of fp16 MFMAs reproduces an fp32 operand to ~2^-22 relative.
+__device__ __forceinline__ void split_f16(float x, f16 &hi, f16 &lo) {
+    hi = (f16)x;
+    lo = (f16)(x - (float)hi);
+}
+
+// Host-side helpers shared by the launchers.
+namespace te_hip {
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline te_status launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TE_STATUS_OK : TE_STATUS_RUNTIME_ERROR;
+}
+
+// Decode split-K geometry, shared by the split-K and combine launches and the
+// workspace-size query so all three agree.
+struct DecodeGeometry {
+    int chunk;       // cache positions per workgroup (multiple of 128)
+    int max_chunks;  // chunks of the longest sequence
+};
+
+DecodeGeometry decode_geometry(size_t seqs, size_t layers, size_t max_position, size_t kv_heads);
+
+size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layers, size_t heads, size_t head_dim);
+
+// Internal launchers used by the host-pointer wrappers (te_hip_runtime.hip).
+te_status launch_decode_f32(const float *query, const float *key_cache, const float *value_cache,
+                            size_t position, size_t heads, size_t kv_heads, size_t head_dim, float *out,
+                            float *part_o, float *part_ml, hipStream_t stream);
+te_status launch_rope_rows(float *values, size_t heads, size_t head_dim, const float *cos_row,
+                           const float *sin_row, hipStream_t stream);
+te_status launch_mma_kat(int mode, const float *query, const float *key_t, const float *value, int k_cols,
+                         int q_base, float *out, hipStream_t stream);
+
+}  // namespace te_hip

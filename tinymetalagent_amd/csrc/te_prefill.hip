@@ -1,0 +1,305 @@
+// Batched-prefill causal attention (flash-attention forward) on fp16 MFMA.
+//
+// Semantics: row t of (seq, layer) is the reference decode at position
+// base + t over the cache (qwen.c:810-824), i.e. the causal mask
+// `key <= base + row` of te_attention_flash_mma_t_f32_kernel
+// (metal_kernels.metal.inc:2767-2775), which also defines chunked prefill.
+//
+// One workgroup = 4 waves = BM (128) query rows of one head; each wave owns
+// 32 rows (two 16-row MFMA column blocks).  K/V blocks of BN (64) positions of
+// the head's KV group are staged through LDS, double-buffered: the global loads
+// of block n+1 are in flight while block n is consumed, one barrier per block.
+//
+//   S^T[64 keys x 32 rows] = K[64 x D] . Q^T[D x 32]            fp16 MFMA 16x16x32
+//   O^T[D x 32 rows]      += V^T[D x 64] . P^T[64 x 32]         fp16 MFMA 16x16x32
+//
+// The S^T result layout (lane = row c, keys 4g+r) is the P^T B-operand layout
+// of the PV MFMA (keys kmap(g,j) = 16(j/4)+4g+(j%4) per 32-key step), so P stays
+// in registers.  V^T's A operand is read from row-major LDS as 16-byte rows of
+// NT consecutive dims for 8 keys and transposed in registers (output tile t
+// covers dims {NT*m + t}), so O^T comes out with each lane holding 4*NT
+// contiguous dims of one row.  Softmax statistics are fp32, base-2, per row.
+// Q and P are single fp16 operands (the rotated q is already fp16 here).
+//
+// Work per (seq, layer): 2*heads*D*sum_t(base+t+1) MACs (QK^T + PV); the
+// roofline unit is that count x2 FLOP.  Query tiles are issued heaviest-first
+// (largest row index first) to balance the causal triangle.
+#include "te_hip_common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int BM = 128;
+constexpr int BN = 64;
+
+struct PrefillArgs {
+    const f16 *q;
+    const f16 *key_cache;
+    const f16 *value_cache;
+    float *out;
+    int layers;
+    int tokens;
+    int base;
+    int ctx;
+    int heads;
+    int kv_heads;
+    int group;
+    int n_qtiles;
+    float qscale;  // log2(e)/sqrt(D), applied to the fp32 scores
+};
+
+template <int D>
+struct VRow;
+template <>
+struct VRow<128> {
+    typedef f16x8 type;
+};
+template <>
+struct VRow<64> {
+    typedef f16x4 type;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) {
+    constexpr int KK = D / 32;          // QK^T K-steps
+    constexpr int NT = D / 16;          // O^T output tiles
+    constexpr int LROW = D + 8;         // LDS row pitch in halves (16-byte pad)
+    constexpr int CPR = D / 8;          // 16-byte chunks per cache row
+    constexpr int LOADS = BN * CPR / 256;
+    typedef typename VRow<D>::type vrow_t;
+
+    __shared__ __attribute__((aligned(16))) f16 lds_k[2][BN * LROW];
+    __shared__ __attribute__((aligned(16))) f16 lds_v[2][BN * LROW];
+
+    const int qt = a.n_qtiles - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y;
+    const int sl = blockIdx.z;
+    const int kvh = h / a.group;
+    const int r0 = qt * BM;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int wr0 = r0 + 32 * wave;  // first row of this wave
+
+    const size_t row_stride = (size_t)a.kv_heads * D;
+    const size_t cache_base = (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
+    const f16 *kbase = a.key_cache + cache_base;
+    const f16 *vbase = a.value_cache + cache_base;
+
+    // Q^T operand for the wave's two 16-row blocks.
+    f16x8 qop[2][KK];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int row = wr0 + 16 * nb + c;
+        const bool ok = row < a.tokens;
+        const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            f16x8 v = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
+            if (!ok) {
+                v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+            qop[nb][kk] = v;
+        }
+    }
+
+    const int last_row = min(r0 + BM, a.tokens) - 1;
+    const int kmax = a.base + last_row;  // last key any row of this tile sees
+    const int n_blocks = kmax / BN + 1;
+
+    f16x8 kreg[LOADS], vreg[LOADS];
+    auto gload = [&](int blk) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int idx = tid + 256 * i;
+            const int key = min(blk * BN + idx / CPR, kmax);
+            const int col = (idx % CPR) * 8;
+            kreg[i] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)key * row_stride + col);
+            vreg[i] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)key * row_stride + col);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int idx = tid + 256 * i;
+            const int off = (idx / CPR) * LROW + (idx % CPR) * 8;
+            *reinterpret_cast<f16x8 *>(&lds_k[buf][off]) = kreg[i];
+            *reinterpret_cast<f16x8 *>(&lds_v[buf][off]) = vreg[i];
+        }
+    };
+
+    float m[2] = {-INFINITY, -INFINITY};
+    float l[2] = {0.0f, 0.0f};
+    f32x4 o[2][NT];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            o[nb][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+
+    const int wave_last_row = min(wr0 + 31, a.tokens - 1);
+    const bool wave_active = wr0 < a.tokens;
+    const int wave_max_pos = a.base + wave_last_row;
+    const int wave_min_pos = a.base + wr0;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+
+    for (int blk = 0; blk < n_blocks; ++blk) {
+        const int buf = blk & 1;
+        if (blk + 1 < n_blocks) {
+            gload(blk + 1);
+        }
+        const int kb0 = blk * BN;
+        if (wave_active && kb0 <= wave_max_pos) {
+            const f16 *lk = lds_k[buf];
+            const f16 *lv = lds_v[buf];
+            // ---- S^T = K Q^T ----
+            f32x4 s[4][2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(lk + (16 * i + c) * LROW + 8 * g + 32 * kk);
+                    s[i][0] = mfma16x16x32(ka, qop[0][kk], s[i][0]);
+                    s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
+                }
+            }
+            // ---- scale, causal mask, online softmax per row ----
+            const bool need_mask = kb0 + BN - 1 > wave_min_pos;
+            f16x8 pb[2][2];  // [k-step][row block]
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const int rowpos = a.base + wr0 + 16 * nb + c;
+                float x[16];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float v = s[i][nb][r] * a.qscale;
+                        if (need_mask && kb0 + 16 * i + 4 * g + r > rowpos) {
+                            v = -INFINITY;
+                        }
+                        x[4 * i + r] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                }
+                mx = wave_xor_max16_32(mx);
+                const float m_new = fmaxf(m[nb], mx);
+                const float alpha = fast_exp2(m[nb] - m_new);
+                m[nb] = m_new;
+                float psum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float p = fast_exp2(x[e] - m_new);
+                    psum += p;
+                    pb[e >> 3][nb][e & 7] = (f16)p;
+                }
+                l[nb] = l[nb] * alpha + psum;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    o[nb][t] = o[nb][t] * alpha;
+                }
+            }
+            // ---- O^T += V^T P^T ----
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                vrow_t vr[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int key = 32 * ks + 16 * (j >> 2) + 4 * g + (j & 3);
+                    vr[j] = *reinterpret_cast<const vrow_t *>(lv + key * LROW + NT * c);
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    f16x8 va;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        va[j] = vr[j][t];
+                    }
+                    o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
+                    o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
+                }
+            }
+        }
+        if (blk + 1 < n_blocks) {
+            lstore(buf ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: normalise and store rows (dims 4NT*g .. 4NT*g + 4NT - 1) ----
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const float lsum = wave_xor_sum16_32(l[nb]);
+        const int row = wr0 + 16 * nb + c;
+        if (row < a.tokens) {
+            const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+            float *orow = a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int t = 0; t < NT; t += 4) {
+                    float4 v;
+                    v.x = o[nb][t][r] * inv;
+                    v.y = o[nb][t + 1][r] * inv;
+                    v.z = o[nb][t + 2][r] * inv;
+                    v.w = o[nb][t + 3][r] * inv;
+                    *reinterpret_cast<float4 *>(orow + NT * (4 * g + r) + t) = v;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" te_status te_hip_attention_prefill_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *stream) {
+    if (q_half == nullptr || key_cache == nullptr || value_cache == nullptr || out == nullptr || seqs == 0 ||
+        layers == 0 || tokens == 0 || context_tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 ||
+        (heads % kv_heads) != 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if ((head_dim != 64 && head_dim != 128) || context_tokens > (1u << 30) || heads > 65535 ||
+        seqs * layers > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    if (base_position > context_tokens || tokens > context_tokens - base_position) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    PrefillArgs a;
+    a.q = reinterpret_cast<const f16 *>(q_half);
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
+    a.out = out;
+    a.layers = (int)layers;
+    a.tokens = (int)tokens;
+    a.base = (int)base_position;
+    a.ctx = (int)context_tokens;
+    a.heads = (int)heads;
+    a.kv_heads = (int)kv_heads;
+    a.group = (int)(heads / kv_heads);
+    a.n_qtiles = (int)((tokens + BM - 1) / BM);
+    a.qscale = TE_LOG2E / sqrtf((float)head_dim);
+    const dim3 grid((unsigned)a.n_qtiles, (unsigned)heads, (unsigned)(seqs * layers));
+    hipStream_t strm = te_hip::as_stream(stream);
+    if (head_dim == 128) {
+        prefill_causal_f16_kernel<128><<<grid, 256, 0, strm>>>(a);
+    } else {
+        prefill_causal_f16_kernel<64><<<grid, 256, 0, strm>>>(a);
+    }
+    return te_hip::launch_status();
+}

@@ -1,0 +1,198 @@
+// Bias + RoPE + fp16 KV-cache append (decode: 1 token per (seq, layer);
+// prefill: `tokens` tokens per (seq, layer)), and the plain row rotation used
+// by te_rope_f32.
+//
+// Semantics follow te_qkv_bias_rope_cache_batch_f32 / _h_f32
+// (reference metal_kernels.metal.inc:2172-2252, :2344-2429) and the CPU order
+// bias-add -> te_qwen_rope_cached -> append (qwen.c:774-808, :998-1036):
+//   a = x[i] + bias[i], b = x[i+half] + bias[i+half]
+//   x[i] = a*cos - b*sin,  x[i+half] = b*cos + a*sin
+// FP contraction is off in this file so the rotated values are bit-identical
+// to the CPU reference given the same cos/sin table rows; the bias add is
+// skipped (not "+0") when no bias is given, again matching the CPU path.
+//
+// HBM traffic per token-layer: read q,k,v fp32 + table row, write q,k,v fp32
+// and k,v fp16 -- a few KB; the kernel is launch/latency-bound at decode and
+// HBM-bound at prefill.
+#include "te_hip_common.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+struct RopeAppendArgs {
+    float *q;
+    float *k;
+    float *v;
+    const float *q_bias;
+    const float *k_bias;
+    const float *v_bias;
+    const float *cos_t;
+    const float *sin_t;
+    f16 *key_cache;
+    f16 *value_cache;
+    f16 *q_half;
+    int layers;
+    int tokens;
+    int ctx;
+    int heads;
+    int kv_heads;
+    int head_dim;
+    int base[TE_HIP_MAX_SEQS];
+};
+
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
+    const int item = blockIdx.x * blockDim.x + threadIdx.x;
+    const int b = blockIdx.y;
+    const int sl = blockIdx.z;
+    const int s = sl / a.layers;
+    const int layer = sl - s * a.layers;
+    const int half = a.head_dim >> 1;
+    const int pos = a.base[s] + b;
+    const int hidden = a.heads * a.head_dim;
+    const int kv_dim = a.kv_heads * a.head_dim;
+    const float *cos_row = a.cos_t + (size_t)pos * half;
+    const float *sin_row = a.sin_t + (size_t)pos * half;
+    const size_t tok = (size_t)sl * a.tokens + b;
+
+    if (item < a.heads * half) {
+        const int head = item / half;
+        const int i = item - head * half;
+        const int off = head * a.head_dim + i;
+        float *qrow = a.q + tok * hidden;
+        float x0 = qrow[off];
+        float x1 = qrow[off + half];
+        if (a.q_bias != nullptr) {
+            x0 = x0 + a.q_bias[(size_t)layer * hidden + off];
+            x1 = x1 + a.q_bias[(size_t)layer * hidden + off + half];
+        }
+        const float c = cos_row[i];
+        const float sn = sin_row[i];
+        const float lo = x0 * c - x1 * sn;
+        const float hi = x1 * c + x0 * sn;
+        qrow[off] = lo;
+        qrow[off + half] = hi;
+        if (a.q_half != nullptr) {
+            a.q_half[tok * hidden + off] = (f16)lo;
+            a.q_half[tok * hidden + off + half] = (f16)hi;
+        }
+    }
+
+    const size_t slot = ((size_t)sl * a.ctx + pos) * kv_dim;
+    if (item < a.kv_heads * half) {
+        const int head = item / half;
+        const int i = item - head * half;
+        const int off = head * a.head_dim + i;
+        float *krow = a.k + tok * kv_dim;
+        float x0 = krow[off];
+        float x1 = krow[off + half];
+        if (a.k_bias != nullptr) {
+            x0 = x0 + a.k_bias[(size_t)layer * kv_dim + off];
+            x1 = x1 + a.k_bias[(size_t)layer * kv_dim + off + half];
+        }
+        const float c = cos_row[i];
+        const float sn = sin_row[i];
+        const float lo = x0 * c - x1 * sn;
+        const float hi = x1 * c + x0 * sn;
+        krow[off] = lo;
+        krow[off + half] = hi;
+        a.key_cache[slot + off] = (f16)lo;
+        a.key_cache[slot + off + half] = (f16)hi;
+    }
+
+    if (item < kv_dim) {
+        float *vrow = a.v + tok * kv_dim;
+        float x = vrow[item];
+        if (a.v_bias != nullptr) {
+            x = x + a.v_bias[(size_t)layer * kv_dim + item];
+            vrow[item] = x;
+        }
+        a.value_cache[slot + item] = (f16)x;
+    }
+}
+
+// In-place rotation of `heads` rows with one cos/sin row (te_rope_f32).
+__global__ __launch_bounds__(256) void rope_rows_kernel(float *values, int heads, int head_dim,
+                                                        const float *cos_row, const float *sin_row) {
+    const int item = blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = head_dim >> 1;
+    if (item >= heads * half) {
+        return;
+    }
+    const int head = item / half;
+    const int i = item - head * half;
+    float *row = values + (size_t)head * head_dim;
+    const float x0 = row[i];
+    const float x1 = row[i + half];
+    const float c = cos_row[i];
+    const float sn = sin_row[i];
+    row[i] = x0 * c - x1 * sn;
+    row[i + half] = x1 * c + x0 * sn;
+}
+
+}  // namespace
+
+namespace te_hip {
+
+te_status launch_rope_rows(float *values, size_t heads, size_t head_dim, const float *cos_row,
+                           const float *sin_row, hipStream_t stream) {
+    const size_t items = heads * (head_dim / 2);
+    const unsigned blocks = (unsigned)((items + 255) / 256);
+    rope_rows_kernel<<<blocks, 256, 0, stream>>>(values, (int)heads, (int)head_dim, cos_row, sin_row);
+    return launch_status();
+}
+
+}  // namespace te_hip
+
+extern "C" te_status te_hip_rope_kv_append_f16(
+    float *q, float *k, float *v,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *q_half,
+    size_t seqs, size_t layers, size_t tokens,
+    const size_t *base_positions, size_t base_position,
+    size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+    void *stream) {
+    if (q == nullptr || k == nullptr || v == nullptr || rope_cos == nullptr || rope_sin == nullptr ||
+        key_cache == nullptr || value_cache == nullptr || seqs == 0 || layers == 0 || tokens == 0 ||
+        context_tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || (head_dim % 2) != 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (seqs > TE_HIP_MAX_SEQS || head_dim > 256 || heads * head_dim > (1u << 20) ||
+        context_tokens > (1u << 30) || tokens > 65535 || seqs * layers > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    RopeAppendArgs a;
+    for (size_t s = 0; s < seqs; ++s) {
+        const size_t base = base_positions != nullptr ? base_positions[s] : base_position;
+        if (base > context_tokens || tokens > context_tokens - base) {
+            return TE_STATUS_INVALID_ARGUMENT;
+        }
+        a.base[s] = (int)base;
+    }
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_bias = q_bias;
+    a.k_bias = k_bias;
+    a.v_bias = v_bias;
+    a.cos_t = rope_cos;
+    a.sin_t = rope_sin;
+    a.key_cache = reinterpret_cast<f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<f16 *>(value_cache);
+    a.q_half = reinterpret_cast<f16 *>(q_half);
+    a.layers = (int)layers;
+    a.tokens = (int)tokens;
+    a.ctx = (int)context_tokens;
+    a.heads = (int)heads;
+    a.kv_heads = (int)kv_heads;
+    a.head_dim = (int)head_dim;
+    const size_t half = head_dim / 2;
+    size_t items = heads * half;
+    if (kv_heads * head_dim > items) {
+        items = kv_heads * head_dim;
+    }
+    const dim3 grid((unsigned)((items + 255) / 256), (unsigned)tokens, (unsigned)(seqs * layers));
+    rope_kv_append_kernel<<<grid, 256, 0, te_hip::as_stream(stream)>>>(a);
+    return te_hip::launch_status();
+}
