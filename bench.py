@@ -124,7 +124,7 @@ def bench_decode(torch, A, args) -> dict:
         v = torch.randn((1, LAYERS, 1, KV, D), generator=g, device=dev)
         sets.append((q, k, v, kc, vc))
     cos, sin = A.rope_table(ctx, D, THETA)
-    ws = A.decode_workspace(1, LAYERS, L, H, KV, D)
+    ws = A.decode_workspace(1, LAYERS, H, KV, D, position=L)
     out = torch.empty((1, LAYERS, H, D), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream()
 

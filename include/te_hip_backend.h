@@ -108,11 +108,15 @@ TE_API te_status te_hip_rope_kv_append_f16(
  * head_dim in {64, 128}; heads/kv_heads <= 16.
  *
  * workspace: device scratch of at least te_hip_attention_decode_workspace_bytes
- * bytes, or NULL to use a buffer the library owns (grown on demand, guarded by
- * the library mutex).  Calls sharing one workspace must be stream-ordered.
+ * bytes for the same positions, or NULL to use a buffer the library owns (grown
+ * on demand, guarded by the library mutex; calls using it must all go to one
+ * stream).  Calls sharing one workspace must be stream-ordered.  The chunking
+ * (and so the workspace size) depends on all positions, not only the longest:
+ * the chunk length balances the total work over the GPU's wave slots.
  */
-TE_API size_t te_hip_attention_decode_workspace_bytes(size_t seqs, size_t layers, size_t max_position,
-                                                      size_t heads, size_t kv_heads, size_t head_dim);
+TE_API size_t te_hip_attention_decode_workspace_bytes(const size_t *positions, size_t position, size_t seqs,
+                                                      size_t layers, size_t heads, size_t kv_heads,
+                                                      size_t head_dim);
 
 TE_API te_status te_hip_attention_decode_f16(
     const float *query, const uint16_t *key_cache, const uint16_t *value_cache,

@@ -126,9 +126,11 @@ def test_backend_guard_conventions(lib):
 
 
 def test_workspace_query(lib):
-    n = lib.te_hip_attention_decode_workspace_bytes(1, 36, 8192, 16, 2, 128)
+    n = lib.te_hip_attention_decode_workspace_bytes(None, 8192, 1, 36, 16, 2, 128)
     assert n > 0
-    assert lib.te_hip_attention_decode_workspace_bytes(0, 36, 8192, 16, 2, 128) == 0
+    assert lib.te_hip_attention_decode_workspace_bytes(None, 8192, 0, 36, 16, 2, 128) == 0
+    pos = (ctypes.c_size_t * 3)(100, 5000, 7)
+    assert lib.te_hip_attention_decode_workspace_bytes(pos, 0, 3, 2, 28, 4, 128) > 0
 
 
 def test_out_of_scope_entry_points_report_unsupported():

@@ -79,10 +79,11 @@ def rope_kv_append(q, k, v, rope_cos, rope_sin, key_cache, value_cache, *, base_
         kv_heads, head_dim, _stream(stream)))
 
 
-def decode_workspace(seqs: int, layers: int, max_position: int, heads: int, kv_heads: int, head_dim: int,
-                     device="cuda") -> torch.Tensor:
-    n = load_library().te_hip_attention_decode_workspace_bytes(seqs, layers, max_position, heads, kv_heads,
-                                                                head_dim)
+def decode_workspace(seqs: int, layers: int, heads: int, kv_heads: int, head_dim: int, *, position: int = 0,
+                     positions: Sequence[int] | None = None, device="cuda") -> torch.Tensor:
+    """Workspace for attention_decode with exactly these positions."""
+    n = load_library().te_hip_attention_decode_workspace_bytes(_positions(positions), position, seqs, layers, heads,
+                                                                kv_heads, head_dim)
     if n == 0:
         raise TinyEngineError("invalid argument")
     return torch.empty(n, dtype=torch.uint8, device=device)

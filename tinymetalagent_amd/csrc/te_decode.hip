@@ -6,11 +6,11 @@
 // the softmax is online (base-2, exp2 of log2e-prescaled scores) per chunk and
 // merged exactly by the combine kernel; every accumulation is fp32.
 //
-// Split-K kernel, one workgroup (4 waves) per (chunk of positions, kv_head,
-// seq*layer).  Each wave streams its share of the chunk 32 positions at a time
-// for all `group` (= heads/kv_heads <= 16) query heads of its KV head at once,
-// so every K/V element is read from HBM exactly once per query token (the GQA
-// sharing of te_attention_flash_gqa_f32_kernel, metal_kernels.metal.inc:3209-3372):
+// Split-K kernel, one single-wave workgroup per (chunk of positions, kv_head,
+// seq*layer).  The wave streams its chunk 32 positions at a time for all
+// `group` (= heads/kv_heads <= 16) query heads of its KV head at once, so every
+// K/V element is read from HBM exactly once per query token (the GQA sharing of
+// te_attention_flash_gqa_f32_kernel, metal_kernels.metal.inc:3209-3372):
 //
 //   S^T[32 pos x 16 heads] = K[32 x D] . Q^T[D x 16]          (fp16 MFMA 16x16x32)
 //   O^T[D x 16 heads]     += V^T[D x 32 pos] . P^T[32 x 16]    (fp16 MFMA 16x16x32)
@@ -25,9 +25,13 @@
 //               output tile t = dims {NT*m + t}.
 //   S^T result: lane holds head c at positions 4g+r (+16h) -- exactly the
 //               P^T B-operand layout of the PV MFMA for kmap, so P never moves.
-//   O^T result: lane holds head c, dims 4NT*g .. 4NT*g + 4NT - 1.
-// K and V go from HBM straight into MFMA operand registers; no LDS staging
-// is needed on this path (LDS is used only for the in-workgroup merge).
+//   O^T result: lane holds head c, dims 4NT*g .. 4NT*g + 4NT - 1, written
+//               straight to the partial with 16-byte stores.
+// K and V go from HBM straight into MFMA operand registers (no LDS), and the
+// next tile's loads are issued before the current tile is consumed (two
+// register tiles, 32 KB in flight per wave).  The chunk length is chosen from
+// the total tile count so one launch gives every wave slot about one chunk,
+// which also balances ragged sequence lengths.
 //
 // HBM bytes per (seq, layer), the roofline unit: 2*(pos+1)*kv_heads*D*2 B of
 // K/V + heads*D*4 B of q; partials add (chunks*heads*(D+2)*4 B) x2.
@@ -38,9 +42,8 @@
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kTile = 32;                   // positions per MFMA step
-constexpr int kMinChunk = kWaves * kTile;   // 128
+constexpr int kTile = 32;               // positions per MFMA step
+constexpr int kWavesPerCU = 8;          // resident split-K waves per CU (2 per SIMD at its register use)
 constexpr int kMaxCombineChunks = 4096;
 
 struct DecodeArgs {
@@ -72,10 +75,92 @@ struct VRow<64> {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void decode_splitk_f16_kernel(DecodeArgs a) {
+struct DecodeTile {
+    f16x8 k[2][D / 32];
+    typename VRow<D>::type v[8];
+};
+
+template <int D>
+__device__ __forceinline__ void decode_load_tile(DecodeTile<D> &t, const f16 *kbase, const f16 *vbase,
+                                                 int row_stride, int p0, int last, int g, int c) {
+    constexpr int NT = D / 16;
+    constexpr int KK = D / 32;
+    typedef typename VRow<D>::type vrow_t;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int pr = min(p0 + 16 * h + c, last);
+        const f16 *kr = kbase + pr * row_stride;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            t.k[h][kk] = *reinterpret_cast<const f16x8 *>(kr + 8 * g + 32 * kk);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int pr = min(p0 + 16 * (j >> 2) + 4 * g + (j & 3), last);
+        t.v[j] = *reinterpret_cast<const vrow_t *>(vbase + pr * row_stride + NT * c);
+    }
+}
+
+// One 32-position step of the online softmax + both MFMA products.
+template <int D>
+__device__ __forceinline__ void decode_consume_tile(const DecodeTile<D> &t, const f16x8 (&qh)[D / 32],
+                                                    const f16x8 (&ql)[D / 32], int p0, int pos, int g,
+                                                    float &m, float &l, f32x4 (&acc)[D / 16]) {
+    constexpr int NT = D / 16;
+    constexpr int KK = D / 32;
+    f32x4 sacc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        sacc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            sacc[h] = mfma16x16x32(t.k[h][kk], qh[kk], sacc[h]);
+            sacc[h] = mfma16x16x32(t.k[h][kk], ql[kk], sacc[h]);
+        }
+    }
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int p = p0 + 16 * (j >> 2) + 4 * g + (j & 3);
+        const float x = sacc[j >> 2][j & 3];
+        sv[j] = p <= pos ? x : -INFINITY;
+        mx = fmaxf(mx, sv[j]);
+    }
+    mx = wave_xor_max16_32(mx);
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp2(m - m_new);
+    m = m_new;
+    f16x8 ph, pl;
+    float psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float p = fast_exp2(sv[j] - m_new);
+        psum += p;
+        f16 hi, lo;
+        split_f16(p, hi, lo);
+        ph[j] = hi;
+        pl[j] = lo;
+    }
+    l = l * alpha + psum;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        f16x8 va;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            va[j] = t.v[j][tt];
+        }
+        acc[tt] = acc[tt] * alpha;
+        acc[tt] = mfma16x16x32(va, ph, acc[tt]);
+        acc[tt] = mfma16x16x32(va, pl, acc[tt]);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) {
     constexpr int NT = D / 16;  // output tiles over head_dim; also dims per lane in V loads
     constexpr int KK = D / 32;  // MFMA K-steps over head_dim for QK^T
-    typedef typename VRow<D>::type vrow_t;
 
     const int chunk_id = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -84,32 +169,37 @@ __global__ __launch_bounds__(256) void decode_splitk_f16_kernel(DecodeArgs a) {
     const int pos = a.positions[s];
     const int c0 = chunk_id * a.chunk;
     if (c0 > pos) {
-        return;  // uniform for the whole workgroup: this sequence has fewer chunks
+        return;  // this sequence has fewer chunks than the longest one
     }
     const int c1 = min(c0 + a.chunk, pos + 1);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int last = c1 - 1;  // loads are clamped to the chunk; positions > pos are masked
+    const int lane = threadIdx.x;
     const int g = lane >> 4;
     const int c = lane & 15;
-    const int span = a.chunk / kWaves;
-    const int w0 = c0 + wave * span;
-    const int w1 = min(w0 + span, c1);
 
-    const size_t row_stride = (size_t)a.kv_heads * D;
+    const int row_stride = a.kv_heads * D;
     const size_t sl_base = (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
     const f16 *kbase = a.key_cache + sl_base;
     const f16 *vbase = a.value_cache + sl_base;
 
-    // Q^T operand, hi/lo split, pre-scaled into the log2 domain.
+    DecodeTile<D> ta, tb;
+    decode_load_tile<D>(ta, kbase, vbase, row_stride, c0, last, g, c);
+
+    // Q^T operand, hi/lo split, pre-scaled into the log2 domain (loads overlap tile 0).
     f16x8 qh[KK], ql[KK];
     {
         const bool head_ok = c < a.group;
         const float *qrow = a.query + ((size_t)sl * a.heads + (size_t)kvh * a.group + (head_ok ? c : 0)) * D;
+        float4 xq[2 * KK];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk);
-            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk + 4);
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            xq[2 * kk] = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk);
+            xq[2 * kk + 1] = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk + 4);
+        }
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const float xs[8] = {xq[2 * kk].x, xq[2 * kk].y, xq[2 * kk].z, xq[2 * kk].w,
+                                 xq[2 * kk + 1].x, xq[2 * kk + 1].y, xq[2 * kk + 1].z, xq[2 * kk + 1].w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float x = head_ok ? xs[j] * a.qscale : 0.0f;
@@ -129,119 +219,47 @@ __global__ __launch_bounds__(256) void decode_splitk_f16_kernel(DecodeArgs a) {
         acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    for (int p0 = w0; p0 < w1; p0 += kTile) {
-        // ---- loads (positions past `pos` are clamped to `pos`, then masked) ----
-        f16x8 kf[2][KK];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int pr = min(p0 + 16 * h + c, pos);
-            const f16 *kr = kbase + (size_t)pr * row_stride;
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                kf[h][kk] = *reinterpret_cast<const f16x8 *>(kr + 8 * g + 32 * kk);
-            }
+    // Two register tiles, ping-pong: the loads of step n+1 are in flight while
+    // step n is consumed.  Every branch below is wave-uniform.
+    int p0 = c0;
+    for (;;) {
+        if (p0 + 32 < c1) {
+            decode_load_tile<D>(tb, kbase, vbase, row_stride, p0 + 32, last, g, c);
         }
-        vrow_t vr[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int pr = min(p0 + 16 * (j >> 2) + 4 * g + (j & 3), pos);
-            vr[j] = *reinterpret_cast<const vrow_t *>(vbase + (size_t)pr * row_stride + NT * c);
+        decode_consume_tile<D>(ta, qh, ql, p0, pos, g, m, l, acc);
+        p0 += 32;
+        if (p0 >= c1) {
+            break;
         }
-
-        // ---- S^T = K Q^T ----
-        f32x4 sacc[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            sacc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                sacc[h] = mfma16x16x32(kf[h][kk], qh[kk], sacc[h]);
-                sacc[h] = mfma16x16x32(kf[h][kk], ql[kk], sacc[h]);
-            }
+        if (p0 + 32 < c1) {
+            decode_load_tile<D>(ta, kbase, vbase, row_stride, p0 + 32, last, g, c);
         }
-
-        // ---- online softmax (per head = per lane column c) ----
-        float sv[8];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int p = p0 + 16 * (j >> 2) + 4 * g + (j & 3);
-            const float x = sacc[j >> 2][j & 3];
-            sv[j] = p <= pos ? x : -INFINITY;
-            mx = fmaxf(mx, sv[j]);
-        }
-        mx = wave_xor_max16_32(mx);
-        const float m_new = fmaxf(m, mx);
-        const float alpha = fast_exp2(m - m_new);
-        m = m_new;
-        f16x8 ph, pl;
-        float psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float p = fast_exp2(sv[j] - m_new);
-            psum += p;
-            f16 hi, lo;
-            split_f16(p, hi, lo);
-            ph[j] = hi;
-            pl[j] = lo;
-        }
-        l = l * alpha + psum;
-
-        // ---- O^T = alpha*O^T + V^T P^T ----
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            f16x8 va;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                va[j] = vr[j][t];
-            }
-            acc[t] = acc[t] * alpha;
-            acc[t] = mfma16x16x32(va, ph, acc[t]);
-            acc[t] = mfma16x16x32(va, pl, acc[t]);
+        decode_consume_tile<D>(tb, qh, ql, p0, pos, g, m, l, acc);
+        p0 += 32;
+        if (p0 >= c1) {
+            break;
         }
     }
 
     l = wave_xor_sum16_32(l);
-
-    // ---- merge the 4 waves of this chunk in LDS, write one partial ----
-    __shared__ float sm_m[kWaves][16];
-    __shared__ float sm_l[kWaves][16];
-    __shared__ float sm_o[kWaves][16][D + 4];
-    if (g == 0) {
-        sm_m[wave][c] = m;
-        sm_l[wave][c] = l;
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    if (c < a.group) {
+        const size_t pidx = ((size_t)sl * a.heads + (size_t)kvh * a.group + c) * a.max_chunks + chunk_id;
+        float *po = a.part_o + pidx * D + 4 * NT * g;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            sm_o[wave][c][NT * (4 * g + r) + t] = acc[t][r];
-        }
-    }
-    __syncthreads();
-
-    const int n_items = a.group * D;
-    for (int item = threadIdx.x; item < n_items; item += blockDim.x) {
-        const int hh = item / D;
-        const int dd = item - hh * D;
-        float M = sm_m[0][hh];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) {
-            M = fmaxf(M, sm_m[w][hh]);
+            for (int t = 0; t < NT; t += 4) {
+                float4 v;
+                v.x = acc[t][r];
+                v.y = acc[t + 1][r];
+                v.z = acc[t + 2][r];
+                v.w = acc[t + 3][r];
+                *reinterpret_cast<float4 *>(po + NT * r + t) = v;
+            }
         }
-        float L = 0.0f;
-        float O = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float wt = fast_exp2(sm_m[w][hh] - M);  // exp2(-inf) = 0 for idle waves
-            L += sm_l[w][hh] * wt;
-            O += sm_o[w][hh][dd] * wt;
-        }
-        const size_t pidx = ((size_t)sl * a.heads + (size_t)kvh * a.group + hh) * a.max_chunks + chunk_id;
-        a.part_o[pidx * D + dd] = O;
-        if (dd == 0) {
-            a.part_ml[pidx * 2] = M;
-            a.part_ml[pidx * 2 + 1] = L;
+        if (g == 0) {
+            a.part_ml[pidx * 2] = m;
+            a.part_ml[pidx * 2 + 1] = l;
         }
     }
 }
@@ -392,8 +410,8 @@ te_status check_decode_args(const size_t *positions, size_t position, size_t seq
         return TE_STATUS_INVALID_ARGUMENT;
     }
     if (seqs > TE_HIP_MAX_SEQS || (head_dim != 64 && head_dim != 128) || heads / kv_heads > 16 ||
-        seqs * layers > 65535 || context_tokens > (1u << 30) || kv_heads > 65535) {
-        return TE_STATUS_UNSUPPORTED;
+        seqs * layers > 65535 || kv_heads > 65535 || context_tokens * kv_heads * head_dim >= ((size_t)1 << 31)) {
+        return TE_STATUS_UNSUPPORTED;  // per-(seq, layer) cache offsets are 32-bit in the kernel
     }
     if (!valid_positions(positions, position, seqs, context_tokens, max_position)) {
         return TE_STATUS_INVALID_ARGUMENT;
@@ -405,30 +423,53 @@ te_status check_decode_args(const size_t *positions, size_t position, size_t seq
 
 namespace te_hip {
 
-DecodeGeometry decode_geometry(size_t seqs, size_t layers, size_t max_position, size_t kv_heads) {
-    // Aim for ~8 workgroups per CU over the whole launch (256 CUs): enough to
-    // fill the machine and balance ragged sequences, few enough that the
-    // partials stay a small fraction of the KV bytes.  TE_HIP_DECODE_CHUNK
-    // (a multiple of 128) overrides the choice.
+int device_compute_units() {
+    static const int cus = [] {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+            prop.multiProcessorCount > 0) {
+            return prop.multiProcessorCount;
+        }
+        (void)hipGetLastError();
+        return 256;  // MI355X
+    }();
+    return cus;
+}
+
+DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
+                               size_t kv_heads) {
+    // One launch should give every resident wave slot about one chunk: the
+    // chunk is the total number of 32-position tiles over all (seq, layer,
+    // kv_head) streams divided by the slot count (CUs x kWavesPerCU), at least
+    // two tiles so the prefetch pipeline has work.  Balancing on the total
+    // rather than the longest sequence keeps ragged batches even.
+    // TE_HIP_DECODE_CHUNK (a multiple of 32) overrides the choice.
     DecodeGeometry g;
-    const size_t n = max_position + 1;
-    const size_t streams = seqs * layers * kv_heads;
-    size_t chunk = kMinChunk;
-    while (chunk < 2048 && streams * ((n + chunk * 2 - 1) / (chunk * 2)) >= 2048) {
-        chunk *= 2;
+    size_t max_n = 0, total_tiles = 0;
+    for (size_t s = 0; s < seqs; ++s) {
+        const size_t n = (positions != nullptr ? positions[s] : position) + 1;
+        max_n = n > max_n ? n : max_n;
+        total_tiles += layers * kv_heads * ((n + kTile - 1) / kTile);
     }
+    const size_t slots = (size_t)device_compute_units() * kWavesPerCU;
+    size_t tiles = (total_tiles + slots - 1) / slots;
+    if (tiles < 2) {
+        tiles = 2;
+    }
+    size_t chunk = tiles * kTile;
     const char *env = getenv("TE_HIP_DECODE_CHUNK");
     if (env != nullptr) {
         const long v = strtol(env, nullptr, 10);
-        if (v >= kMinChunk && v % kMinChunk == 0 && v <= (1 << 20)) {
+        if (v >= kTile && v % kTile == 0 && v <= (1 << 24)) {
             chunk = (size_t)v;
         }
     }
-    while ((n + chunk - 1) / chunk > (size_t)kMaxCombineChunks) {
+    while ((max_n + chunk - 1) / chunk > (size_t)kMaxCombineChunks) {
         chunk *= 2;
     }
     g.chunk = (int)chunk;
-    g.max_chunks = (int)((n + chunk - 1) / chunk);
+    g.max_chunks = (int)((max_n + chunk - 1) / chunk);
     return g;
 }
 
@@ -466,12 +507,13 @@ te_status launch_decode_f32(const float *query, const float *key_cache, const fl
 
 }  // namespace te_hip
 
-extern "C" size_t te_hip_attention_decode_workspace_bytes(size_t seqs, size_t layers, size_t max_position,
-                                                          size_t heads, size_t kv_heads, size_t head_dim) {
-    if (seqs == 0 || layers == 0 || heads == 0 || kv_heads == 0 || head_dim == 0) {
+extern "C" size_t te_hip_attention_decode_workspace_bytes(const size_t *positions, size_t position, size_t seqs,
+                                                          size_t layers, size_t heads, size_t kv_heads,
+                                                          size_t head_dim) {
+    if (seqs == 0 || seqs > TE_HIP_MAX_SEQS || layers == 0 || heads == 0 || kv_heads == 0 || head_dim == 0) {
         return 0;
     }
-    const te_hip::DecodeGeometry g = te_hip::decode_geometry(seqs, layers, max_position, kv_heads);
+    const te_hip::DecodeGeometry g = te_hip::decode_geometry(positions, position, seqs, layers, kv_heads);
     return te_hip::decode_workspace_bytes(g, seqs, layers, heads, head_dim);
 }
 
@@ -490,7 +532,7 @@ extern "C" te_status te_hip_attention_decode_splitk_f16(
     if (st != TE_STATUS_OK) {
         return st;
     }
-    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(seqs, layers, max_position, kv_heads);
+    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(positions, position, seqs, layers, kv_heads);
     if (workspace_bytes < te_hip::decode_workspace_bytes(geo, seqs, layers, heads, head_dim)) {
         return TE_STATUS_INVALID_ARGUMENT;
     }
@@ -515,9 +557,9 @@ extern "C" te_status te_hip_attention_decode_splitk_f16(
     const dim3 grid((unsigned)geo.max_chunks, (unsigned)kv_heads, (unsigned)(seqs * layers));
     hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
-        decode_splitk_f16_kernel<128><<<grid, 256, 0, strm>>>(a);
+        decode_splitk_f16_kernel<128><<<grid, 64, 0, strm>>>(a);
     } else {
-        decode_splitk_f16_kernel<64><<<grid, 256, 0, strm>>>(a);
+        decode_splitk_f16_kernel<64><<<grid, 64, 0, strm>>>(a);
     }
     return te_hip::launch_status();
 }
@@ -529,13 +571,19 @@ extern "C" te_status te_hip_attention_decode_combine(
     if (out == nullptr || workspace == nullptr) {
         return TE_STATUS_INVALID_ARGUMENT;
     }
+    // The combine reads no cache: validate against the smallest cache the
+    // positions could belong to.
     size_t max_position = 0;
-    te_status st = check_decode_args(positions, position, seqs, layers, (size_t)1 << 30, heads, kv_heads,
+    for (size_t s = 0; s < seqs && s < TE_HIP_MAX_SEQS; ++s) {
+        const size_t p = positions != nullptr ? positions[s] : position;
+        max_position = p > max_position ? p : max_position;
+    }
+    te_status st = check_decode_args(positions, position, seqs, layers, max_position + 1, heads, kv_heads,
                                      head_dim, &max_position);
     if (st != TE_STATUS_OK) {
         return st;
     }
-    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(seqs, layers, max_position, kv_heads);
+    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(positions, position, seqs, layers, kv_heads);
     if (workspace_bytes < te_hip::decode_workspace_bytes(geo, seqs, layers, heads, head_dim)) {
         return TE_STATUS_INVALID_ARGUMENT;
     }

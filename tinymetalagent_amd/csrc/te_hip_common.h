@@ -64,11 +64,12 @@ inline te_status launch_status() {
 // Decode split-K geometry, shared by the split-K and combine launches and the
 // workspace-size query so all three agree.
 struct DecodeGeometry {
-    int chunk;       // cache positions per workgroup (multiple of 128)
+    int chunk;       // cache positions per workgroup (multiple of 32)
     int max_chunks;  // chunks of the longest sequence
 };
 
-DecodeGeometry decode_geometry(size_t seqs, size_t layers, size_t max_position, size_t kv_heads);
+DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
+                               size_t kv_heads);
 
 size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layers, size_t heads, size_t head_dim);
 

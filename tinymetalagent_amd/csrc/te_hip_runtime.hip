@@ -305,13 +305,8 @@ extern "C" te_status te_hip_attention_decode_f16(
         return TE_STATUS_INVALID_ARGUMENT;
     }
     if (workspace == nullptr) {
-        size_t max_position = 0;
-        for (size_t s = 0; s < seqs && s < TE_HIP_MAX_SEQS; ++s) {
-            const size_t p = positions != nullptr ? positions[s] : position;
-            max_position = p > max_position ? p : max_position;
-        }
         const size_t need =
-            te_hip_attention_decode_workspace_bytes(seqs, layers, max_position, heads, kv_heads, head_dim);
+            te_hip_attention_decode_workspace_bytes(positions, position, seqs, layers, heads, kv_heads, head_dim);
         if (need == 0) {
             return TE_STATUS_INVALID_ARGUMENT;
         }

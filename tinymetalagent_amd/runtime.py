@@ -173,7 +173,7 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_hip_rope_table_f32", [_vp, _vp, _sz, _sz, ctypes.c_float])
     _sig(lib, "te_hip_rope_kv_append_f16",
          [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _szp, _sz, _sz, _sz, _sz, _sz, _vp])
-    _sig(lib, "te_hip_attention_decode_workspace_bytes", [_sz, _sz, _sz, _sz, _sz, _sz], _sz)
+    _sig(lib, "te_hip_attention_decode_workspace_bytes", [_szp, _sz, _sz, _sz, _sz, _sz, _sz], _sz)
     _sig(lib, "te_hip_attention_decode_f16",
          [_vp, _vp, _vp, _szp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _vp])
     _sig(lib, "te_hip_attention_decode_splitk_f16",
