@@ -74,51 +74,71 @@ struct VRow<64> {
     typedef f16x4 type;
 };
 
+// A 32-position tile of one KV head as loaded from HBM.  Both K and V are read
+// the same way: each load instruction covers 4 cache rows, 16 lanes x NT
+// halves per row (a whole D*2-byte head row, contiguous), non-temporal since
+// the stream is read once.
+//   k[j]: row 4j + g,           dims NT*c .. NT*c + NT-1  (row-major staging)
+//   v[j]: row kmap(g, j),       dims NT*c .. NT*c + NT-1  (PV A-operand order)
 template <int D>
 struct DecodeTile {
-    f16x8 k[2][D / 32];
+    typename VRow<D>::type k[8];
     typename VRow<D>::type v[8];
+};
+
+// LDS staging of the K tile, transposed into the QK^T A-operand layout:
+// 32 rows of D halves padded by 8 halves (16 bytes), which makes the
+// 16-row x 16-byte operand reads bank-conflict free.
+template <int D>
+struct KStage {
+    static constexpr int kPitch = D + 8;
+    f16 rows[32 * kPitch];
 };
 
 template <int D>
 __device__ __forceinline__ void decode_load_tile(DecodeTile<D> &t, const f16 *kbase, const f16 *vbase,
                                                  int row_stride, int p0, int last, int g, int c) {
     constexpr int NT = D / 16;
-    constexpr int KK = D / 32;
     typedef typename VRow<D>::type vrow_t;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int pr = min(p0 + 16 * h + c, last);
-        const f16 *kr = kbase + pr * row_stride;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            t.k[h][kk] = *reinterpret_cast<const f16x8 *>(kr + 8 * g + 32 * kk);
-        }
-    }
-#pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int pr = min(p0 + 16 * (j >> 2) + 4 * g + (j & 3), last);
-        t.v[j] = *reinterpret_cast<const vrow_t *>(vbase + pr * row_stride + NT * c);
+        const int kr = min(p0 + 4 * j + g, last);
+        t.k[j] = __builtin_nontemporal_load(reinterpret_cast<const vrow_t *>(kbase + kr * row_stride + NT * c));
+        const int vr = min(p0 + 16 * (j >> 2) + 4 * g + (j & 3), last);
+        t.v[j] = __builtin_nontemporal_load(reinterpret_cast<const vrow_t *>(vbase + vr * row_stride + NT * c));
     }
 }
 
 // One 32-position step of the online softmax + both MFMA products.
 template <int D>
-__device__ __forceinline__ void decode_consume_tile(const DecodeTile<D> &t, const f16x8 (&qh)[D / 32],
-                                                    const f16x8 (&ql)[D / 32], int p0, int pos, int g,
-                                                    float &m, float &l, f32x4 (&acc)[D / 16]) {
+__device__ __forceinline__ void decode_consume_tile(const DecodeTile<D> &t, KStage<D> &ks,
+                                                    const f16x8 (&qh)[D / 32], const f16x8 (&ql)[D / 32], int p0,
+                                                    int pos, int g, int c, float &m, float &l,
+                                                    f32x4 (&acc)[D / 16]) {
     constexpr int NT = D / 16;
     constexpr int KK = D / 32;
+    constexpr int P = KStage<D>::kPitch;
+    typedef typename VRow<D>::type vrow_t;
+    // K tile -> LDS (row-major) -> A operand rows 16h + c, dims 8g + 32kk.
+    // One wave per workgroup: the LDS unit serves this wave's writes before its
+    // later reads; the barrier only orders the compiler.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        *reinterpret_cast<vrow_t *>(&ks.rows[(4 * j + g) * P + NT * c]) = t.k[j];
+    }
+    __syncthreads();
     f32x4 sacc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         sacc[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            sacc[h] = mfma16x16x32(t.k[h][kk], qh[kk], sacc[h]);
-            sacc[h] = mfma16x16x32(t.k[h][kk], ql[kk], sacc[h]);
+            const f16x8 ka = *reinterpret_cast<const f16x8 *>(&ks.rows[(16 * h + c) * P + 8 * g + 32 * kk]);
+            sacc[h] = mfma16x16x32(ka, qh[kk], sacc[h]);
+            sacc[h] = mfma16x16x32(ka, ql[kk], sacc[h]);
         }
     }
+    __syncthreads();  // the next tile's staging writes come after these reads
     float sv[8];
     float mx = -INFINITY;
 #pragma unroll
@@ -221,12 +241,13 @@ __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) 
 
     // Two register tiles, ping-pong: the loads of step n+1 are in flight while
     // step n is consumed.  Every branch below is wave-uniform.
+    __shared__ KStage<D> kstage;
     int p0 = c0;
     for (;;) {
         if (p0 + 32 < c1) {
             decode_load_tile<D>(tb, kbase, vbase, row_stride, p0 + 32, last, g, c);
         }
-        decode_consume_tile<D>(ta, qh, ql, p0, pos, g, m, l, acc);
+        decode_consume_tile<D>(ta, kstage, qh, ql, p0, pos, g, c, m, l, acc);
         p0 += 32;
         if (p0 >= c1) {
             break;
@@ -234,7 +255,7 @@ __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) 
         if (p0 + 32 < c1) {
             decode_load_tile<D>(ta, kbase, vbase, row_stride, p0 + 32, last, g, c);
         }
-        decode_consume_tile<D>(tb, qh, ql, p0, pos, g, m, l, acc);
+        decode_consume_tile<D>(tb, kstage, qh, ql, p0, pos, g, c, m, l, acc);
         p0 += 32;
         if (p0 >= c1) {
             break;
