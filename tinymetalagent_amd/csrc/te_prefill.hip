@@ -5,10 +5,15 @@
 // `key <= base + row` of te_attention_flash_mma_t_f32_kernel
 // (metal_kernels.metal.inc:2767-2775), which also defines chunked prefill.
 //
-// One workgroup = 4 waves = BM (128) query rows of one head; each wave owns
-// 32 rows (two 16-row MFMA column blocks).  K/V blocks of BN (64) positions of
-// the head's KV group are staged through LDS, double-buffered: the global loads
-// of block n+1 are in flight while block n is consumed, one barrier per block.
+// Work decomposition.  Query rows are cut into tiles of BM (128) rows.  One
+// workgroup = 8 waves = the PAIR of tiles (n-1-i, i) of one head: waves 0-3 own
+// the long tile n-1-i, waves 4-7 the short tile i (32 rows per wave, two
+// 16-row MFMA column blocks).  The short tile's key range is a prefix of the
+// long tile's, so one LDS stream of K/V blocks serves both; every workgroup
+// does the same causal work ((n+1) tiles' worth of blocks), so a launch of
+// n/2 x heads workgroups finishes evenly.  K/V blocks of BN (64) positions of
+// the head's KV group are double-buffered in LDS: the global loads of block
+// b+1 are in flight while block b is consumed, one barrier per block.
 //
 //   S^T[64 keys x 32 rows] = K[64 x D] . Q^T[D x 32]            fp16 MFMA 16x16x32
 //   O^T[D x 32 rows]      += V^T[D x 64] . P^T[64 x 32]         fp16 MFMA 16x16x32
@@ -18,12 +23,17 @@
 // in registers.  V^T's A operand is read from row-major LDS as 16-byte rows of
 // NT consecutive dims for 8 keys and transposed in registers (output tile t
 // covers dims {NT*m + t}), so O^T comes out with each lane holding 4*NT
-// contiguous dims of one row.  Softmax statistics are fp32, base-2, per row.
+// contiguous dims of one row.
+//
+// Softmax: fp32, base 2.  The row maximum is taken on raw scores; p =
+// exp2(s*qscale - m_ref) with one FMA.  m_ref is only raised (and O, l
+// rescaled) when a row's maximum exceeds it by more than 2^kLazyLog2, so the
+// rescale is skipped in almost every block; O/l is exact for any m_ref >= the
+// true maximum minus kLazyLog2 (P stays <= 2^kLazyLog2, fine for fp16).
 // Q and P are single fp16 operands (the rotated q is already fp16 here).
 //
 // Work per (seq, layer): 2*heads*D*sum_t(base+t+1) MACs (QK^T + PV); the
-// roofline unit is that count x2 FLOP.  Query tiles are issued heaviest-first
-// (largest row index first) to balance the causal triangle.
+// roofline unit is that count x2 FLOP.
 #include "te_hip_common.h"
 
 #include <math.h>
@@ -32,6 +42,9 @@ namespace {
 
 constexpr int BM = 128;
 constexpr int BN = 64;
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr float kLazyLog2 = 8.0f;
 
 struct PrefillArgs {
     const f16 *q;
@@ -61,28 +74,30 @@ struct VRow<64> {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
     constexpr int KK = D / 32;          // QK^T K-steps
     constexpr int NT = D / 16;          // O^T output tiles
     constexpr int LROW = D + 8;         // LDS row pitch in halves (16-byte pad)
     constexpr int CPR = D / 8;          // 16-byte chunks per cache row
-    constexpr int LOADS = BN * CPR / 256;
+    constexpr int LOADS = BN * CPR / kThreads;
     typedef typename VRow<D>::type vrow_t;
 
     __shared__ __attribute__((aligned(16))) f16 lds_k[2][BN * LROW];
     __shared__ __attribute__((aligned(16))) f16 lds_v[2][BN * LROW];
 
-    const int qt = a.n_qtiles - 1 - (int)blockIdx.x;
+    const int pair = blockIdx.x;
     const int h = blockIdx.y;
     const int sl = blockIdx.z;
     const int kvh = h / a.group;
-    const int r0 = qt * BM;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int g = lane >> 4;
     const int c = lane & 15;
-    const int wr0 = r0 + 32 * wave;  // first row of this wave
+    const int long_tile = a.n_qtiles - 1 - pair;
+    const int qt = wave < 4 ? long_tile : pair;
+    const bool tile_ok = wave < 4 || pair != long_tile;  // odd tile count: the middle tile has no partner
+    const int wr0 = qt * BM + 32 * (wave & 3);          // first row of this wave
 
     const size_t row_stride = (size_t)a.kv_heads * D;
     const size_t cache_base = (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
@@ -94,7 +109,7 @@ __global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) 
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         const int row = wr0 + 16 * nb + c;
-        const bool ok = row < a.tokens;
+        const bool ok = tile_ok && row < a.tokens;
         const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
@@ -106,15 +121,15 @@ __global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) 
         }
     }
 
-    const int last_row = min(r0 + BM, a.tokens) - 1;
-    const int kmax = a.base + last_row;  // last key any row of this tile sees
+    const int last_row = min(long_tile * BM + BM, a.tokens) - 1;
+    const int kmax = a.base + last_row;  // last key any row of the pair sees
     const int n_blocks = kmax / BN + 1;
 
     f16x8 kreg[LOADS], vreg[LOADS];
     auto gload = [&](int blk) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + kThreads * i;
             const int key = min(blk * BN + idx / CPR, kmax);
             const int col = (idx % CPR) * 8;
             kreg[i] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)key * row_stride + col);
@@ -124,14 +139,14 @@ __global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) 
     auto lstore = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + kThreads * i;
             const int off = (idx / CPR) * LROW + (idx % CPR) * 8;
             *reinterpret_cast<f16x8 *>(&lds_k[buf][off]) = kreg[i];
             *reinterpret_cast<f16x8 *>(&lds_v[buf][off]) = vreg[i];
         }
     };
 
-    float m[2] = {-INFINITY, -INFINITY};
+    float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
     float l[2] = {0.0f, 0.0f};
     f32x4 o[2][NT];
 #pragma unroll
@@ -143,9 +158,10 @@ __global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) 
     }
 
     const int wave_last_row = min(wr0 + 31, a.tokens - 1);
-    const bool wave_active = wr0 < a.tokens;
+    const bool wave_active = tile_ok && wr0 < a.tokens;
     const int wave_max_pos = a.base + wave_last_row;
     const int wave_min_pos = a.base + wr0;
+    const float qs = a.qscale;
 
     gload(0);
     lstore(0);
@@ -173,42 +189,43 @@ __global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) 
                     s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
                 }
             }
-            // ---- scale, causal mask, online softmax per row ----
+            // ---- causal mask, lazy online softmax per row ----
             const bool need_mask = kb0 + BN - 1 > wave_min_pos;
             f16x8 pb[2][2];  // [k-step][row block]
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 const int rowpos = a.base + wr0 + 16 * nb + c;
-                float x[16];
                 float mx = -INFINITY;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        float v = s[i][nb][r] * a.qscale;
                         if (need_mask && kb0 + 16 * i + 4 * g + r > rowpos) {
-                            v = -INFINITY;
+                            s[i][nb][r] = -INFINITY;
                         }
-                        x[4 * i + r] = v;
-                        mx = fmaxf(mx, v);
+                        mx = fmaxf(mx, s[i][nb][r]);
                     }
                 }
-                mx = wave_xor_max16_32(mx);
-                const float m_new = fmaxf(m[nb], mx);
-                const float alpha = fast_exp2(m[nb] - m_new);
-                m[nb] = m_new;
+                mx = wave_xor_max16_32(mx) * qs;
+                if (__any(mx > mref[nb] + kLazyLog2)) {
+                    const float nref = fmaxf(mref[nb], mx);
+                    const float alpha = fast_exp2(mref[nb] - nref);
+                    mref[nb] = nref;
+                    l[nb] *= alpha;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        o[nb][t] = o[nb][t] * alpha;
+                    }
+                }
+                const float nm = -mref[nb];
                 float psum = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = fast_exp2(x[e] - m_new);
+                    const float p = fast_exp2(fmaf(s[e >> 2][nb][e & 3], qs, nm));
                     psum += p;
                     pb[e >> 3][nb][e & 7] = (f16)p;
                 }
-                l[nb] = l[nb] * alpha + psum;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    o[nb][t] = o[nb][t] * alpha;
-                }
+                l[nb] += psum;
             }
             // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -242,7 +259,7 @@ __global__ __launch_bounds__(256) void prefill_causal_f16_kernel(PrefillArgs a) 
     for (int nb = 0; nb < 2; ++nb) {
         const float lsum = wave_xor_sum16_32(l[nb]);
         const int row = wr0 + 16 * nb + c;
-        if (row < a.tokens) {
+        if (wave_active && row < a.tokens) {
             const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
             float *orow = a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
 #pragma unroll
@@ -294,12 +311,13 @@ extern "C" te_status te_hip_attention_prefill_f16(
     a.group = (int)(heads / kv_heads);
     a.n_qtiles = (int)((tokens + BM - 1) / BM);
     a.qscale = TE_LOG2E / sqrtf((float)head_dim);
-    const dim3 grid((unsigned)a.n_qtiles, (unsigned)heads, (unsigned)(seqs * layers));
+    const int n_pairs = (a.n_qtiles + 1) / 2;
+    const dim3 grid((unsigned)n_pairs, (unsigned)heads, (unsigned)(seqs * layers));
     hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
-        prefill_causal_f16_kernel<128><<<grid, 256, 0, strm>>>(a);
+        prefill_causal_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
     } else {
-        prefill_causal_f16_kernel<64><<<grid, 256, 0, strm>>>(a);
+        prefill_causal_f16_kernel<64><<<grid, kThreads, 0, strm>>>(a);
     }
     return te_hip::launch_status();
 }
