@@ -66,7 +66,48 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--quick", action="store_true", help="headline decode + prefill only")
+    p.add_argument("--profile", action="store_true",
+                   help="run a fixed kernel sequence for rocprofv3 (5x decode step at 3B/8K/36 layers, "
+                        "5x prefill at L=4096, 3x a 512 MiB device copy for counter calibration) and exit")
     return p.parse_args()
+
+
+def profile_sequence(torch, A) -> None:
+    """Fixed launch sequence profiled by the commands recorded under profiles/.
+    The device copy (torch's elementwise copy kernel, 512 MiB read + 512 MiB
+    written) calibrates FETCH_SIZE / WRITE_SIZE against known bytes."""
+    dev = "cuda"
+    H, KV, D, LAYERS, L = 16, 2, 128, 36, 8192
+    g = torch.Generator(device=dev).manual_seed(42)
+    kc = torch.randn((1, LAYERS, L + 1, KV, D), generator=g, device=dev).half()
+    vc = torch.randn((1, LAYERS, L + 1, KV, D), generator=g, device=dev).half()
+    q = torch.randn((1, LAYERS, 1, H, D), generator=g, device=dev) / math.sqrt(D)
+    k = torch.randn((1, LAYERS, 1, KV, D), generator=g, device=dev)
+    v = torch.randn((1, LAYERS, 1, KV, D), generator=g, device=dev)
+    cos, sin = A.rope_table(L + 1, D, THETA)
+    ws = A.decode_workspace(1, LAYERS, H, KV, D, position=L)
+    out = torch.empty((1, LAYERS, H, D), dtype=torch.float32, device=dev)
+    for _ in range(5):
+        A.rope_kv_append(q, k, v, cos, sin, kc, vc, base_position=L)
+        A.attention_decode(q, kc, vc, position=L, out=out, workspace=ws, stage="splitk")
+        A.attention_decode(q, kc, vc, position=L, out=out, workspace=ws, stage="combine")
+    torch.cuda.synchronize()
+    del kc, vc
+    Lp = 4096
+    qh = torch.randn((1, 1, Lp, H, D), generator=g, device=dev).half()
+    kp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
+    vp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
+    po = torch.empty((1, 1, Lp, H, D), dtype=torch.float32, device=dev)
+    for _ in range(5):
+        A.attention_prefill(qh, kp, vp, out=po)
+    torch.cuda.synchronize()
+    src = torch.ones(128 << 20, dtype=torch.float32, device=dev)  # 512 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("profile sequence done: decode step x5 (3B, L=8192, 36 layers), prefill x5 (L=4096), "
+          "copy x3 (536870912 B read + written)")
 
 
 class Timer:
@@ -251,6 +292,9 @@ def main():
     if not R.hip_available():
         raise SystemExit("bench.py: libtinyengine.so found no gfx950 GPU")
     name, cus = R.device_info()
+    if args.profile:
+        profile_sequence(torch, A)
+        return
     timer = Timer(torch)
     H, KV, D, LAYERS = 16, 2, 128, 36
     K = args.steps

@@ -32,6 +32,17 @@ __device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ds_read_b64_tr_b16 (gfx950): every lane passes an LDS address of 4 halves;
+// within each 16-lane group, lane i receives element i%4 of the 4 halves read
+// by source lanes 4j + i/4, j = 0..3 (checked on the device: a 16 x 4 block of
+// halves comes back transposed).
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (s16x4 __attribute__((address_space(3))) *)(const_cast<f16 *>(p)));
+    return __builtin_bit_cast(f16x4, v);
+}
+
 __device__ __forceinline__ float wave_xor_max16_32(float v) {
     v = fmaxf(v, __shfl_xor(v, 16, 64));
     v = fmaxf(v, __shfl_xor(v, 32, 64));

@@ -9,10 +9,10 @@
 // workgroup = 8 waves = the PAIR of tiles (n-1-i, i) of one head: waves 0-3 own
 // the long tile n-1-i, waves 4-7 the short tile i (32 rows per wave, two
 // 16-row MFMA column blocks).  The short tile's key range is a prefix of the
-// long tile's, so one LDS stream of K/V blocks serves both; every workgroup
-// does the same causal work ((n+1) tiles' worth of blocks), so a launch of
-// n/2 x heads workgroups finishes evenly.  K/V blocks of BN (64) positions of
-// the head's KV group are double-buffered in LDS: the global loads of block
+// long tile's, so one LDS stream of K/V blocks serves both (256 rows per
+// staged block while both are active), and every workgroup does the same
+// causal work ((n+1) tiles' worth of blocks).  K/V blocks of BN (64) positions
+// of the head's KV group are double-buffered in LDS: the global loads of block
 // b+1 are in flight while block b is consumed, one barrier per block.
 //
 //   S^T[64 keys x 32 rows] = K[64 x D] . Q^T[D x 32]            fp16 MFMA 16x16x32
@@ -20,10 +20,9 @@
 //
 // The S^T result layout (lane = row c, keys 4g+r) is the P^T B-operand layout
 // of the PV MFMA (keys kmap(g,j) = 16(j/4)+4g+(j%4) per 32-key step), so P stays
-// in registers.  V^T's A operand is read from row-major LDS as 16-byte rows of
-// NT consecutive dims for 8 keys and transposed in registers (output tile t
-// covers dims {NT*m + t}), so O^T comes out with each lane holding 4*NT
-// contiguous dims of one row.
+// in registers.  V^T's A operand comes from row-major LDS through the gfx950
+// transposing read ds_read_b64_tr_b16 (two per 16-dim output tile), so O^T
+// comes out with each lane holding dims 16t + 4g + {0..3} of one row.
 //
 // Softmax: fp32, base 2.  The row maximum is taken on raw scores; p =
 // exp2(s*qscale - m_ref) with one FMA.  m_ref is only raised (and O, l
@@ -63,27 +62,17 @@ struct PrefillArgs {
 };
 
 template <int D>
-struct VRow;
-template <>
-struct VRow<128> {
-    typedef f16x8 type;
-};
-template <>
-struct VRow<64> {
-    typedef f16x4 type;
-};
-
-template <int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
     constexpr int KK = D / 32;          // QK^T K-steps
     constexpr int NT = D / 16;          // O^T output tiles
-    constexpr int LROW = D + 8;         // LDS row pitch in halves (16-byte pad)
+    constexpr int LROW = D + 8;         // K row pitch in halves: 16-row x 16-byte reads conflict-free
+    constexpr int VROW = D + 16;        // V row pitch in halves: transposing 8-byte reads conflict-free
     constexpr int CPR = D / 8;          // 16-byte chunks per cache row
     constexpr int LOADS = BN * CPR / kThreads;
-    typedef typename VRow<D>::type vrow_t;
+    constexpr int KSTAGE = BN * LROW;
+    constexpr int VSTAGE = BN * VROW;
 
-    __shared__ __attribute__((aligned(16))) f16 lds_k[2][BN * LROW];
-    __shared__ __attribute__((aligned(16))) f16 lds_v[2][BN * LROW];
+    __shared__ __attribute__((aligned(16))) f16 lds[2 * (KSTAGE + VSTAGE)];
 
     const int pair = blockIdx.x;
     const int h = blockIdx.y;
@@ -137,12 +126,15 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         }
     };
     auto lstore = [&](int buf) {
+        f16 *lk = lds + buf * (KSTAGE + VSTAGE);
+        f16 *lv = lk + KSTAGE;
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const int idx = tid + kThreads * i;
-            const int off = (idx / CPR) * LROW + (idx % CPR) * 8;
-            *reinterpret_cast<f16x8 *>(&lds_k[buf][off]) = kreg[i];
-            *reinterpret_cast<f16x8 *>(&lds_v[buf][off]) = vreg[i];
+            const int row = idx / CPR;
+            const int col = (idx % CPR) * 8;
+            *reinterpret_cast<f16x8 *>(&lk[row * LROW + col]) = kreg[i];
+            *reinterpret_cast<f16x8 *>(&lv[row * VROW + col]) = vreg[i];
         }
     };
 
@@ -163,10 +155,94 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     const int wave_min_pos = a.base + wr0;
     const float qs = a.qscale;
 
+    // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv.
+    auto compute = [&](int kb0, const f16 *lk, const f16 *lv) {
+        // ---- S^T = K Q^T ----
+        f32x4 s[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                const f16x8 ka = *reinterpret_cast<const f16x8 *>(lk + (16 * i + c) * LROW + 8 * g + 32 * kk);
+                s[i][0] = mfma16x16x32(ka, qop[0][kk], s[i][0]);
+                s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
+            }
+        }
+        // ---- causal mask (diagonal blocks only), lazy online softmax per row ----
+        if (kb0 + BN - 1 > wave_min_pos) {
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const int lim = a.base + wr0 + 16 * nb + c - kb0 - 4 * g;  // mask key offsets > lim
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (16 * i + r > lim) {
+                            s[i][nb][r] = -INFINITY;
+                        }
+                    }
+                }
+            }
+        }
+        f16x8 pb[2][2];  // [k-step][row block]
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    mx = fmaxf(mx, s[i][nb][r]);
+                }
+            }
+            mx = wave_xor_max16_32(mx) * qs;
+            if (__any(mx > mref[nb] + kLazyLog2)) {
+                // A row that has seen no unmasked key keeps m_ref = -inf (its l
+                // and O are still zero); the key-split waves can meet such rows.
+                const float nref = fmaxf(mref[nb], mx);
+                const float alpha = mref[nb] == -INFINITY ? 0.0f : fast_exp2(mref[nb] - nref);
+                mref[nb] = nref;
+                l[nb] *= alpha;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    o[nb][t] = o[nb][t] * alpha;
+                }
+            }
+            const float nm = mref[nb] == -INFINITY ? 0.0f : -mref[nb];  // all-masked row: p = exp2(-inf) = 0
+            float psum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = fast_exp2(fmaf(s[e >> 2][nb][e & 3], qs, nm));
+                psum += p;
+                pb[e >> 3][nb][e & 7] = (f16)p;
+            }
+            l[nb] += psum;
+        }
+        // ---- O^T += V^T P^T ----
+        // V^T A operand of tile t (dims 16t + m) straight from row-major LDS
+        // with the transposing read: source lane k of each 16-lane group reads
+        // 4 dims (16t + 4(k%4) ..) of key kmap(g, k/4) (+16 rows for the second
+        // half), and lane c receives dim 16t + c of all 8 keys.
+        const f16 *vsrc = lv + (4 * g + (c >> 2)) * VROW + 4 * (c & 3);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const f16 *p0 = vsrc + (32 * ks) * VROW + 16 * t;
+                const f16x4 lo = lds_read_tr16(p0);
+                const f16x4 hi = lds_read_tr16(p0 + 16 * VROW);
+                const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
+                o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
+            }
+        }
+    };
+
     gload(0);
     lstore(0);
     __syncthreads();
-
     for (int blk = 0; blk < n_blocks; ++blk) {
         const int buf = blk & 1;
         if (blk + 1 < n_blocks) {
@@ -174,79 +250,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         }
         const int kb0 = blk * BN;
         if (wave_active && kb0 <= wave_max_pos) {
-            const f16 *lk = lds_k[buf];
-            const f16 *lv = lds_v[buf];
-            // ---- S^T = K Q^T ----
-            f32x4 s[4][2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(lk + (16 * i + c) * LROW + 8 * g + 32 * kk);
-                    s[i][0] = mfma16x16x32(ka, qop[0][kk], s[i][0]);
-                    s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
-                }
-            }
-            // ---- causal mask, lazy online softmax per row ----
-            const bool need_mask = kb0 + BN - 1 > wave_min_pos;
-            f16x8 pb[2][2];  // [k-step][row block]
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const int rowpos = a.base + wr0 + 16 * nb + c;
-                float mx = -INFINITY;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (need_mask && kb0 + 16 * i + 4 * g + r > rowpos) {
-                            s[i][nb][r] = -INFINITY;
-                        }
-                        mx = fmaxf(mx, s[i][nb][r]);
-                    }
-                }
-                mx = wave_xor_max16_32(mx) * qs;
-                if (__any(mx > mref[nb] + kLazyLog2)) {
-                    const float nref = fmaxf(mref[nb], mx);
-                    const float alpha = fast_exp2(mref[nb] - nref);
-                    mref[nb] = nref;
-                    l[nb] *= alpha;
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        o[nb][t] = o[nb][t] * alpha;
-                    }
-                }
-                const float nm = -mref[nb];
-                float psum = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float p = fast_exp2(fmaf(s[e >> 2][nb][e & 3], qs, nm));
-                    psum += p;
-                    pb[e >> 3][nb][e & 7] = (f16)p;
-                }
-                l[nb] += psum;
-            }
-            // ---- O^T += V^T P^T ----
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                vrow_t vr[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int key = 32 * ks + 16 * (j >> 2) + 4 * g + (j & 3);
-                    vr[j] = *reinterpret_cast<const vrow_t *>(lv + key * LROW + NT * c);
-                }
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    f16x8 va;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        va[j] = vr[j][t];
-                    }
-                    o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
-                    o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
-                }
-            }
+            const f16 *lk = lds + buf * (KSTAGE + VSTAGE);
+            compute(kb0, lk, lk + KSTAGE);
         }
         if (blk + 1 < n_blocks) {
             lstore(buf ^ 1);
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         __syncthreads();
     }
 
-    // ---- epilogue: normalise and store rows (dims 4NT*g .. 4NT*g + 4NT - 1) ----
+    // ---- epilogue: normalise and store rows (lane holds dims 16t + 4g + r) ----
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         const float lsum = wave_xor_sum16_32(l[nb]);
@@ -263,16 +268,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
             float *orow = a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-#pragma unroll
-                for (int t = 0; t < NT; t += 4) {
-                    float4 v;
-                    v.x = o[nb][t][r] * inv;
-                    v.y = o[nb][t + 1][r] * inv;
-                    v.z = o[nb][t + 2][r] * inv;
-                    v.w = o[nb][t + 3][r] * inv;
-                    *reinterpret_cast<float4 *>(orow + NT * (4 * g + r) + t) = v;
-                }
+            for (int t = 0; t < NT; ++t) {
+                float4 v;
+                v.x = o[nb][t][0] * inv;
+                v.y = o[nb][t][1] * inv;
+                v.z = o[nb][t][2] * inv;
+                v.w = o[nb][t][3] * inv;
+                *reinterpret_cast<float4 *>(orow + 16 * t + 4 * g) = v;
             }
         }
     }
