@@ -278,6 +278,21 @@ def r(x, n=4):
     return round(x, n)
 
 
+def measured_traffic(ctx_len: int):
+    """HBM bytes per split-K launch measured with rocprofv3 counters for the
+    headline workload (recorded in profiles/), or None for other contexts."""
+    import re
+
+    if ctx_len != 8192:
+        return None
+    path = ROOT / "profiles" / "decode_splitk_3b_ctx8k.md"
+    try:
+        m = re.search(r"^TRAFFIC_BYTES_PER_LAUNCH=(\d+)$", path.read_text(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -330,7 +345,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": r(dec["splitk_gbs"] / HBM_PEAK_GBS),
-            "traffic": None,
+            "traffic": measured_traffic(args.ctx),
+            "traffic_source": "profiles/decode_splitk_3b_ctx8k.md: rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE, "
+                              "calibrated on a 512 MiB device copy",
             "bytes_per_launch": dec["bytes_per_step"],
             "launch_us": r(dec["splitk_ms"] * 1e3, 2),
         },
