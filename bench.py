@@ -5,10 +5,12 @@
 Headline workload (the config the metric is quoted
 on): Qwen2.5-Coder-3B-shaped decode attention across all 36 layers at context
 8K -- 16 query heads, 2 KV heads, head_dim 128, batch 1, fp16 KV cache.  One
-step = one decode token through the attention step of all 36 layers:
-    RoPE(q, k) + fp16 append of k/v at position L   (1 launch, all layers)
-    split-K GQA decode attention over positions 0..L (1 launch, all layers)
+step = one decode token through the attention step of all 36 layers, fused:
+    split-K GQA decode attention over positions 0..L, whose prologue applies
+    RoPE to q and appends the RoPE'd fp16 k/v at position L (1 launch, all layers)
     combine of the split-K partials                  (1 launch)
+The unfused sequence (separate RoPE+append launch, split-K, combine) is timed
+too and reported as decode.step_3launch_us.
 Inputs are synthetic (torch N(0,1) on the GPU, seed 42; Q scaled by 1/sqrt(128))
 and resident in HBM before timing.  Distinct KV caches (>= 1.2 GB in total) are
 rotated across steps so the 256 MB MALL cannot serve a step from the previous
@@ -47,9 +49,11 @@ THETA = 1e6
 
 
 def decode_bytes(heads: int, kv: int, d: int, positions) -> int:
-    """Algorithmic HBM bytes of decode attention summed over (seq, layer) units:
-    fp16 K+V over positions 0..L plus fp32 q in and o out."""
-    return sum(2 * (p + 1) * kv * d * 2 + heads * d * (4 + 4) for p in positions)
+    """Algorithmic HBM bytes of one fused decode step summed over (seq, layer)
+    units: fp16 K+V over positions 0..L (the appended slot included), fp32 q in
+    and o out, the new token's fp32 k/v in and fp16 k/v out, one fp32 cos/sin row."""
+    return sum(2 * (p + 1) * kv * d * 2 + heads * d * (4 + 4) + kv * d * (2 * 4 + 2 * 2) + d * 4
+               for p in positions)
 
 
 def prefill_flops(heads: int, d: int, tokens: int, base: int = 0) -> float:
@@ -88,9 +92,7 @@ def profile_sequence(torch, A) -> None:
     ws = A.decode_workspace(1, LAYERS, H, KV, D, position=L)
     out = torch.empty((1, LAYERS, H, D), dtype=torch.float32, device=dev)
     for _ in range(5):
-        A.rope_kv_append(q, k, v, cos, sin, kc, vc, base_position=L)
-        A.attention_decode(q, kc, vc, position=L, out=out, workspace=ws, stage="splitk")
-        A.attention_decode(q, kc, vc, position=L, out=out, workspace=ws, stage="combine")
+        A.decode_step(q, k, v, cos, sin, kc, vc, position=L, out=out, workspace=ws)
     torch.cuda.synchronize()
     del kc, vc
     Lp = 4096
@@ -215,19 +217,29 @@ def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_s
         q, k, v, kc, vc = sets[i % ns]
         A.attention_decode(q, kc, vc, positions=positions, out=out, workspace=ws, stage="combine")
 
-    def step(i):
+    def step_3launch(i):
         rope(i)
         splitk(i)
         combine(i)
 
-    step_ms = timer(step, reps)
+    def step_fused(i):
+        q, k, v, kc, vc = sets[i % ns]
+        A.decode_step(q, k, v, cos, sin, kc, vc, positions=positions, out=out, workspace=ws)
+
+    def step_splitk(i):
+        q, k, v, kc, vc = sets[i % ns]
+        A.decode_step(q, k, v, cos, sin, kc, vc, positions=positions, workspace=ws, stage="splitk")
+
+    step_ms = timer(step_fused, reps)
+    fsplitk_ms = timer(step_splitk, reps)
+    step3_ms = timer(step_3launch, reps)
     splitk_ms = timer(splitk, reps)
     rope_ms = timer(rope, reps)
     combine_ms = timer(combine, reps)
     nbytes = decode_bytes(heads, kv, d, [p for p in positions for _ in range(layers)])
-    res = dict(step_ms=step_ms, splitk_ms=splitk_ms, rope_append_ms=rope_ms, combine_ms=combine_ms,
-               bytes_per_step=nbytes, splitk_gbs=nbytes / (splitk_ms * 1e-3) / 1e9,
-               step_gbs=nbytes / (step_ms * 1e-3) / 1e9)
+    res = dict(step_ms=step_ms, step3_ms=step3_ms, fsplitk_ms=fsplitk_ms, splitk_ms=splitk_ms,
+               rope_append_ms=rope_ms, combine_ms=combine_ms, bytes_per_step=nbytes,
+               splitk_gbs=nbytes / (fsplitk_ms * 1e-3) / 1e9, step_gbs=nbytes / (step_ms * 1e-3) / 1e9)
     if keep_cpu_sample:
         q, k, v, kc, vc = sets[0]
         res["cpu_sample"] = (q[0, 0, 0].reshape(-1).float().cpu().numpy().copy(),
@@ -333,14 +345,15 @@ def main():
         "dtype": "f16",
         "data": "synthetic",
         "config": {
-            "workload": f"Qwen2.5-3B decode attention step (RoPE + fp16 KV append + split-K GQA attention), "
+            "workload": f"Qwen2.5-3B decode attention step (fused RoPE + fp16 KV append + split-K GQA attention, "
+                        f"then combine), "
                         f"all {LAYERS} layers per step, ctx {args.ctx} (BASELINE configs[1])",
             "heads": H, "kv_heads": KV, "head_dim": D, "layers": LAYERS, "context": args.ctx, "batch": 1,
             "kv_cache": "fp16", "softmax_accumulate": "f32", "device": name, "compute_units": cus,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_splitk_f16_kernel<128>",
+            "kernel": "decode_splitk_f16_kernel<128, FUSED=true>",
             "achieved": round(dec["splitk_gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -349,10 +362,12 @@ def main():
             "traffic_source": "profiles/decode_splitk_3b_ctx8k.md: rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE, "
                               "calibrated on a 512 MiB device copy",
             "bytes_per_launch": dec["bytes_per_step"],
-            "launch_us": r(dec["splitk_ms"] * 1e3, 2),
+            "launch_us": r(dec["fsplitk_ms"] * 1e3, 2),
         },
         "decode": {
             "step_us": r(dec["step_ms"] * 1e3, 2),
+            "fused_splitk_us": r(dec["fsplitk_ms"] * 1e3, 2),
+            "step_3launch_us": r(dec["step3_ms"] * 1e3, 2),
             "rope_append_us": r(dec["rope_append_ms"] * 1e3, 2),
             "splitk_us": r(dec["splitk_ms"] * 1e3, 2),
             "combine_us": r(dec["combine_ms"] * 1e3, 2),

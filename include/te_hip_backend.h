@@ -140,6 +140,43 @@ TE_API te_status te_hip_attention_decode_combine(
     float *out, const void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Fused decode step: te_hip_rope_kv_append_f16 (tokens = 1) followed by
+ * te_hip_attention_decode_f16, as one split-K launch plus the combine launch.
+ * Same semantics as that pair for the cache and the output, with one
+ * difference: `query`, `k_new` and `v_new` are inputs only (not rotated or
+ * bias-added in place) -- the rotated q lives in registers, and the rotated k /
+ * biased v go straight to the fp16 cache slot of each sequence's position.
+ * The append happens inside the workgroup that owns that position, before it
+ * reads it.  Layouts: query [seqs][layers][heads][head_dim], k_new / v_new
+ * [seqs][layers][kv_heads][head_dim]; other arguments as above.  The
+ * workspace (required, no NULL form) is sized by
+ * te_hip_attention_decode_workspace_bytes.
+ */
+TE_API te_status te_hip_attention_decode_step_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The split-K launch of te_hip_attention_decode_step_f16 alone (append +
+ * partials into the workspace), for timing; te_hip_attention_decode_combine with
+ * the same workspace completes the step.  Repeating it is idempotent: the
+ * appended slot is rewritten with the same values. */
+TE_API te_status te_hip_attention_decode_step_splitk_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Batched-prefill causal attention over the fp16 cache.  Replaces the CPU
  * per-token loop (qwen.c:810-824: row t = decode at position t) and the MMA
  * prefill kernel te_attention_flash_mma_t_f32_kernel

@@ -115,6 +115,14 @@ def test_backend_guard_conventions(lib):
                                                   None) == 1  # position >= context
     assert lib.te_hip_attention_decode_splitk_f16(buf, buf, buf, None, 0, 1, 1, 8, 2, 1, 128, ws, 16,
                                                   None) == 1  # workspace too small
+    for fn in (lib.te_hip_attention_decode_step_f16, lib.te_hip_attention_decode_step_splitk_f16):
+        tail = (buf, ws, 1 << 20, None) if fn is lib.te_hip_attention_decode_step_f16 else (ws, 1 << 20, None)
+        assert fn(buf, None, buf, None, None, None, buf, buf, buf, buf, None, 0, 1, 1, 8, 2, 1, 128,
+                  *tail) == 1  # no k_new
+        assert fn(buf, buf, buf, None, None, None, buf, buf, buf, buf, None, 0, 1, 1, 8, 2, 1, 96,
+                  *tail) == 3  # head_dim 96
+        assert fn(buf, buf, buf, None, None, None, buf, buf, buf, buf, None, 8, 1, 1, 8, 2, 1, 128,
+                  *tail) == 1  # position >= context
     assert lib.te_hip_attention_prefill_f16(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None) in ok
     assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 6, 8, 2, 1, 128, buf, None) == 1
     assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None) == 3

@@ -392,3 +392,57 @@ def test_prefill_full_size_4k_rows(oracle_mod):
         dec = A.attention_decode(q[:, :, t].contiguous(), kc, vc, position=t)
         e = float((dec[0, 0] - out[0, 0, t]).abs().max())
         assert e <= TOL, (t, e)
+
+
+# ------------------------------------------------------------- fused step ---
+
+@pytest.mark.parametrize("h,kv,d,layers,positions,bias", [
+    (16, 2, 128, 2, [0, 63, 64, 1000], True),
+    (14, 2, 64, 3, [512], False),
+    (28, 4, 128, 1, [4095, 17, 2048], True),
+])
+def test_decode_step_fused_vs_oracle(oracle_mod, h, kv, d, layers, positions, bias):
+    """te_hip_attention_decode_step_f16 == rope_kv_append + decode, per the oracle:
+    cache slots bit-exact, outputs within the bar, inputs left untouched."""
+    seqs = len(positions)
+    ctx = max(positions) + 2
+    tag = f"step{h}{kv}{d}{layers}{seqs}"
+    q = S.normal(26, tag + "q", (seqs, layers, 1, h, d), 1 / math.sqrt(d))
+    k = S.normal(26, tag + "k", (seqs, layers, 1, kv, d))
+    v = S.normal(26, tag + "v", (seqs, layers, 1, kv, d))
+    qb = S.normal(26, tag + "qb", (layers, h * d), 0.1) if bias else None
+    kb = S.normal(26, tag + "kb", (layers, kv * d), 0.1) if bias else None
+    vb = S.normal(26, tag + "vb", (layers, kv * d), 0.1) if bias else None
+    kc0 = S.to_f16_bits(S.normal(26, tag + "kc", (seqs, layers, ctx, kv, d)))
+    vc0 = S.to_f16_bits(S.normal(26, tag + "vc", (seqs, layers, ctx, kv, d)))
+    cos, sin = oracle_mod.rope_table(ctx, d, 1e6)
+    # oracle: append then decode
+    q_o, k_o, v_o, kc_o, vc_o = q.copy(), k.copy(), v.copy(), kc0.copy(), vc0.copy()
+    oracle_mod.rope_kv_append_f16(q_o, k_o, v_o, qb, kb, vb, cos, sin, kc_o, vc_o, seqs, layers, 1, positions, 0, ctx,
+                                  h, kv, d)
+    want = oracle_mod.attention_decode_f16kv(q_o[:, :, 0].copy(), kc_o, vc_o, positions, 0, seqs, layers, ctx, h, kv, d)
+    # GPU fused step
+    tq, tk, tv = to_dev(q), to_dev(k), to_dev(v)
+    dcos, dsin = A.rope_table(ctx, d, 1e6)
+    kc, vc = f16_dev(kc0), f16_dev(vc0)
+    out = A.decode_step(tq, tk, tv, dcos, dsin, kc, vc, positions=positions,
+                        q_bias=to_dev(qb) if bias else None, k_bias=to_dev(kb) if bias else None,
+                        v_bias=to_dev(vb) if bias else None)
+    torch.cuda.synchronize()
+    assert np.array_equal(f16_host_bits(kc), kc_o) and np.array_equal(f16_host_bits(vc), vc_o)
+    assert np.array_equal(tq.cpu().numpy(), q) and np.array_equal(tk.cpu().numpy(), k)
+    err = maxabs(out.cpu().numpy(), want)
+    print(f"fused decode step H{h} KV{kv} d{d} layers{layers} positions={positions}: max abs err {err:.3e}")
+    assert err <= TOL
+    # the fused split-K launch alone, repeated (idempotent append), then the
+    # combine: the same output bits and the same cache
+    ws = A.decode_workspace(seqs, layers, h, kv, d, positions=positions)
+    out2 = torch.empty_like(out)
+    for _ in range(2):
+        A.decode_step(tq, tk, tv, dcos, dsin, kc, vc, positions=positions,
+                      q_bias=to_dev(qb) if bias else None, k_bias=to_dev(kb) if bias else None,
+                      v_bias=to_dev(vb) if bias else None, workspace=ws, stage="splitk")
+    A.attention_decode(tq, kc, vc, positions=positions, out=out2, workspace=ws, stage="combine")
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)
+    assert np.array_equal(f16_host_bits(kc), kc_o) and np.array_equal(f16_host_bits(vc), vc_o)

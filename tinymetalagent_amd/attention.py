@@ -127,6 +127,42 @@ def attention_decode(query, key_cache, value_cache, *, position: int = 0, positi
     return out
 
 
+def decode_step(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_cache, *, position: int = 0,
+                positions: Sequence[int] | None = None, q_bias=None, k_bias=None, v_bias=None,
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None, stream=None,
+                stage: str = "both") -> torch.Tensor:
+    """Fused decode step: bias + RoPE + fp16 append of the new token and split-K
+    attention, one split-K launch + the combine.  query/k_new/v_new are read only.
+
+    stage: "both", or "splitk" for the fused split-K launch alone (partials into
+    the workspace; attention_decode(..., stage="combine") finishes the step)."""
+    q = query if query.dim() == 4 else query.reshape(query.shape[0], query.shape[1], query.shape[-2],
+                                                     query.shape[-1])
+    seqs, layers, heads, head_dim = q.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    for t, dt, n in ((q, torch.float32, "query"), (k_new, torch.float32, "k_new"), (v_new, torch.float32, "v_new"),
+                     (key_cache, torch.float16, "key_cache"), (value_cache, torch.float16, "value_cache")):
+        _dtype(t, dt, n)
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        workspace = decode_workspace(seqs, layers, heads, kv_heads, head_dim, position=position, positions=positions,
+                                     device=q.device)
+    lib = load_library()
+    args = (_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(rope_cos),
+            _ptr(rope_sin), _ptr(key_cache), _ptr(value_cache), _positions(positions), position, seqs, layers, ctx,
+            heads, kv_heads, head_dim)
+    if stage == "both":
+        check(lib.te_hip_attention_decode_step_f16(*args, _ptr(out), _ptr(workspace), workspace.numel(),
+                                                   _stream(stream)))
+    elif stage == "splitk":
+        check(lib.te_hip_attention_decode_step_splitk_f16(*args, _ptr(workspace), workspace.numel(),
+                                                          _stream(stream)))
+    else:
+        raise ValueError(stage)
+    return out
+
+
 def attention_prefill(q_half, key_cache, value_cache, *, base_position: int = 0, out: torch.Tensor | None = None,
                       stream=None) -> torch.Tensor:
     """Causal prefill: q_half fp16 [seqs, layers, tokens, heads, d] -> out fp32, same shape."""

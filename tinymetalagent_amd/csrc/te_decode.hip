@@ -18,17 +18,19 @@
 // q and P are fp32 values split into hi+lo fp16 pairs (two MFMAs each), so the
 // only rounding relative to an fp32 computation is the fp16 cache itself.
 // Lane mapping (l = lane, g = l/16, c = l%16):
-//   K operand : lane reads K[p0 + 16h + c][8g + 32kk .. +7]          (16 B loads)
-//   V operand : lane reads V[p0 + kmap(g,j)][NT*c .. NT*c+NT-1]       (16 B loads,
-//               a 256-byte cache row per 16 lanes), kmap(g,j) = 16(j/4)+4g+(j%4),
-//               then an in-register 8 x NT transpose gives the A operand of
-//               output tile t = dims {NT*m + t}.
+//   K, V loads: each instruction reads 4 whole cache rows (16 lanes x 16 B =
+//               one 256-byte row for D = 128), non-temporal:
+//               K rows p0 + 4j + g, V rows p0 + kmap(g,j),
+//               kmap(g,j) = 16(j/4)+4g+(j%4), dims NT*c .. NT*c+NT-1.
+//   K operand : the K tile is written row-major to a padded LDS stage and read
+//               back as A-operand rows 16h + c, dims 8g + 32kk.
+//   V operand : an in-register 8 x NT transpose of the V rows gives the A
+//               operand of output tile t = dims {NT*m + t}.
 //   S^T result: lane holds head c at positions 4g+r (+16h) -- exactly the
 //               P^T B-operand layout of the PV MFMA for kmap, so P never moves.
 //   O^T result: lane holds head c, dims 4NT*g .. 4NT*g + 4NT - 1, written
 //               straight to the partial with 16-byte stores.
-// K and V go from HBM straight into MFMA operand registers (no LDS), and the
-// next tile's loads are issued before the current tile is consumed (two
+// The next tile's loads are issued before the current tile is consumed (two
 // register tiles, 32 KB in flight per wave).  The chunk length is chosen from
 // the total tile count so one launch gives every wave slot about one chunk,
 // which also balances ragged sequence lengths.
@@ -52,6 +54,17 @@ struct DecodeArgs {
     const f16 *value_cache;
     float *part_o;   // [SL][heads][max_chunks][D]
     float *part_ml;  // [SL][heads][max_chunks][2]  (m in log2 units, l)
+    // Fused decode step only (bias + RoPE of q and of the new k, fp16 append of
+    // the new k/v at `positions[s]`); unused by the plain split-K kernel.
+    const float *k_new;   // [SL][kv_heads][D]
+    const float *v_new;   // [SL][kv_heads][D]
+    const float *q_bias;  // [layers][heads*D] or null
+    const float *k_bias;  // [layers][kv_heads*D] or null
+    const float *v_bias;  // [layers][kv_heads*D] or null
+    const float *rope_cos;
+    const float *rope_sin;
+    f16 *key_cache_w;
+    f16 *value_cache_w;
     int layers;
     int ctx;
     int heads;
@@ -177,7 +190,85 @@ __device__ __forceinline__ void decode_consume_tile(const DecodeTile<D> &t, KSta
     }
 }
 
+// Fused decode step, in the workgroup whose chunk holds the query position:
+// bias + RoPE of the new token's k and bias of its v for this KV head, rounded
+// to fp16 into the cache slot, with the same operation order as
+// rope_kv_append_kernel (FP contraction off), then fenced so the tile loads
+// that follow see it.  Only this workgroup reads that position.
 template <int D>
+__device__ __forceinline__ void decode_append_new_token(const DecodeArgs &a, int sl, int layer, int kvh, int pos,
+                                                        int lane) {
+#pragma clang fp contract(off)
+    constexpr int HALF = D / 2;
+    const int kv_dim = a.kv_heads * D;
+    const float *kn = a.k_new + ((size_t)sl * a.kv_heads + kvh) * D;
+    const float *vn = a.v_new + ((size_t)sl * a.kv_heads + kvh) * D;
+    const size_t slot = ((size_t)sl * a.ctx + pos) * kv_dim + (size_t)kvh * D;
+    const float *cos_row = a.rope_cos + (size_t)pos * HALF;
+    const float *sin_row = a.rope_sin + (size_t)pos * HALF;
+    for (int i = lane; i < HALF; i += 64) {
+        float x0 = kn[i];
+        float x1 = kn[i + HALF];
+        if (a.k_bias != nullptr) {
+            x0 = x0 + a.k_bias[(size_t)layer * kv_dim + kvh * D + i];
+            x1 = x1 + a.k_bias[(size_t)layer * kv_dim + kvh * D + i + HALF];
+        }
+        const float cs = cos_row[i];
+        const float sn = sin_row[i];
+        a.key_cache_w[slot + i] = (f16)(x0 * cs - x1 * sn);
+        a.key_cache_w[slot + i + HALF] = (f16)(x1 * cs + x0 * sn);
+    }
+    for (int i = lane; i < D; i += 64) {
+        float x = vn[i];
+        if (a.v_bias != nullptr) {
+            x = x + a.v_bias[(size_t)layer * kv_dim + kvh * D + i];
+        }
+        a.value_cache_w[slot + i] = (f16)x;
+    }
+    // The workgroup is this one wave and the only reader of the slot, so a
+    // workgroup-scope release/acquire orders the stores before the tile loads;
+    // an agent-scope fence would also write back and invalidate the XCD's L2.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Bias + RoPE of this lane's q values in registers (fused step).  Lane (g, c)
+// holds dims 8g + 32kk + j of head c; the rotation partner of dim d < D/2 is
+// d + D/2, held by the same lane at kk + KK/2.
+template <int D>
+__device__ __forceinline__ void decode_rope_q(const DecodeArgs &a, float (&xs)[D / 32][8], int layer, int head,
+                                              int pos, int g) {
+#pragma clang fp contract(off)
+    constexpr int KK = D / 32;
+    constexpr int HALF = D / 2;
+    if (a.q_bias != nullptr) {
+        const float *qb = a.q_bias + ((size_t)layer * a.heads + head) * D;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xs[kk][j] = xs[kk][j] + qb[8 * g + 32 * kk + j];
+            }
+        }
+    }
+    const float *cos_row = a.rope_cos + (size_t)pos * HALF;
+    const float *sin_row = a.rope_sin + (size_t)pos * HALF;
+#pragma unroll
+    for (int kk = 0; kk < KK / 2; ++kk) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = 8 * g + 32 * kk + j;
+            const float cs = cos_row[i];
+            const float sn = sin_row[i];
+            const float x0 = xs[kk][j];
+            const float x1 = xs[kk + KK / 2][j];
+            xs[kk][j] = x0 * cs - x1 * sn;
+            xs[kk + KK / 2][j] = x1 * cs + x0 * sn;
+        }
+    }
+}
+
+template <int D, bool FUSED>
 __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) {
     constexpr int NT = D / 16;  // output tiles over head_dim; also dims per lane in V loads
     constexpr int KK = D / 32;  // MFMA K-steps over head_dim for QK^T
@@ -202,6 +293,10 @@ __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) 
     const f16 *kbase = a.key_cache + sl_base;
     const f16 *vbase = a.value_cache + sl_base;
 
+    if (FUSED && c1 == pos + 1) {
+        decode_append_new_token<D>(a, sl, sl - s * a.layers, kvh, pos, lane);
+    }
+
     DecodeTile<D> ta, tb;
     decode_load_tile<D>(ta, kbase, vbase, row_stride, c0, last, g, c);
 
@@ -209,20 +304,30 @@ __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) 
     f16x8 qh[KK], ql[KK];
     {
         const bool head_ok = c < a.group;
-        const float *qrow = a.query + ((size_t)sl * a.heads + (size_t)kvh * a.group + (head_ok ? c : 0)) * D;
-        float4 xq[2 * KK];
+        const int head = kvh * a.group + (head_ok ? c : 0);
+        const float *qrow = a.query + ((size_t)sl * a.heads + head) * D;
+        float xs[KK][8];
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            xq[2 * kk] = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk);
-            xq[2 * kk + 1] = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk + 4);
+            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk + 4);
+            xs[kk][0] = x0.x;
+            xs[kk][1] = x0.y;
+            xs[kk][2] = x0.z;
+            xs[kk][3] = x0.w;
+            xs[kk][4] = x1.x;
+            xs[kk][5] = x1.y;
+            xs[kk][6] = x1.z;
+            xs[kk][7] = x1.w;
+        }
+        if (FUSED) {
+            decode_rope_q<D>(a, xs, sl - s * a.layers, head, pos, g);
         }
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            const float xs[8] = {xq[2 * kk].x, xq[2 * kk].y, xq[2 * kk].z, xq[2 * kk].w,
-                                 xq[2 * kk + 1].x, xq[2 * kk + 1].y, xq[2 * kk + 1].z, xq[2 * kk + 1].w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float x = head_ok ? xs[j] * a.qscale : 0.0f;
+                const float x = head_ok ? xs[kk][j] * a.qscale : 0.0f;
                 f16 hi, lo;
                 split_f16(x, hi, lo);
                 qh[kk][j] = hi;
@@ -296,6 +401,74 @@ struct CombineArgs {
     int max_chunks;
     int positions[TE_HIP_MAX_SEQS];
 };
+
+// Merge of two softmax partials (m, l, o) in the log2 domain; a side whose max
+// equals the merged max keeps weight 1, so -inf maxima never form -inf - -inf.
+__device__ __forceinline__ void merge_partial(float &m, float &l, float4 &o, float mi, float li, float4 oi) {
+    const float mn = fmaxf(m, mi);
+    const float sa = m == mn ? 1.0f : fast_exp2(m - mn);
+    const float sb = mi == mn ? 1.0f : fast_exp2(mi - mn);
+    m = mn;
+    l = l * sa + li * sb;
+    o.x = o.x * sa + oi.x * sb;
+    o.y = o.y * sa + oi.y * sb;
+    o.z = o.z * sa + oi.z * sb;
+    o.w = o.w * sa + oi.w * sb;
+}
+
+// Combine for the split-K f16 path (head_dim D in {64, 128}), one 256-thread
+// workgroup per (head, seq*layer): thread (grp, col) owns the float4 column col
+// of the head and the chunks grp, grp + G, ...; it merges them online, so all of
+// its partial loads are independent and in flight together.  The G group
+// results are then merged through LDS.  Same result as decode_combine_kernel
+// up to fp32 rounding of the rescale factors.
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(CombineArgs a) {
+    constexpr int COLS = D / 4;
+    constexpr int G = 256 / COLS;
+    const int h = blockIdx.x;
+    const int sl = blockIdx.y;
+    const int s = sl / a.layers;
+    const int n_chunks = (a.positions[s] + a.chunk) / a.chunk;  // ceil((pos+1)/chunk)
+    const size_t base = ((size_t)sl * a.heads + h) * a.max_chunks;
+    const int tid = threadIdx.x;
+    const int col = tid % COLS;
+    const int grp = tid / COLS;
+    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + base;
+    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + base * D) + col;
+
+    float m = -INFINITY;
+    float l = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+    for (int i = grp; i < n_chunks; i += G) {
+        const float2 mli = ml[i];
+        const float4 oi = po[(size_t)i * COLS];
+        merge_partial(m, l, o, mli.x, mli.y, oi);
+    }
+
+    __shared__ float4 o_s[G][COLS];
+    __shared__ float m_s[G];
+    __shared__ float l_s[G];
+    o_s[grp][col] = o;
+    if (col == 0) {
+        m_s[grp] = m;
+        l_s[grp] = l;
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+        for (int k = 1; k < G; ++k) {
+            merge_partial(m, l, o, m_s[k], l_s[k], o_s[k][col]);
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 1.0f;
+        o.x *= inv;
+        o.y *= inv;
+        o.z *= inv;
+        o.w *= inv;
+        reinterpret_cast<float4 *>(a.out + ((size_t)sl * a.heads + h) * D)[col] = o;
+    }
+}
 
 // One workgroup per (head, seq*layer): out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c.
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
@@ -538,12 +711,14 @@ extern "C" size_t te_hip_attention_decode_workspace_bytes(const size_t *position
     return te_hip::decode_workspace_bytes(g, seqs, layers, heads, head_dim);
 }
 
-extern "C" te_status te_hip_attention_decode_splitk_f16(
-    const float *query, const uint16_t *key_cache, const uint16_t *value_cache,
-    const size_t *positions, size_t position,
-    size_t seqs, size_t layers, size_t context_tokens,
-    size_t heads, size_t kv_heads, size_t head_dim,
-    void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+
+// Shared by the plain split-K entry point and the fused decode step; `fused`
+// carries the new token (k_new/v_new non-null) and the RoPE tables.
+te_status launch_splitk(const DecodeArgs &fused, bool is_fused, const float *query, const uint16_t *key_cache,
+                        const uint16_t *value_cache, const size_t *positions, size_t position, size_t seqs,
+                        size_t layers, size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+                        void *workspace, size_t workspace_bytes, void *stream) {
     if (query == nullptr || key_cache == nullptr || value_cache == nullptr || workspace == nullptr) {
         return TE_STATUS_INVALID_ARGUMENT;
     }
@@ -557,7 +732,7 @@ extern "C" te_status te_hip_attention_decode_splitk_f16(
     if (workspace_bytes < te_hip::decode_workspace_bytes(geo, seqs, layers, heads, head_dim)) {
         return TE_STATUS_INVALID_ARGUMENT;
     }
-    DecodeArgs a;
+    DecodeArgs a = fused;
     a.query = query;
     a.key_cache = reinterpret_cast<const f16 *>(key_cache);
     a.value_cache = reinterpret_cast<const f16 *>(value_cache);
@@ -578,11 +753,80 @@ extern "C" te_status te_hip_attention_decode_splitk_f16(
     const dim3 grid((unsigned)geo.max_chunks, (unsigned)kv_heads, (unsigned)(seqs * layers));
     hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
-        decode_splitk_f16_kernel<128><<<grid, 64, 0, strm>>>(a);
+        if (is_fused) {
+            decode_splitk_f16_kernel<128, true><<<grid, 64, 0, strm>>>(a);
+        } else {
+            decode_splitk_f16_kernel<128, false><<<grid, 64, 0, strm>>>(a);
+        }
     } else {
-        decode_splitk_f16_kernel<64><<<grid, 64, 0, strm>>>(a);
+        if (is_fused) {
+            decode_splitk_f16_kernel<64, true><<<grid, 64, 0, strm>>>(a);
+        } else {
+            decode_splitk_f16_kernel<64, false><<<grid, 64, 0, strm>>>(a);
+        }
     }
     return te_hip::launch_status();
+}
+
+}  // namespace
+
+extern "C" te_status te_hip_attention_decode_splitk_f16(
+    const float *query, const uint16_t *key_cache, const uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    DecodeArgs none = {};
+    return launch_splitk(none, false, query, key_cache, value_cache, positions, position, seqs, layers,
+                         context_tokens, heads, kv_heads, head_dim, workspace, workspace_bytes, stream);
+}
+
+extern "C" te_status te_hip_attention_decode_step_splitk_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    if (k_new == nullptr || v_new == nullptr || rope_cos == nullptr || rope_sin == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    DecodeArgs f = {};
+    f.k_new = k_new;
+    f.v_new = v_new;
+    f.q_bias = q_bias;
+    f.k_bias = k_bias;
+    f.v_bias = v_bias;
+    f.rope_cos = rope_cos;
+    f.rope_sin = rope_sin;
+    f.key_cache_w = reinterpret_cast<f16 *>(key_cache);
+    f.value_cache_w = reinterpret_cast<f16 *>(value_cache);
+    return launch_splitk(f, true, query, key_cache, value_cache, positions, position, seqs, layers,
+                         context_tokens, heads, kv_heads, head_dim, workspace, workspace_bytes, stream);
+}
+
+extern "C" te_status te_hip_attention_decode_step_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    if (out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_status st = te_hip_attention_decode_step_splitk_f16(
+        query, k_new, v_new, q_bias, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache, positions,
+        position, seqs, layers, context_tokens, heads, kv_heads, head_dim, workspace, workspace_bytes, stream);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    return te_hip_attention_decode_combine(positions, position, seqs, layers, heads, kv_heads, head_dim, out,
+                                           workspace, workspace_bytes, stream);
 }
 
 extern "C" te_status te_hip_attention_decode_combine(
@@ -621,6 +865,11 @@ extern "C" te_status te_hip_attention_decode_combine(
     for (size_t s = 0; s < seqs; ++s) {
         c.positions[s] = (int)(positions != nullptr ? positions[s] : position);
     }
-    decode_combine_kernel<<<dim3((unsigned)heads, (unsigned)(seqs * layers)), 256, 0, te_hip::as_stream(stream)>>>(c);
+    const dim3 grid((unsigned)heads, (unsigned)(seqs * layers));
+    if (head_dim == 128) {
+        decode_merge_kernel<128><<<grid, 256, 0, te_hip::as_stream(stream)>>>(c);
+    } else {
+        decode_merge_kernel<64><<<grid, 256, 0, te_hip::as_stream(stream)>>>(c);
+    }
     return te_hip::launch_status();
 }
