@@ -39,8 +39,8 @@
 
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 64;
+constexpr int BM = 128;   // query rows per tile: 4 row groups of 32
+constexpr int BN = 64;    // keys per block
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr float kLazyLog2 = 8.0f;
@@ -61,18 +61,38 @@ struct PrefillArgs {
     float qscale;  // log2(e)/sqrt(D), applied to the fp32 scores
 };
 
+__device__ __forceinline__ float xor_max_16_32(float v) {
+    // lanes l, l^16, l^32, l^48 hold one row's values: two permlane swaps (VALU, no LDS)
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float xor_sum_16_32(float v) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
-    constexpr int KK = D / 32;          // QK^T K-steps
-    constexpr int NT = D / 16;          // O^T output tiles
-    constexpr int LROW = D + 8;         // K row pitch in halves: 16-row x 16-byte reads conflict-free
-    constexpr int VROW = D + 16;        // V row pitch in halves: transposing 8-byte reads conflict-free
-    constexpr int CPR = D / 8;          // 16-byte chunks per cache row
-    constexpr int LOADS = BN * CPR / kThreads;
-    constexpr int KSTAGE = BN * LROW;
-    constexpr int VSTAGE = BN * VROW;
+    constexpr int KK = D / 32;                      // QK^T K-steps
+    constexpr int NT = D / 16;                      // O^T output tiles
+    constexpr int LROW = D + 8;                     // K row pitch (halves): 16-row x 16-byte reads conflict-free
+    constexpr int VROW = D + 16;                    // V row pitch (halves): transposing 8-byte reads conflict-free
+    constexpr int CPR = D / 8;                      // 16-byte chunks per cache row
+    constexpr int SROWS = 2 * BN;                   // keys staged per step: one block per key half
+    constexpr int LOADS = SROWS * CPR / kThreads;   // 16-byte K (and V) loads per thread per step
+    constexpr int KSTAGE = SROWS * LROW;
+    constexpr int VSTAGE = SROWS * VROW;
+    constexpr int STAGE = KSTAGE + VSTAGE;
+    constexpr int XFER = (4 * NT + 2) * 64;         // floats per wave in the merge exchange
+    static_assert(LOADS * kThreads == SROWS * CPR, "staging loads must tile the step");
+    static_assert(kWaves * XFER * 4 <= 2 * STAGE * 2, "merge exchange must fit in the staging buffers");
 
-    __shared__ __attribute__((aligned(16))) f16 lds[2 * (KSTAGE + VSTAGE)];
+    __shared__ __attribute__((aligned(16))) f16 lds[2 * STAGE];
 
     const int pair = blockIdx.x;
     const int h = blockIdx.y;
@@ -81,52 +101,33 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int half = wave >> 2;  // key half: blocks 2*step + half
     const int g = lane >> 4;
     const int c = lane & 15;
     const int long_tile = a.n_qtiles - 1 - pair;
-    const int qt = wave < 4 ? long_tile : pair;
-    const bool tile_ok = wave < 4 || pair != long_tile;  // odd tile count: the middle tile has no partner
-    const int wr0 = qt * BM + 32 * (wave & 3);          // first row of this wave
+    const int n_tiles_wg = pair == long_tile ? 1 : 2;  // odd tile count: the middle tile has no partner
 
     const size_t row_stride = (size_t)a.kv_heads * D;
     const size_t cache_base = (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
     const f16 *kbase = a.key_cache + cache_base;
     const f16 *vbase = a.value_cache + cache_base;
+    const float qs = a.qscale;
 
-    // Q^T operand for the wave's two 16-row blocks.
-    f16x8 qop[2][KK];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int row = wr0 + 16 * nb + c;
-        const bool ok = tile_ok && row < a.tokens;
-        const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            f16x8 v = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
-            if (!ok) {
-                v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-            qop[nb][kk] = v;
-        }
-    }
-
-    const int last_row = min(long_tile * BM + BM, a.tokens) - 1;
-    const int kmax = a.base + last_row;  // last key any row of the pair sees
-    const int n_blocks = kmax / BN + 1;
+    auto tile_kmax = [&](int qt) { return a.base + min(qt * BM + BM, a.tokens) - 1; };  // last key of a tile
 
     f16x8 kreg[LOADS], vreg[LOADS];
-    auto gload = [&](int blk) {
+    auto gload = [&](int step, int kmax) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const int idx = tid + kThreads * i;
-            const int key = min(blk * BN + idx / CPR, kmax);
+            const int key = min(step * SROWS + idx / CPR, kmax);
             const int col = (idx % CPR) * 8;
             kreg[i] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)key * row_stride + col);
             vreg[i] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)key * row_stride + col);
         }
     };
     auto lstore = [&](int buf) {
-        f16 *lk = lds + buf * (KSTAGE + VSTAGE);
+        f16 *lk = lds + buf * STAGE;
         f16 *lv = lk + KSTAGE;
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
@@ -138,144 +139,216 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         }
     };
 
-    float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
-    float l[2] = {0.0f, 0.0f};
-    f32x4 o[2][NT];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            o[nb][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    }
+    gload(0, tile_kmax(long_tile));
+    for (int ti = 0; ti < n_tiles_wg; ++ti) {
+        const int qt = ti == 0 ? long_tile : pair;
+        const int wr0 = qt * BM + 32 * (wave & 3);  // first row of this wave
+        const int kmax = tile_kmax(qt);
+        const int n_steps = (kmax / BN + 2) / 2;    // ceil(blocks / 2)
 
-    const int wave_last_row = min(wr0 + 31, a.tokens - 1);
-    const bool wave_active = tile_ok && wr0 < a.tokens;
-    const int wave_max_pos = a.base + wave_last_row;
-    const int wave_min_pos = a.base + wr0;
-    const float qs = a.qscale;
-
-    // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv.
-    auto compute = [&](int kb0, const f16 *lk, const f16 *lv) {
-        // ---- S^T = K Q^T ----
-        f32x4 s[4][2];
+        // Q^T operand for the wave's two 16-row blocks.
+        f16x8 qop[2][KK];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int nb = 0; nb < 2; ++nb) {
+            const int row = wr0 + 16 * nb + c;
+            const bool ok = row < a.tokens;
+            const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
-                const f16x8 ka = *reinterpret_cast<const f16x8 *>(lk + (16 * i + c) * LROW + 8 * g + 32 * kk);
-                s[i][0] = mfma16x16x32(ka, qop[0][kk], s[i][0]);
-                s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
+                f16x8 v = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
+                if (!ok) {
+                    v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                }
+                qop[nb][kk] = v;
             }
         }
-        // ---- causal mask (diagonal blocks only), lazy online softmax per row ----
-        if (kb0 + BN - 1 > wave_min_pos) {
+
+        float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
+        float l[2] = {0.0f, 0.0f};               // per-lane partial row sums
+        f32x4 o[2][NT];
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const int lim = a.base + wr0 + 16 * nb + c - kb0 - 4 * g;  // mask key offsets > lim
+        for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+            for (int t = 0; t < NT; ++t) {
+                o[nb][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+        const int wave_last_row = min(wr0 + 31, a.tokens - 1);
+        const bool wave_active = wr0 < a.tokens;
+        const int wave_max_pos = a.base + wave_last_row;
+        const int wave_min_pos = a.base + wr0;
+
+        // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv.
+        auto compute = [&](int kb0, const f16 *lk, const f16 *lv) {
+            // ---- S^T = K Q^T ----
+            f32x4 s[4][2];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (16 * i + r > lim) {
-                            s[i][nb][r] = -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+                s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(lk + (16 * i + c) * LROW + 8 * g + 32 * kk);
+                    s[i][0] = mfma16x16x32(ka, qop[0][kk], s[i][0]);
+                    s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
+                }
+            }
+            // ---- causal mask (diagonal blocks only), lazy online softmax per row ----
+            if (kb0 + BN - 1 > wave_min_pos) {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    const int lim = a.base + wr0 + 16 * nb + c - kb0 - 4 * g;  // mask key offsets > lim
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (16 * i + r > lim) {
+                                s[i][nb][r] = -INFINITY;
+                            }
                         }
                     }
                 }
             }
-        }
-        f16x8 pb[2][2];  // [k-step][row block]
+            f16x8 pb[2][2];  // [k-step][row block]
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            float mx = -INFINITY;
+            for (int nb = 0; nb < 2; ++nb) {
+                float mx = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 4; ++i) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    mx = fmaxf(mx, s[i][nb][r]);
+                    for (int r = 0; r < 4; ++r) {
+                        mx = fmaxf(mx, s[i][nb][r]);
+                    }
                 }
+                mx = xor_max_16_32(mx) * qs;
+                if (__any(mx > mref[nb] + kLazyLog2)) {
+                    // A row that has seen no unmasked key keeps m_ref = -inf (its
+                    // l and O are still zero): a key half can meet such rows.
+                    const float nref = fmaxf(mref[nb], mx);
+                    const float alpha = mref[nb] == -INFINITY ? 0.0f : fast_exp2(mref[nb] - nref);
+                    mref[nb] = nref;
+                    l[nb] *= alpha;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        o[nb][t] = o[nb][t] * alpha;
+                    }
+                }
+                const float nm = mref[nb] == -INFINITY ? 0.0f : -mref[nb];  // all-masked row: p = exp2(-inf) = 0
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    pb[e >> 3][nb][e & 7] = (f16)fast_exp2(fmaf(s[e >> 2][nb][e & 3], qs, nm));
+                }
+                // row sum of the fp16 weights the PV product uses (v_dot2_f32_f16)
+                float psum = l[nb];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        const f16x2 pr = {pb[ks][nb][j], pb[ks][nb][j + 1]};
+                        psum = __builtin_amdgcn_fdot2(pr, f16x2{(f16)1.0f, (f16)1.0f}, psum, false);
+                    }
+                }
+                l[nb] = psum;
             }
-            mx = wave_xor_max16_32(mx) * qs;
-            if (__any(mx > mref[nb] + kLazyLog2)) {
-                // A row that has seen no unmasked key keeps m_ref = -inf (its l
-                // and O are still zero); the key-split waves can meet such rows.
-                const float nref = fmaxf(mref[nb], mx);
-                const float alpha = mref[nb] == -INFINITY ? 0.0f : fast_exp2(mref[nb] - nref);
-                mref[nb] = nref;
-                l[nb] *= alpha;
+            // ---- O^T += V^T P^T ----
+            // V^T A operand of tile t (dims 16t + m) straight from row-major LDS
+            // with the transposing read: source lane k of each 16-lane group
+            // reads 4 dims (16t + 4(k%4) ..) of key kmap(g, k/4) (+16 rows for
+            // the second half), and lane c receives dim 16t + c of all 8 keys.
+            const f16 *vsrc = lv + (4 * g + (c >> 2)) * VROW + 4 * (c & 3);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    o[nb][t] = o[nb][t] * alpha;
+                    const f16 *p0 = vsrc + (32 * ks) * VROW + 16 * t;
+                    const f16x4 lo = lds_read_tr16(p0);
+                    const f16x4 hi = lds_read_tr16(p0 + 16 * VROW);
+                    const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
+                    o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
                 }
             }
-            const float nm = mref[nb] == -INFINITY ? 0.0f : -mref[nb];  // all-masked row: p = exp2(-inf) = 0
-            float psum = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float p = fast_exp2(fmaf(s[e >> 2][nb][e & 3], qs, nm));
-                psum += p;
-                pb[e >> 3][nb][e & 7] = (f16)p;
-            }
-            l[nb] += psum;
+        };
+
+        if (ti == 0) {
+            lstore(0);
+            __syncthreads();
         }
-        // ---- O^T += V^T P^T ----
-        // V^T A operand of tile t (dims 16t + m) straight from row-major LDS
-        // with the transposing read: source lane k of each 16-lane group reads
-        // 4 dims (16t + 4(k%4) ..) of key kmap(g, k/4) (+16 rows for the second
-        // half), and lane c receives dim 16t + c of all 8 keys.
-        const f16 *vsrc = lv + (4 * g + (c >> 2)) * VROW + 4 * (c & 3);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int step = 0; step < n_steps; ++step) {
+            const int buf = step & 1;
+            const bool more = step + 1 < n_steps;
+            if (more) {
+                gload(step + 1, kmax);
+            } else if (ti + 1 < n_tiles_wg) {
+                gload(0, tile_kmax(pair));  // the next tile's first step, in flight across the merge
+            }
+            const int kb0 = (2 * step + half) * BN;
+            if (wave_active && kb0 <= wave_max_pos) {
+                const f16 *lk = lds + buf * STAGE + half * BN * LROW;
+                compute(kb0, lk, lds + buf * STAGE + KSTAGE + half * BN * VROW);
+            }
+            if (more) {
+                lstore(buf ^ 1);
+            }
+            __syncthreads();
+        }
+
+        // ---- merge the two key halves through LDS, normalise, store ----
+        // Wave w and wave w^4 hold the same 32 rows.  Each hands the partner
+        // one 16-row block (half 0 keeps block 0, half 1 keeps block 1).
+        float *xf = reinterpret_cast<float *>(lds);
+        auto put = [&](const f32x4 (&ob)[NT], float m, float lsum) {
+            float *dst = xf + wave * XFER + lane;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const f16 *p0 = vsrc + (32 * ks) * VROW + 16 * t;
-                const f16x4 lo = lds_read_tr16(p0);
-                const f16x4 hi = lds_read_tr16(p0 + 16 * VROW);
-                const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
-                o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    dst[(4 * t + r) * 64] = ob[t][r];
+                }
             }
-        }
-    };
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int blk = 0; blk < n_blocks; ++blk) {
-        const int buf = blk & 1;
-        if (blk + 1 < n_blocks) {
-            gload(blk + 1);
-        }
-        const int kb0 = blk * BN;
-        if (wave_active && kb0 <= wave_max_pos) {
-            const f16 *lk = lds + buf * (KSTAGE + VSTAGE);
-            compute(kb0, lk, lk + KSTAGE);
-        }
-        if (blk + 1 < n_blocks) {
-            lstore(buf ^ 1);
+            dst[4 * NT * 64] = m;
+            dst[(4 * NT + 1) * 64] = lsum;
+        };
+        auto finish = [&](f32x4 (&ob)[NT], float m, float lsum, int nb) {
+            const float *src = xf + (wave ^ 4) * XFER + lane;
+            const float m2 = src[4 * NT * 64];
+            const float l2 = src[(4 * NT + 1) * 64];
+            const float mn = fmaxf(m, m2);
+            const float s1 = m == mn ? 1.0f : fast_exp2(m - mn);
+            const float s2 = m2 == mn ? 1.0f : fast_exp2(m2 - mn);
+            const float ltot = xor_sum_16_32(lsum * s1 + l2 * s2);
+            const int row = wr0 + 16 * nb + c;
+            if (row < a.tokens) {
+                const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+                const float w1 = s1 * inv;
+                const float w2 = s2 * inv;
+                float *orow = a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    float4 v;
+                    v.x = ob[t][0] * w1 + src[(4 * t + 0) * 64] * w2;
+                    v.y = ob[t][1] * w1 + src[(4 * t + 1) * 64] * w2;
+                    v.z = ob[t][2] * w1 + src[(4 * t + 2) * 64] * w2;
+                    v.w = ob[t][3] * w1 + src[(4 * t + 3) * 64] * w2;
+                    *reinterpret_cast<float4 *>(orow + 16 * t + 4 * g) = v;  // dims 16t + 4g + r
+                }
+            }
+        };
+        if (half == 0) {
+            put(o[1], mref[1], l[1]);
+        } else {
+            put(o[0], mref[0], l[0]);
         }
         __syncthreads();
-    }
-
-    // ---- epilogue: normalise and store rows (lane holds dims 16t + 4g + r) ----
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const float lsum = wave_xor_sum16_32(l[nb]);
-        const int row = wr0 + 16 * nb + c;
-        if (wave_active && row < a.tokens) {
-            const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-            float *orow = a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float4 v;
-                v.x = o[nb][t][0] * inv;
-                v.y = o[nb][t][1] * inv;
-                v.z = o[nb][t][2] * inv;
-                v.w = o[nb][t][3] * inv;
-                *reinterpret_cast<float4 *>(orow + 16 * t + 4 * g) = v;
-            }
+        if (half == 0) {
+            finish(o[0], mref[0], l[0], 0);
+        } else {
+            finish(o[1], mref[1], l[1], 1);
+        }
+        __syncthreads();  // exchange reads finish before the next tile's staging writes
+        if (ti + 1 < n_tiles_wg) {
+            lstore(0);
+            __syncthreads();
         }
     }
 }
