@@ -37,6 +37,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace {
 
 constexpr int BM = 128;   // query rows per tile: 4 row groups of 32
@@ -76,23 +78,52 @@ __device__ __forceinline__ float xor_sum_16_32(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// LDS layout of a 64-key half block (one key half of a step), built for
+// global_load_lds_dwordx4: one wave instruction writes 1 KB contiguous, lane l
+// at +16 l.  The 64 keys form NB groups of R = 1024 / (2 D) keys; group b
+// holds keys b, b + NB, b + 2 NB, ... as R unpadded rows at
+//   b * kGroupPitch + 16 * rho(b) + (key / NB) * 2D   bytes,
+// rho(b) = 2 (b & 3) + ((b >> 2) & 1).  The group offsets 16 rho(b) mod 128
+// make both operand reads conflict-free with plain immediate offsets:
+//   K (ds_read_b128): 8 lanes read keys c..c+7 (groups c & (NB-1)), 16 B each,
+//     at 8 distinct 16-byte bank slots;
+//   V (ds_read_b64_tr_b16): 16 lanes read 4 keys x 32 B, groups 4(g&1) + j,
+//     at 4 distinct 32-byte bank slots.
+constexpr int kGroupPitch = 1024 + 128;
+
+__device__ __forceinline__ int rho(int b) { return 2 * (b & 3) + ((b >> 2) & 1); }
+
+template <int D>
+struct HalfLayout {
+    static constexpr int R = 1024 / (2 * D);   // keys per group (one 1 KB load)
+    static constexpr int NB = BN / R;          // groups per 64 keys
+    static constexpr int BYTES = NB * kGroupPitch;
+    // byte offset of (key, 16-byte chunk q) inside the half block
+    static __device__ __forceinline__ int offset(int key, int q) {
+        const int b = key % NB;
+        return b * kGroupPitch + 16 * rho(b) + (key / NB) * (2 * D) + 16 * q;
+    }
+};
+
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
+    typedef HalfLayout<D> HL;
     constexpr int KK = D / 32;                      // QK^T K-steps
     constexpr int NT = D / 16;                      // O^T output tiles
-    constexpr int LROW = D + 8;                     // K row pitch (halves): 16-row x 16-byte reads conflict-free
-    constexpr int VROW = D + 16;                    // V row pitch (halves): transposing 8-byte reads conflict-free
     constexpr int CPR = D / 8;                      // 16-byte chunks per cache row
-    constexpr int SROWS = 2 * BN;                   // keys staged per step: one block per key half
-    constexpr int LOADS = SROWS * CPR / kThreads;   // 16-byte K (and V) loads per thread per step
-    constexpr int KSTAGE = SROWS * LROW;
-    constexpr int VSTAGE = SROWS * VROW;
-    constexpr int STAGE = KSTAGE + VSTAGE;
+    constexpr int HB = HL::BYTES;                   // one 64-key half block (K or V)
+    constexpr int STAGE = 4 * HB;                   // K halves 0,1 then V halves 0,1
+    constexpr int GROUPS = 2 * 2 * HL::NB;          // 1 KB loads per step (K and V, both halves)
+    constexpr int LOADS = GROUPS / kWaves;          // per wave per step
     constexpr int XFER = (4 * NT + 2) * 64;         // floats per wave in the merge exchange
-    static_assert(LOADS * kThreads == SROWS * CPR, "staging loads must tile the step");
-    static_assert(kWaves * XFER * 4 <= 2 * STAGE * 2, "merge exchange must fit in the staging buffers");
+    static_assert(LOADS * kWaves == GROUPS, "staging loads must tile the step");
+    static_assert(kWaves * XFER * 4 <= STAGE, "merge exchange must fit in one staging buffer");
 
-    __shared__ __attribute__((aligned(16))) f16 lds[2 * STAGE];
+    // Two staging buffers as separate LDS variables: the compiler can then
+    // tell the DMA into one from the operand reads of the other and does not
+    // make those reads wait for the DMA (vmcnt).
+    __shared__ __attribute__((aligned(1024))) unsigned char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) unsigned char st1[STAGE];
 
     const int pair = blockIdx.x;
     const int h = blockIdx.y;
@@ -115,31 +146,32 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
 
     auto tile_kmax = [&](int qt) { return a.base + min(qt * BM + BM, a.tokens) - 1; };  // last key of a tile
 
-    f16x8 kreg[LOADS], vreg[LOADS];
-    auto gload = [&](int step, int kmax) {
+    // Direct global -> LDS staging of step `step` (keys step*128 ..) into buffer
+    // `buf`: wave w issues groups w, w + 8, ...; group u = (kv, half, b) lands
+    // at its 1 KB slot, lane l carrying row l / CPR, chunk l % CPR of the group.
+    const int ld_pos = lane / CPR;
+    const int ld_q = lane % CPR;
+    auto stage_load = [&](int step, int kmax, unsigned char *stage) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int idx = tid + kThreads * i;
-            const int key = min(step * SROWS + idx / CPR, kmax);
-            const int col = (idx % CPR) * 8;
-            kreg[i] = *reinterpret_cast<const f16x8 *>(kbase + (size_t)key * row_stride + col);
-            vreg[i] = *reinterpret_cast<const f16x8 *>(vbase + (size_t)key * row_stride + col);
+            const int u = wave + kWaves * i;
+            const int is_v = u / (2 * HL::NB);
+            const int hh = (u / HL::NB) & 1;
+            const int b = u % HL::NB;
+            const int key = min(step * 2 * BN + hh * BN + b + HL::NB * ld_pos, kmax);
+            const f16 *src = (is_v ? vbase : kbase) + (size_t)key * row_stride + 8 * ld_q;
+            unsigned char *dst = stage + (2 * is_v + hh) * HB + b * kGroupPitch + 16 * rho(b);
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
         }
     };
-    auto lstore = [&](int buf) {
-        f16 *lk = lds + buf * STAGE;
-        f16 *lv = lk + KSTAGE;
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int idx = tid + kThreads * i;
-            const int row = idx / CPR;
-            const int col = (idx % CPR) * 8;
-            *reinterpret_cast<f16x8 *>(&lk[row * LROW + col]) = kreg[i];
-            *reinterpret_cast<f16x8 *>(&lv[row * VROW + col]) = vreg[i];
-        }
-    };
+    auto stage_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0): this wave's loads are in LDS
 
-    gload(0, tile_kmax(long_tile));
+    // Lane-dependent parts of the operand addresses (the rest are immediates).
+    const int k_off = HL::offset(c, g);                          // K[c][chunk g]; + 16i rows, + 4kk chunks
+    const int v_key = 4 * g + (c >> 2);
+    const int v_off = HL::offset(v_key, 0) + 8 * (c & 3);        // + 16 rows (hi), 32 rows (ks), 32 B per t
+
+    stage_load(0, tile_kmax(long_tile), st0);  // every tile's first step is staged in st0
     for (int ti = 0; ti < n_tiles_wg; ++ti) {
         const int qt = ti == 0 ? long_tile : pair;
         const int wr0 = qt * BM + 32 * (wave & 3);  // first row of this wave
@@ -178,19 +210,26 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         const int wave_max_pos = a.base + wave_last_row;
         const int wave_min_pos = a.base + wr0;
 
-        // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv.
-        auto compute = [&](int kb0, const f16 *lk, const f16 *lv) {
-            // ---- S^T = K Q^T ----
+        // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv (byte pointers).
+        auto compute = [&](int kb0, const unsigned char *lk, const unsigned char *lv) {
+            // ---- S^T = K Q^T, kk outermost: eight independent accumulators ----
             f32x4 s[4][2];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(lk + (16 * i + c) * LROW + 8 * g + 32 * kk);
-                    s[i][0] = mfma16x16x32(ka, qop[0][kk], s[i][0]);
-                    s[i][1] = mfma16x16x32(ka, qop[1][kk], s[i][1]);
+            for (int kk = 0; kk < KK; ++kk) {
+                f16x8 ka[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    ka[i] = *reinterpret_cast<const f16x8 *>(lk + k_off + HL::offset(16 * i, 4 * kk) - HL::offset(0, 0));
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    s[i][0] = mfma16x16x32(ka[i], qop[0][kk], s[i][0]);
+                    s[i][1] = mfma16x16x32(ka[i], qop[1][kk], s[i][1]);
                 }
             }
             // ---- causal mask (diagonal blocks only), lazy online softmax per row ----
@@ -251,18 +290,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                 l[nb] = psum;
             }
             // ---- O^T += V^T P^T ----
-            // V^T A operand of tile t (dims 16t + m) straight from row-major LDS
-            // with the transposing read: source lane k of each 16-lane group
-            // reads 4 dims (16t + 4(k%4) ..) of key kmap(g, k/4) (+16 rows for
-            // the second half), and lane c receives dim 16t + c of all 8 keys.
-            const f16 *vsrc = lv + (4 * g + (c >> 2)) * VROW + 4 * (c & 3);
+            // V^T A operand of tile t (dims 16t + m) with the transposing read:
+            // source lane k of each 16-lane group reads 4 dims (16t + 4(k%4) ..)
+            // of key kmap(g, k/4) (+16 keys for the second half), and lane c
+            // receives dim 16t + c of all 8 keys.
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const f16 *p0 = vsrc + (32 * ks) * VROW + 16 * t;
-                    const f16x4 lo = lds_read_tr16(p0);
-                    const f16x4 hi = lds_read_tr16(p0 + 16 * VROW);
+                    const unsigned char *p0 = lv + v_off + HL::offset(32 * ks, 2 * t) - HL::offset(0, 0);
+                    const unsigned char *p1 = lv + v_off + HL::offset(32 * ks + 16, 2 * t) - HL::offset(0, 0);
+                    const f16x4 lo = lds_read_tr16(reinterpret_cast<const f16 *>(p0));
+                    const f16x4 hi = lds_read_tr16(reinterpret_cast<const f16 *>(p1));
                     const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
                     o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
@@ -270,33 +309,38 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             }
         };
 
-        if (ti == 0) {
-            lstore(0);
-            __syncthreads();
-        }
-        for (int step = 0; step < n_steps; ++step) {
-            const int buf = step & 1;
-            const bool more = step + 1 < n_steps;
-            if (more) {
-                gload(step + 1, kmax);
-            } else if (ti + 1 < n_tiles_wg) {
-                gload(0, tile_kmax(pair));  // the next tile's first step, in flight across the merge
+        // Steps alternate st0 / st1 (the loop is unrolled by two so every
+        // buffer reference is static); an odd step count gets one empty step,
+        // so a tile always ends on st1, whose last step is done before the
+        // next tile's first DMA (into st0) is issued.
+        auto body = [&](auto tag, int step) {
+            constexpr int B = decltype(tag)::value;
+            const unsigned char *cur = B == 0 ? st0 : st1;
+            unsigned char *nxt = B == 0 ? st1 : st0;
+            if (step + 1 < n_steps) {
+                stage_load(step + 1, kmax, nxt);
+            } else if (B == 1 && ti + 1 < n_tiles_wg) {
+                stage_load(0, tile_kmax(pair), nxt);  // the next tile's first step, in flight across the merge
             }
             const int kb0 = (2 * step + half) * BN;
-            if (wave_active && kb0 <= wave_max_pos) {
-                const f16 *lk = lds + buf * STAGE + half * BN * LROW;
-                compute(kb0, lk, lds + buf * STAGE + KSTAGE + half * BN * VROW);
+            if (step < n_steps && wave_active && kb0 <= wave_max_pos) {
+                compute(kb0, cur + half * HB, cur + (2 + half) * HB);
             }
-            if (more) {
-                lstore(buf ^ 1);
-            }
+            stage_wait();
             __syncthreads();
+        };
+        stage_wait();
+        __syncthreads();
+        for (int step = 0; step < n_steps; step += 2) {
+            body(std::integral_constant<int, 0>(), step);
+            body(std::integral_constant<int, 1>(), step + 1);
         }
 
         // ---- merge the two key halves through LDS, normalise, store ----
         // Wave w and wave w^4 hold the same 32 rows.  Each hands the partner
-        // one 16-row block (half 0 keeps block 0, half 1 keeps block 1).
-        float *xf = reinterpret_cast<float *>(lds);
+        // one 16-row block (half 0 keeps block 0, half 1 keeps block 1).  The
+        // exchange uses st1, free after the last step's barrier.
+        float *xf = reinterpret_cast<float *>(st1);
         auto put = [&](const f32x4 (&ob)[NT], float m, float lsum) {
             float *dst = xf + wave * XFER + lane;
 #pragma unroll
@@ -309,7 +353,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             dst[4 * NT * 64] = m;
             dst[(4 * NT + 1) * 64] = lsum;
         };
-        auto finish = [&](f32x4 (&ob)[NT], float m, float lsum, int nb) {
+        auto finish = [&](const f32x4 (&ob)[NT], float m, float lsum, int nb) {
             const float *src = xf + (wave ^ 4) * XFER + lane;
             const float m2 = src[4 * NT * 64];
             const float l2 = src[(4 * NT + 1) * 64];
@@ -345,11 +389,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         } else {
             finish(o[1], mref[1], l[1], 1);
         }
-        __syncthreads();  // exchange reads finish before the next tile's staging writes
-        if (ti + 1 < n_tiles_wg) {
-            lstore(0);
-            __syncthreads();
-        }
+        __syncthreads();  // exchange reads finish before st1 is staged again
     }
 }
 
