@@ -133,6 +133,23 @@ class Timer:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps  # ms
 
+    def spread(self, fn, reps: int) -> dict:
+        """Per-repetition durations (an event between consecutive launches of
+        the back-to-back sequence): median, p10, p90 in ms."""
+        torch = self.torch
+        fn(0)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record(stream)
+        for i in range(reps):
+            fn(i)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        d = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+        q = lambda f: d[min(reps - 1, int(round(f * (reps - 1))))]
+        return {"median": q(0.5), "p10": q(0.1), "p90": q(0.9)}
+
 
 def cpu_baseline(q_layer, k_layer, v_layer, heads, kv, d, ctx_len: int, layers: int, seconds: float) -> dict:
     """Reference CPU decode attention on one layer, one pinned core, median of reps."""
@@ -173,8 +190,45 @@ def cpu_baseline(q_layer, k_layer, v_layer, heads, kv, d, ctx_len: int, layers: 
     }
 
 
+def cpu_prefill_baseline(heads: int, kv: int, d: int, lengths=(512, 2048)) -> dict:
+    """Reference CPU causal prefill (the per-token loop: row t = decode at
+    position t) for one 3B layer at each length, one pinned core, timed once."""
+    import numpy as np
+
+    import oracle
+
+    use_ref = oracle.ref_lib() is not None
+    rng = np.random.default_rng(42)
+    cpus = sorted(os.sched_getaffinity(0))
+    old = set(cpus)
+    os.sched_setaffinity(0, {cpus[0]})
+    res = {}
+    try:
+        for L in lengths:
+            q = (rng.standard_normal((L, heads * d)) / math.sqrt(d)).astype(np.float32)
+            k = rng.standard_normal((L, kv * d)).astype(np.float16).astype(np.float32)
+            v = rng.standard_normal((L, kv * d)).astype(np.float16).astype(np.float32)
+            t0 = time.perf_counter()
+            for t in range(L):
+                oracle.attention_decode_f32(q[t], k, v, t, heads, kv, d, use_ref=use_ref)
+            res[L] = time.perf_counter() - t0
+    finally:
+        os.sched_setaffinity(0, old)
+    flops = {L: prefill_flops(heads, d, L) for L in lengths}
+    last = max(lengths)
+    return {
+        "value": round(flops[last] / res[last] / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": 1,
+        "kind": "reference" if use_ref else "port",
+        "sample": (f"causal prefill as the reference runs it (qwen.c:810-824: te_attention_decode_f32 at position t "
+                   f"for every row t, {'reference c/src/ops.c' if use_ref else 'oracle port'}), one 3B layer, "
+                   + ", ".join(f"L={L}: {res[L]:.2f} s" for L in lengths) + ", one pinned core, timed once"),
+    }
+
+
 def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_set_bytes=1.2e9, outliers=False,
-                keep_cpu_sample=False):
+                keep_cpu_sample=False, warmup=3, per_layer=False):
     """Decode step over `layers` layers of len(positions) sequences; returns timings."""
     dev = "cuda"
     seqs = len(positions)
@@ -230,7 +284,8 @@ def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_s
         q, k, v, kc, vc = sets[i % ns]
         A.decode_step(q, k, v, cos, sin, kc, vc, positions=positions, workspace=ws, stage="splitk")
 
-    step_ms = timer(step_fused, reps)
+    step_ms = timer(step_fused, reps, warmup=warmup)
+    spread = timer.spread(step_fused, reps)
     fsplitk_ms = timer(step_splitk, reps)
     step3_ms = timer(step_3launch, reps)
     splitk_ms = timer(splitk, reps)
@@ -238,8 +293,43 @@ def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_s
     combine_ms = timer(combine, reps)
     nbytes = decode_bytes(heads, kv, d, [p for p in positions for _ in range(layers)])
     res = dict(step_ms=step_ms, step3_ms=step3_ms, fsplitk_ms=fsplitk_ms, splitk_ms=splitk_ms,
-               rope_append_ms=rope_ms, combine_ms=combine_ms, bytes_per_step=nbytes,
+               rope_append_ms=rope_ms, combine_ms=combine_ms, bytes_per_step=nbytes, spread=spread,
                splitk_gbs=nbytes / (fsplitk_ms * 1e-3) / 1e9, step_gbs=nbytes / (step_ms * 1e-3) / 1e9)
+    if per_layer and seqs == 1:
+        # The same step as `layers` separate fused launches (one layer each, as a
+        # runtime that finishes layer l before layer l+1 would issue them), eager
+        # and captured in one HIP graph.
+        ws1 = A.decode_workspace(1, 1, heads, kv, d, positions=positions)
+        views = []
+        for q, k, v, kc, vc in sets:
+            views.append([(q[:, l:l + 1], k[:, l:l + 1], v[:, l:l + 1], kc[:, l:l + 1], vc[:, l:l + 1],
+                           out[:, l:l + 1]) for l in range(layers)])
+
+        def layer_by_layer(i):
+            for ql, kl, vl, kcl, vcl, ol in views[i % ns]:
+                A.decode_step(ql, kl, vl, cos, sin, kcl, vcl, positions=positions, out=ol, workspace=ws1)
+
+        res["per_layer_ms"] = timer(layer_by_layer, max(5, reps // 5))
+        layer_by_layer(0)
+        torch.cuda.synchronize()
+        eager = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                layer_by_layer(0)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        same = True
+        for _ in range(3):  # every replay must reproduce the eager result
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            same = same and torch.equal(out, eager)
+        res["per_layer_graph_ms"] = timer(lambda i: graph.replay(), max(5, reps // 5))
+        res["per_layer_graph_matches_eager"] = same
+        del graph
     if keep_cpu_sample:
         q, k, v, kc, vc = sets[0]
         res["cpu_sample"] = (q[0, 0, 0].reshape(-1).float().cpu().numpy().copy(),
@@ -325,10 +415,8 @@ def main():
     timer = Timer(torch)
     H, KV, D, LAYERS = 16, 2, 128, 36
     K = args.steps
-    for _ in range(args.warmup):
-        pass  # warm-up launches are done per timed sequence by Timer
     dec = decode_case(torch, A, timer, heads=H, kv=KV, d=D, layers=LAYERS, positions=[args.ctx], reps=K,
-                      keep_cpu_sample=not args.no_cpu_baseline)
+                      keep_cpu_sample=not args.no_cpu_baseline, warmup=args.warmup, per_layer=True)
     pre = prefill_case(torch, A, timer, heads=H, kv=KV, d=D, tokens=4096, reps=max(5, K // 5))
     us_per_layer = dec["step_ms"] * 1e3 / LAYERS
     line = {
@@ -366,6 +454,11 @@ def main():
         },
         "decode": {
             "step_us": r(dec["step_ms"] * 1e3, 2),
+            # per-step distribution, an event recorded between consecutive steps
+            "step_us_evented_median_p10_p90": [r(dec["spread"][k] * 1e3, 2) for k in ("median", "p10", "p90")],
+            "per_layer_launches_step_us": r(dec["per_layer_ms"] * 1e3, 2),
+            "per_layer_launches_graph_step_us": r(dec["per_layer_graph_ms"] * 1e3, 2),
+            "per_layer_graph_matches_eager": dec["per_layer_graph_matches_eager"],
             "fused_splitk_us": r(dec["fsplitk_ms"] * 1e3, 2),
             "step_3launch_us": r(dec["step3_ms"] * 1e3, 2),
             "rope_append_us": r(dec["rope_append_ms"] * 1e3, 2),
@@ -424,6 +517,10 @@ def main():
         cpu = cpu_baseline(ql, kl, vl, H, KV, D, args.ctx, LAYERS, args.cpu_seconds)
         cpu["gpu_speedup"] = round(cpu["value"] / us_per_layer, 1)
         line["cpu_baseline"] = cpu
+        if not args.quick:
+            cp = cpu_prefill_baseline(H, KV, D)
+            cp["gpu_speedup_L4096"] = round(pre["tflops"] * 1e3 / cp["value"], 1)
+            line["cpu_baseline_prefill"] = cp
     print(json.dumps(line))
 
 

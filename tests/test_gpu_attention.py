@@ -446,3 +446,47 @@ def test_decode_step_fused_vs_oracle(oracle_mod, h, kv, d, layers, positions, bi
     torch.cuda.synchronize()
     assert torch.equal(out2, out)
     assert np.array_equal(f16_host_bits(kc), kc_o) and np.array_equal(f16_host_bits(vc), vc_o)
+
+
+# ------------------------------------------------------------ HIP graphs ---
+
+def test_decode_step_graph_replay():
+    """The per-layer fused decode step captured in one HIP graph: every replay
+    (with eager work and synchronisation between replays) reproduces the eager
+    launches bit for bit, and the appended cache slots stay identical."""
+    h, kv, d, layers, pos = 16, 2, 128, 4, 777
+    ctx = pos + 1
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn((1, layers, 1, h, d), generator=g, device="cuda") / math.sqrt(d)
+    k = torch.randn((1, layers, 1, kv, d), generator=g, device="cuda")
+    v = torch.randn((1, layers, 1, kv, d), generator=g, device="cuda")
+    kc = torch.randn((1, layers, ctx, kv, d), generator=g, device="cuda").half()
+    vc = torch.randn((1, layers, ctx, kv, d), generator=g, device="cuda").half()
+    cos, sin = A.rope_table(ctx, d, 1e6)
+    ws = A.decode_workspace(1, 1, h, kv, d, position=pos)
+    out = torch.empty((1, layers, h, d), dtype=torch.float32, device="cuda")
+
+    def run():
+        for l in range(layers):
+            A.decode_step(q[:, l:l + 1], k[:, l:l + 1], v[:, l:l + 1], cos, sin, kc[:, l:l + 1], vc[:, l:l + 1],
+                          position=pos, out=out[:, l:l + 1], workspace=ws)
+
+    run()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    kc_eager, vc_eager = kc.clone(), vc.clone()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.fill_(float(rep + 1))       # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from the eager launches"
+        assert torch.equal(kc, kc_eager) and torch.equal(vc, vc_eager)
+    print(f"graph of {2 * layers} launches: 4 replays identical to eager")
