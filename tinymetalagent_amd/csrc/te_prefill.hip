@@ -211,55 +211,70 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         const int wave_min_pos = a.base + wr0;
 
         // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv (byte pointers).
-        auto compute = [&](int kb0, const unsigned char *lk, const unsigned char *lv) {
-            // ---- S^T = K Q^T, kk outermost: eight independent accumulators ----
+        // MASK: a diagonal block (some key beyond some row's position); the
+        // interior variant carries no mask code, so nothing splits the QK^T
+        // MFMAs from the softmax into separate scheduling regions.
+        auto compute = [&](auto mask_tag, int kb0, const unsigned char *lk, const unsigned char *lv)
+                           __attribute__((always_inline)) {
+            constexpr bool MASK = decltype(mask_tag)::value;
+            // ---- S^T = K Q^T, keys 0-31 then 32-63 (kk inner): the row
+            // maximum of the first half is taken while the second half's MFMAs run ----
             f32x4 s[4][2];
+            float mxh[2][2];  // [key half][row block]
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+            for (int hk = 0; hk < 2; ++hk) {
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                f16x8 ka[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    ka[i] = *reinterpret_cast<const f16x8 *>(lk + k_off + HL::offset(16 * i, 4 * kk) - HL::offset(0, 0));
+                for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
+                    s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    s[i][0] = mfma16x16x32(ka[i], qop[0][kk], s[i][0]);
-                    s[i][1] = mfma16x16x32(ka[i], qop[1][kk], s[i][1]);
+                for (int kk = 0; kk < KK; ++kk) {
+                    f16x8 ka[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        ka[i] = *reinterpret_cast<const f16x8 *>(lk + k_off + HL::offset(16 * (2 * hk + i), 4 * kk) -
+                                                                 HL::offset(0, 0));
+                    }
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        s[2 * hk + i][0] = mfma16x16x32(ka[i], qop[0][kk], s[2 * hk + i][0]);
+                        s[2 * hk + i][1] = mfma16x16x32(ka[i], qop[1][kk], s[2 * hk + i][1]);
+                    }
                 }
-            }
-            // ---- causal mask (diagonal blocks only), lazy online softmax per row ----
-            if (kb0 + BN - 1 > wave_min_pos) {
+                if (MASK) {
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    const int lim = a.base + wr0 + 16 * nb + c - kb0 - 4 * g;  // mask key offsets > lim
+                    for (int nb = 0; nb < 2; ++nb) {
+                        const int lim = a.base + wr0 + 16 * nb + c - kb0 - 4 * g;  // mask key offsets > lim
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
+                        for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            if (16 * i + r > lim) {
-                                s[i][nb][r] = -INFINITY;
+                            for (int r = 0; r < 4; ++r) {
+                                if (16 * i + r > lim) {
+                                    s[i][nb][r] = -INFINITY;
+                                }
                             }
                         }
                     }
                 }
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    float m = -INFINITY;
+#pragma unroll
+                    for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            m = fmaxf(m, s[i][nb][r]);
+                        }
+                    }
+                    mxh[hk][nb] = m;
+                }
             }
+            // ---- lazy online softmax per row ----
             f16x8 pb[2][2];  // [k-step][row block]
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-                float mx = -INFINITY;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        mx = fmaxf(mx, s[i][nb][r]);
-                    }
-                }
-                mx = xor_max_16_32(mx) * qs;
+                float mx = xor_max_16_32(fmaxf(mxh[0][nb], mxh[1][nb])) * qs;
                 if (__any(mx > mref[nb] + kLazyLog2)) {
                     // A row that has seen no unmasked key keeps m_ref = -inf (its
                     // l and O are still zero): a key half can meet such rows.
@@ -324,7 +339,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             }
             const int kb0 = (2 * step + half) * BN;
             if (step < n_steps && wave_active && kb0 <= wave_max_pos) {
-                compute(kb0, cur + half * HB, cur + (2 + half) * HB);
+                if (kb0 + BN - 1 > wave_min_pos) {
+                    compute(std::true_type(), kb0, cur + half * HB, cur + (2 + half) * HB);  // diagonal block
+                } else {
+                    compute(std::false_type(), kb0, cur + half * HB, cur + (2 + half) * HB);
+                }
             }
             stage_wait();
             __syncthreads();
