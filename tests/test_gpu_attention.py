@@ -330,6 +330,60 @@ def test_decode_constant_values_32k():
     assert err <= 1e-4
 
 
+def test_decode_step_full_size_1p5b_128k_outliers(oracle_mod):
+    """BASELINE config 5 decode at full size: 1.5B shape, position 131072, K with
+    +-20 spikes on 3 fixed channels per KV head; the fused step (RoPE + append +
+    split-K) on 2 layers, layer 1 against the oracle, appended slots bit-exact."""
+    h, kv, d, layers, pos = 12, 2, 128, 2, 131072
+    ctx = pos + 1
+    g = torch.Generator(device=DEV).manual_seed(11)
+    kc = torch.randn((1, layers, ctx, kv, d), generator=g, device=DEV)
+    gen = torch.Generator().manual_seed(7)
+    for hk in range(kv):
+        ch = torch.randperm(d, generator=gen)[:3].to(DEV)
+        sign = torch.randint(0, 2, (1, layers, ctx, 3), generator=g, device=DEV) * 2 - 1
+        kc[:, :, :, hk, ch] += 20.0 * sign
+    kc = kc.half()
+    vc = torch.randn((1, layers, ctx, kv, d), generator=g, device=DEV).half()
+    q = torch.randn((1, layers, 1, h, d), generator=g, device=DEV) / math.sqrt(d)
+    k = torch.randn((1, layers, 1, kv, d), generator=g, device=DEV)
+    v = torch.randn((1, layers, 1, kv, d), generator=g, device=DEV)
+    cos, sin = A.rope_table(ctx, d, 1e6)
+    out = A.decode_step(q, k, v, cos, sin, kc, vc, position=pos)
+    torch.cuda.synchronize()
+    # oracle: RoPE + append of the new token into a host copy of layer 1, then decode
+    hcos, hsin = oracle_mod.rope_table(ctx, d, 1e6)
+    kc1, vc1 = f16_host_bits(kc[:, 1:2]).copy(), f16_host_bits(vc[:, 1:2]).copy()
+    q1, k1, v1 = (t[:, 1:2].cpu().numpy().copy() for t in (q, k, v))
+    kslot, vslot = kc1[0, 0, pos].copy(), vc1[0, 0, pos].copy()
+    oracle_mod.rope_kv_append_f16(q1, k1, v1, None, None, None, hcos, hsin, kc1, vc1, 1, 1, 1, None, pos, ctx, h, kv, d)
+    assert np.array_equal(kslot, kc1[0, 0, pos]) and np.array_equal(vslot, vc1[0, 0, pos])  # GPU wrote the same slot
+    want = oracle_mod.attention_decode_f16kv(q1[:, :, 0].copy(), kc1, vc1, None, pos, 1, 1, ctx, h, kv, d)
+    err = maxabs(out[:, 1].cpu().numpy(), want)
+    print(f"1.5B 128K outlier keys, fused step, layer 1: max abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_chunk_after_128k_cache(oracle_mod):
+    """BASELINE config 5 (B): a 256-token prefill chunk at base 131072 over the
+    cached prefix; sampled rows t against the oracle decode at base + t."""
+    h, kv, d, tokens, base = 12, 2, 128, 256, 131072
+    ctx = base + tokens
+    g = torch.Generator(device=DEV).manual_seed(12)
+    kc = torch.randn((1, 1, ctx, kv, d), generator=g, device=DEV).half()
+    vc = torch.randn((1, 1, ctx, kv, d), generator=g, device=DEV).half()
+    qh = torch.randn((1, 1, tokens, h, d), generator=g, device=DEV).half()
+    out = A.attention_prefill(qh, kc, vc, base_position=base).cpu().numpy().reshape(tokens, h, d)
+    kb, vb = f16_host_bits(kc), f16_host_bits(vc)
+    qf = qh.float().cpu().numpy().reshape(tokens, h, d)
+    for t in (0, 129, tokens - 1):
+        want = oracle_mod.attention_decode_f16kv(qf[t].reshape(1, 1, h, d).copy(), kb, vb, None, base + t, 1, 1, ctx,
+                                                 h, kv, d)
+        err = maxabs(out[t], want.reshape(h, d))
+        print(f"prefill chunk after 128K, row {t}: max abs err {err:.3e}")
+        assert err <= TOL
+
+
 # ----------------------------------------------------------------- prefill ---
 
 def _prefill_case(oracle_mod, h, kv, d, tokens, base, seed):
