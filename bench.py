@@ -16,9 +16,11 @@ and resident in HBM before timing.  Distinct KV caches (>= 1.2 GB in total) are
 rotated across steps so the 256 MB MALL cannot serve a step from the previous
 one.
 
-Timing: the step is timed over K back-to-back steps between two HIP events on
-the launch stream; each kernel is also timed alone over K back-to-back
-launches (the per-kernel average that rocprofv3 --kernel-trace reports).
+Timing: after --warmup-seconds of sustained GPU load (the engine clock ramps
+up over the first seconds of work) and W warm-up steps, the step is timed over
+K back-to-back steps between two HIP events on the launch stream; each kernel
+is also timed alone over K back-to-back launches (the per-kernel average that
+rocprofv3 --kernel-trace reports).
 
 Reported: value = microseconds per layer for the whole step; the split-K
 kernel's achieved HBM GB/s against the 8 TB/s peak; prefill TFLOP/s (config 3,
@@ -70,15 +72,31 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--quick", action="store_true", help="headline decode + prefill only")
+    p.add_argument("--warmup-seconds", type=float, default=1.0,
+                   help="sustained GPU load before timing, so clocks are at their steady state")
     p.add_argument("--profile", action="store_true",
                    help="run a fixed kernel sequence for rocprofv3 (5x decode step at 3B/8K/36 layers, "
                         "5x prefill at L=4096, 3x a 512 MiB device copy for counter calibration) and exit")
     return p.parse_args()
 
 
+def settle(torch, fn, seconds: float = 0.25) -> None:
+    """Repeat fn for `seconds` of wall time: the engine clock drops while the
+    host sets a case up and needs tens of milliseconds of load to recover."""
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        fn()
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def profile_sequence(torch, A) -> None:
     """Fixed launch sequence profiled by the commands recorded under profiles/.
-    The device copy (torch's elementwise copy kernel, 512 MiB read + 512 MiB
+    Each kernel first runs for 0.25 s of wall time (clock settling), so the
+    traced averages are steady-state durations.  The device copy (torch's elementwise copy kernel, 512 MiB read + 512 MiB
     written) calibrates FETCH_SIZE / WRITE_SIZE against known bytes."""
     dev = "cuda"
     H, KV, D, LAYERS, L = 16, 2, 128, 36, 8192
@@ -91,6 +109,7 @@ def profile_sequence(torch, A) -> None:
     cos, sin = A.rope_table(L + 1, D, THETA)
     ws = A.decode_workspace(1, LAYERS, H, KV, D, position=L)
     out = torch.empty((1, LAYERS, H, D), dtype=torch.float32, device=dev)
+    settle(torch, lambda: A.decode_step(q, k, v, cos, sin, kc, vc, position=L, out=out, workspace=ws))
     for _ in range(5):
         A.decode_step(q, k, v, cos, sin, kc, vc, position=L, out=out, workspace=ws)
     torch.cuda.synchronize()
@@ -100,6 +119,7 @@ def profile_sequence(torch, A) -> None:
     kp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
     vp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
     po = torch.empty((1, 1, Lp, H, D), dtype=torch.float32, device=dev)
+    settle(torch, lambda: A.attention_prefill(qh, kp, vp, out=po))
     for _ in range(5):
         A.attention_prefill(qh, kp, vp, out=po)
     torch.cuda.synchronize()
@@ -108,21 +128,46 @@ def profile_sequence(torch, A) -> None:
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("profile sequence done: decode step x5 (3B, L=8192, 36 layers), prefill x5 (L=4096), "
-          "copy x3 (536870912 B read + written)")
+    print("profile sequence done: decode step (0.25 s of steps, then 5 more; 3B, L=8192, 36 layers), "
+          "prefill (0.25 s, then 5 more; L=4096), copy x3 (536870912 B read + written)")
+
+
+def gpu_warmup(torch, A, seconds: float) -> None:
+    """Sustained load before any timing: the engine clock of a freshly idle GPU
+    ramps up over the first seconds of work (prefill times fall by ~10 % over
+    the first three seconds), and every figure here is a steady-state rate."""
+    if seconds <= 0:
+        return
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(3)
+    L, H, KV, D = 4096, 16, 2, 128
+    q = torch.randn((1, 1, L, H, D), generator=g, device=dev).half()
+    k = torch.randn((1, 1, L, KV, D), generator=g, device=dev).half()
+    v = torch.randn((1, 1, L, KV, D), generator=g, device=dev).half()
+    out = torch.empty((1, 1, L, H, D), dtype=torch.float32, device=dev)
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            A.attention_prefill(q, k, v, out=out)
+        torch.cuda.synchronize()
+    del q, k, v, out
 
 
 class Timer:
     """Average duration of a launch sequence over back-to-back repetitions."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, settle_seconds: float = 0.25):
         self.torch = torch
+        self.settle = settle_seconds
 
     def __call__(self, fn, reps: int, warmup: int = 3) -> float:
         torch = self.torch
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
+        # keep the GPU busy on this very launch sequence for a moment first
+        count = iter(range(1 << 30))
+        settle(torch, lambda: fn(next(count)), self.settle)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         stream = torch.cuda.current_stream()
@@ -410,11 +455,13 @@ def main():
         raise SystemExit("bench.py: libtinyengine.so found no gfx950 GPU")
     name, cus = R.device_info()
     if args.profile:
+        gpu_warmup(torch, A, args.warmup_seconds)
         profile_sequence(torch, A)
         return
     timer = Timer(torch)
     H, KV, D, LAYERS = 16, 2, 128, 36
     K = args.steps
+    gpu_warmup(torch, A, args.warmup_seconds)
     dec = decode_case(torch, A, timer, heads=H, kv=KV, d=D, layers=LAYERS, positions=[args.ctx], reps=K,
                       keep_cpu_sample=not args.no_cpu_baseline, warmup=args.warmup, per_layer=True)
     pre = prefill_case(torch, A, timer, heads=H, kv=KV, d=D, tokens=4096, reps=max(5, K // 5))
