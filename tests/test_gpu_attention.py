@@ -231,6 +231,7 @@ def test_decode_f16_golden(golden):
     (12, 2, 128, 1, [4096]),
     (16, 16, 128, 1, [300]),
     (8, 1, 64, 2, [5000, 3]),
+    (16, 1, 128, 1, [777]),  # a 16-head group: every MFMA column is a real head
 ])
 def test_decode_f16_vs_oracle(oracle_mod, shape):
     h, kv, d, layers, positions = shape
@@ -415,6 +416,27 @@ def test_prefill_vs_oracle(oracle_mod, h, kv, d, tokens, base):
     err = maxabs(got, want)
     print(f"prefill H{h} KV{kv} d{d} L{tokens} base{base}: max abs err {err:.3e}")
     assert err <= TOL
+
+
+def test_prefill_several_sequences_and_layers(oracle_mod):
+    """seqs x layers (seq, layer) units in one launch, each with its own data,
+    chunk at base 50: every row of every unit against the oracle."""
+    seqs, layers, h, kv, d, tokens, base = 2, 3, 16, 2, 128, 200, 50
+    ctx = base + tokens + 7
+    tag = "pfsl"
+    kc = S.to_f16_bits(S.normal(27, tag + "k", (seqs, layers, ctx, kv, d)))
+    vc = S.to_f16_bits(S.normal(27, tag + "v", (seqs, layers, ctx, kv, d)))
+    q16 = S.to_f16_bits(S.normal(27, tag + "q", (seqs, layers, tokens, h, d)))
+    out = A.attention_prefill(f16_dev(q16), f16_dev(kc), f16_dev(vc), base_position=base)
+    got = out.cpu().numpy()
+    worst = 0.0
+    for s_ in range(seqs):
+        for l_ in range(layers):
+            want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q16[s_, l_]).reshape(tokens, h, d),
+                                                kc[s_, l_].copy(), vc[s_, l_].copy(), tokens, base, ctx, h, kv, d)
+            worst = max(worst, maxabs(got[s_, l_], want.reshape(tokens, h, d)))
+    print(f"prefill {seqs} seqs x {layers} layers, base {base}: max abs err {worst:.3e}")
+    assert worst <= TOL
 
 
 def test_prefill_full_size_4k_rows(oracle_mod):
