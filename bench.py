@@ -412,12 +412,17 @@ def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, rep
         for c in range(chunks):
             A.rope_kv_append(q[c], k[c], v[c], cos, sin, kc, vc, base_position=base + c * tokens, q_half=qh[c])
 
+    def step_fused(i):
+        for c in range(chunks):
+            A.prefill_step(q0[c], k0[c], v0[c], cos, sin, kc, vc, base_position=base + c * tokens, out=out)
+
     attn_ms = timer(attn, reps, warmup=2)
     rope_ms = timer(rope, reps, warmup=1)
+    step_ms = timer(step_fused, reps, warmup=2)
     flops = sum(prefill_flops(heads, d, tokens, base + c * tokens) for c in range(chunks))
     del kc, vc, q0, k0, v0, q, k, v, qh, out
     torch.cuda.empty_cache()
-    return dict(attention_ms=attn_ms, rope_append_ms=rope_ms, flops=flops,
+    return dict(attention_ms=attn_ms, rope_append_ms=rope_ms, step_ms=step_ms, flops=flops,
                 tflops=flops / (attn_ms * 1e-3) / 1e12)
 
 
@@ -518,6 +523,10 @@ def main():
             "workload": "Qwen2.5-3B causal prefill attention, L=4096, one layer per launch (BASELINE configs[2])",
             "attention_us": r(pre["attention_ms"] * 1e3, 2),
             "rope_append_us": r(pre["rope_append_ms"] * 1e3, 2),
+            # the whole prefill step: separate RoPE+append then attention, and the
+            # fused step (K/V append launch + attention with q RoPE on load)
+            "step_unfused_us": r((pre["rope_append_ms"] + pre["attention_ms"]) * 1e3, 2),
+            "step_fused_us": r(pre["step_ms"] * 1e3, 2),
             "tflops": round(pre["tflops"], 1),
             "roofline": {"bound": "mfma", "kernel": "prefill_causal_f16_kernel<128>",
                          "achieved": round(pre["tflops"], 1), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",

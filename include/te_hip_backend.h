@@ -197,6 +197,27 @@ TE_API te_status te_hip_attention_prefill_f16(
     float *out, void *stream);
 
 /*
+ * Fused prefill step: te_hip_rope_kv_append_f16 (tokens tokens at base_position)
+ * followed by te_hip_attention_prefill_f16, as two launches: bias + RoPE + fp16
+ * append of the chunk's k/v, then the causal attention, whose prologue applies
+ * bias + RoPE to each query row in registers and rounds it to the fp16 operand
+ * (the same bits te_hip_rope_kv_append_f16 writes to q_half).  `query`, `k_new`
+ * and `v_new` are inputs only: nothing is rotated in place and no fp16 copy of
+ * the queries is stored.  Layouts: query [seqs][layers][tokens][heads][head_dim],
+ * k_new / v_new [seqs][layers][tokens][kv_heads][head_dim], out like query.
+ * Every sequence starts at base_position.  Arguments and limits otherwise as
+ * te_hip_rope_kv_append_f16 and te_hip_attention_prefill_f16.
+ */
+TE_API te_status te_hip_attention_prefill_step_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *stream);
+
+/*
  * Host-pointer twins of the reference MMA attention entry points
  * (metal_backend.h:104-142, metal_backend.mm:30-373), same signatures and the
  * same shape guards (q_rows == 8, head_dim == 64; k_cols == 8 for qk/tile,

@@ -126,6 +126,17 @@ def test_backend_guard_conventions(lib):
     assert lib.te_hip_attention_prefill_f16(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None) in ok
     assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 6, 8, 2, 1, 128, buf, None) == 1
     assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None) == 3
+    step = lib.te_hip_attention_prefill_step_f16
+    assert step(buf, None, buf, None, None, None, buf, buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128,
+                buf, None) == 1  # no k_new
+    assert step(buf, buf, buf, None, None, None, None, buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128,
+                buf, None) == 1  # no rope table
+    assert step(buf, buf, buf, None, None, None, buf, buf, buf, buf, 1, 1, 4, 6, 8, 2, 1, 128,
+                buf, None) == 1  # chunk past the cache
+    assert step(buf, buf, buf, None, None, None, buf, buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80,
+                buf, None) == 3  # head_dim 80
+    assert step(buf, buf, buf, None, None, None, buf, buf, buf, buf, 65, 1, 4, 0, 8, 2, 1, 128,
+                buf, None) == 3  # more than 64 sequences
     q = np.ones(8 * 64, np.float32).ctypes.data_as(ctypes.POINTER(ctypes.c_float))
     assert lib.te_hip_attention_qk_mma_f32(None, q, 8, 8, 64, q) in ok
     assert lib.te_hip_attention_qk_mma_f32(q, q, 4, 8, 64, q) == 3

@@ -439,6 +439,55 @@ def test_prefill_several_sequences_and_layers(oracle_mod):
     assert worst <= TOL
 
 
+@pytest.mark.parametrize("seqs,layers,h,kv,d,tokens,base,bias", [
+    (1, 1, 16, 2, 128, 300, 0, True),
+    (2, 2, 14, 2, 64, 130, 37, True),
+    (1, 2, 12, 2, 128, 200, 500, False),
+])
+def test_prefill_step_fused_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens, base, bias):
+    """te_hip_attention_prefill_step_f16 == rope_kv_append (with q_half) +
+    prefill, per the oracle: cache slots bit-exact, outputs within the bar,
+    query/k/v untouched."""
+    ctx = base + tokens + 3
+    tag = f"pfs{h}{kv}{d}{tokens}{base}"
+    q = S.normal(28, tag + "q", (seqs, layers, tokens, h, d), 1 / math.sqrt(d))
+    k = S.normal(28, tag + "k", (seqs, layers, tokens, kv, d))
+    v = S.normal(28, tag + "v", (seqs, layers, tokens, kv, d))
+    qb = S.normal(28, tag + "qb", (layers, h * d), 0.1) if bias else None
+    kb = S.normal(28, tag + "kb", (layers, kv * d), 0.1) if bias else None
+    vb = S.normal(28, tag + "vb", (layers, kv * d), 0.1) if bias else None
+    kc0 = S.to_f16_bits(S.normal(28, tag + "kc", (seqs, layers, ctx, kv, d)))  # cached prefix (positions < base)
+    vc0 = S.to_f16_bits(S.normal(28, tag + "vc", (seqs, layers, ctx, kv, d)))
+    cos, sin = oracle_mod.rope_table(ctx, d, 1e6)
+    q_o, k_o, v_o, kc_o, vc_o = q.copy(), k.copy(), v.copy(), kc0.copy(), vc0.copy()
+    oracle_mod.rope_kv_append_f16(q_o, k_o, v_o, qb, kb, vb, cos, sin, kc_o, vc_o, seqs, layers, tokens, None, base,
+                                  ctx, h, kv, d)
+    q_half = S.to_f16_bits(q_o)  # the fp16 operand the unfused path stores
+    tq, tk, tv = to_dev(q), to_dev(k), to_dev(v)
+    dcos, dsin = A.rope_table(ctx, d, 1e6)
+    kc, vc = f16_dev(kc0), f16_dev(vc0)
+    out = A.prefill_step(tq, tk, tv, dcos, dsin, kc, vc, base_position=base,
+                         q_bias=to_dev(qb) if bias else None, k_bias=to_dev(kb) if bias else None,
+                         v_bias=to_dev(vb) if bias else None)
+    torch.cuda.synchronize()
+    assert np.array_equal(f16_host_bits(kc), kc_o) and np.array_equal(f16_host_bits(vc), vc_o)
+    assert np.array_equal(tq.cpu().numpy(), q) and np.array_equal(tk.cpu().numpy(), k)
+    assert np.array_equal(tv.cpu().numpy(), v)
+    # same output bits as the unfused kernel on the stored fp16 queries
+    ref = A.attention_prefill(f16_dev(q_half), kc, vc, base_position=base)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    got = out.cpu().numpy()
+    worst = 0.0
+    for s_ in range(seqs):
+        for l_ in range(layers):
+            want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q_half[s_, l_]).reshape(tokens, h, d),
+                                                kc_o[s_, l_].copy(), vc_o[s_, l_].copy(), tokens, base, ctx, h, kv, d)
+            worst = max(worst, maxabs(got[s_, l_], want.reshape(tokens, h, d)))
+    print(f"fused prefill step H{h} KV{kv} d{d} L{tokens} base{base} x{seqs * layers}: max abs err {worst:.3e}")
+    assert worst <= TOL
+
+
 def test_prefill_full_size_4k_rows(oracle_mod):
     """BASELINE config 3 at L=4096 (fp16 Q/K/V ~ N(0,1), RoPE at 0..L-1, causal):
     strided rows against the oracle, plus row t == the decode kernel at position t."""

@@ -177,3 +177,23 @@ def attention_prefill(q_half, key_cache, value_cache, *, base_position: int = 0,
                                                       layers, tokens, base_position, ctx, heads, kv_heads, head_dim,
                                                       _ptr(out), _stream(stream)))
     return out
+
+
+def prefill_step(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_cache, *, base_position: int = 0,
+                 q_bias=None, k_bias=None, v_bias=None, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Fused prefill step: bias + RoPE + fp16 append of the chunk's k/v, then causal
+    attention with bias + RoPE of q applied on load.  query fp32 [seqs, layers,
+    tokens, heads, d]; query/k_new/v_new are read only; out fp32, same shape."""
+    seqs, layers, tokens, heads, head_dim = query.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    for t, dt, n in ((query, torch.float32, "query"), (k_new, torch.float32, "k_new"), (v_new, torch.float32, "v_new"),
+                     (key_cache, torch.float16, "key_cache"), (value_cache, torch.float16, "value_cache"),
+                     (rope_cos, torch.float32, "rope_cos"), (rope_sin, torch.float32, "rope_sin")):
+        _dtype(t, dt, n)
+    if out is None:
+        out = torch.empty(query.shape, dtype=torch.float32, device=query.device)
+    check(load_library().te_hip_attention_prefill_step_f16(
+        _ptr(query), _ptr(k_new), _ptr(v_new), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(rope_cos),
+        _ptr(rope_sin), _ptr(key_cache), _ptr(value_cache), seqs, layers, tokens, base_position, ctx, heads,
+        kv_heads, head_dim, _ptr(out), _stream(stream)))
+    return out

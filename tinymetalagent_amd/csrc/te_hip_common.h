@@ -89,6 +89,10 @@ size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layer
 te_status launch_decode_f32(const float *query, const float *key_cache, const float *value_cache,
                             size_t position, size_t heads, size_t kv_heads, size_t head_dim, float *out,
                             float *part_o, float *part_ml, hipStream_t stream);
+te_status launch_kv_append(const float *k, const float *v, const float *k_bias, const float *v_bias,
+                           const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+                           uint16_t *value_cache, size_t seqs, size_t layers, size_t tokens, size_t base_position,
+                           size_t context_tokens, size_t kv_heads, size_t head_dim, hipStream_t stream);
 te_status launch_rope_rows(float *values, size_t heads, size_t head_dim, const float *cos_row,
                            const float *sin_row, hipStream_t stream);
 te_status launch_mma_kat(int mode, const float *query, const float *key_t, const float *value, int k_cols,

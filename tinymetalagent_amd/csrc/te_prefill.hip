@@ -48,7 +48,11 @@ constexpr int kThreads = kWaves * 64;
 constexpr float kLazyLog2 = 8.0f;
 
 struct PrefillArgs {
-    const f16 *q;
+    const f16 *q;            // fp16 rotated queries, or null when q32 is given
+    const float *q32;        // fused step: fp32 queries, bias + RoPE applied on load
+    const float *q_bias;     // fused step: [layers][heads*D] or null
+    const float *rope_cos;   // fused step: [ctx][D/2]
+    const float *rope_sin;
     const f16 *key_cache;
     const f16 *value_cache;
     float *out;
@@ -62,6 +66,66 @@ struct PrefillArgs {
     int n_qtiles;
     float qscale;  // log2(e)/sqrt(D), applied to the fp32 scores
 };
+
+// Fused prefill step: query row `row` of (sl, layer) for head h, bias + RoPE at
+// its position, rounded to the fp16 Q^T operand -- the operation order of
+// rope_kv_append_kernel (FP contraction off), so the operand bits equal the
+// fp16 queries the unfused path stores.  Lane (g, c) holds dims 8g + 32kk + j;
+// the rotation partner of dim d < D/2 is d + D/2, at kk + KK/2 in the same lane.
+template <int D>
+__device__ __forceinline__ void load_q_rope(const PrefillArgs &a, int sl, int layer, int h, int row, int g,
+                                            f16x8 (&qop)[D / 32]) {
+#pragma clang fp contract(off)
+    constexpr int KK = D / 32;
+    constexpr int HALF = D / 2;
+    const float *qrow = a.q32 + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
+    float x[KK][8];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        const float4 v0 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk);
+        const float4 v1 = *reinterpret_cast<const float4 *>(qrow + 8 * g + 32 * kk + 4);
+        x[kk][0] = v0.x;
+        x[kk][1] = v0.y;
+        x[kk][2] = v0.z;
+        x[kk][3] = v0.w;
+        x[kk][4] = v1.x;
+        x[kk][5] = v1.y;
+        x[kk][6] = v1.z;
+        x[kk][7] = v1.w;
+    }
+    if (a.q_bias != nullptr) {
+        const float *qb = a.q_bias + ((size_t)layer * a.heads + h) * D;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const float4 b0 = *reinterpret_cast<const float4 *>(qb + 8 * g + 32 * kk);
+            const float4 b1 = *reinterpret_cast<const float4 *>(qb + 8 * g + 32 * kk + 4);
+            const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                x[kk][j] = x[kk][j] + bv[j];
+            }
+        }
+    }
+    const int pos = a.base + row;
+    const float *cos_row = a.rope_cos + (size_t)pos * HALF;
+    const float *sin_row = a.rope_sin + (size_t)pos * HALF;
+#pragma unroll
+    for (int kk = 0; kk < KK / 2; ++kk) {
+        const float4 c0 = *reinterpret_cast<const float4 *>(cos_row + 8 * g + 32 * kk);
+        const float4 c1 = *reinterpret_cast<const float4 *>(cos_row + 8 * g + 32 * kk + 4);
+        const float4 s0 = *reinterpret_cast<const float4 *>(sin_row + 8 * g + 32 * kk);
+        const float4 s1 = *reinterpret_cast<const float4 *>(sin_row + 8 * g + 32 * kk + 4);
+        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x0 = x[kk][j];
+            const float x1 = x[kk + KK / 2][j];
+            qop[kk][j] = (f16)(x0 * cv[j] - x1 * sv[j]);
+            qop[kk + KK / 2][j] = (f16)(x1 * cv[j] + x0 * sv[j]);
+        }
+    }
+}
 
 __device__ __forceinline__ float xor_max_16_32(float v) {
     // lanes l, l^16, l^32, l^48 hold one row's values: two permlane swaps (VALU, no LDS)
@@ -184,14 +248,20 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         for (int nb = 0; nb < 2; ++nb) {
             const int row = wr0 + 16 * nb + c;
             const bool ok = row < a.tokens;
-            const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
+            if (a.q32 != nullptr) {
+                load_q_rope<D>(a, sl, sl % a.layers, h, ok ? row : 0, g, qop[nb]);
+            } else {
+                const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                f16x8 v = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
-                if (!ok) {
-                    v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                for (int kk = 0; kk < KK; ++kk) {
+                    qop[nb][kk] = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
                 }
-                qop[nb][kk] = v;
+            }
+            if (!ok) {
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    qop[nb][kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                }
             }
         }
 
@@ -414,28 +484,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
 
 }  // namespace
 
-extern "C" te_status te_hip_attention_prefill_f16(
-    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
-    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
-    size_t heads, size_t kv_heads, size_t head_dim,
-    float *out, void *stream) {
-    if (q_half == nullptr || key_cache == nullptr || value_cache == nullptr || out == nullptr || seqs == 0 ||
-        layers == 0 || tokens == 0 || context_tokens == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 ||
-        (heads % kv_heads) != 0) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    if ((head_dim != 64 && head_dim != 128) || context_tokens > (1u << 30) || heads > 65535 ||
-        seqs * layers > 65535) {
-        return TE_STATUS_UNSUPPORTED;
-    }
-    if (base_position > context_tokens || tokens > context_tokens - base_position) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    PrefillArgs a;
-    a.q = reinterpret_cast<const f16 *>(q_half);
-    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
-    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
-    a.out = out;
+namespace {
+
+te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t tokens, size_t base_position,
+                         size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim, void *stream) {
     a.layers = (int)layers;
     a.tokens = (int)tokens;
     a.base = (int)base_position;
@@ -454,4 +506,78 @@ extern "C" te_status te_hip_attention_prefill_f16(
         prefill_causal_f16_kernel<64><<<grid, kThreads, 0, strm>>>(a);
     }
     return te_hip::launch_status();
+}
+
+te_status check_prefill_args(size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+                             size_t heads, size_t kv_heads, size_t head_dim) {
+    if (seqs == 0 || layers == 0 || tokens == 0 || context_tokens == 0 || heads == 0 || kv_heads == 0 ||
+        head_dim == 0 || (heads % kv_heads) != 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    // Cache offsets of one (seq, layer) are 32-bit buffer offsets in the kernel.
+    if ((head_dim != 64 && head_dim != 128) || context_tokens * kv_heads * head_dim * 2 >= ((size_t)1 << 31) ||
+        heads > 65535 || seqs * layers > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    if (base_position > context_tokens || tokens > context_tokens - base_position) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    return TE_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" te_status te_hip_attention_prefill_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *stream) {
+    if (q_half == nullptr || key_cache == nullptr || value_cache == nullptr || out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_status st = check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    PrefillArgs a = {};
+    a.q = reinterpret_cast<const f16 *>(q_half);
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
+    a.out = out;
+    return launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
+}
+
+extern "C" te_status te_hip_attention_prefill_step_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim, float *out, void *stream) {
+    if (query == nullptr || k_new == nullptr || v_new == nullptr || rope_cos == nullptr || rope_sin == nullptr ||
+        key_cache == nullptr || value_cache == nullptr || out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_status st = check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    if (seqs > TE_HIP_MAX_SEQS || tokens > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    st = te_hip::launch_kv_append(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache, seqs,
+                                  layers, tokens, base_position, context_tokens, kv_heads, head_dim,
+                                  te_hip::as_stream(stream));
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    PrefillArgs a = {};
+    a.q32 = query;
+    a.q_bias = q_bias;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
+    a.out = out;
+    return launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
 }

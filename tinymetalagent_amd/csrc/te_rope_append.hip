@@ -32,6 +32,7 @@ struct RopeAppendArgs {
     f16 *key_cache;
     f16 *value_cache;
     f16 *q_half;
+    int write_back;  // 0: k and v are inputs only (fused prefill step)
     int layers;
     int tokens;
     int ctx;
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
     const float *sin_row = a.sin_t + (size_t)pos * half;
     const size_t tok = (size_t)sl * a.tokens + b;
 
-    if (item < a.heads * half) {
+    if (a.q != nullptr && item < a.heads * half) {
         const int head = item / half;
         const int i = item - head * half;
         const int off = head * a.head_dim + i;
@@ -94,8 +95,10 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
         const float sn = sin_row[i];
         const float lo = x0 * c - x1 * sn;
         const float hi = x1 * c + x0 * sn;
-        krow[off] = lo;
-        krow[off + half] = hi;
+        if (a.write_back) {
+            krow[off] = lo;
+            krow[off + half] = hi;
+        }
         a.key_cache[slot + off] = (f16)lo;
         a.key_cache[slot + off + half] = (f16)hi;
     }
@@ -105,7 +108,9 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
         float x = vrow[item];
         if (a.v_bias != nullptr) {
             x = x + a.v_bias[(size_t)layer * kv_dim + item];
-            vrow[item] = x;
+            if (a.write_back) {
+                vrow[item] = x;
+            }
         }
         a.value_cache[slot + item] = (f16)x;
     }
@@ -133,6 +138,36 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(float *values, int heads
 }  // namespace
 
 namespace te_hip {
+
+te_status launch_kv_append(const float *k, const float *v, const float *k_bias, const float *v_bias,
+                           const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+                           uint16_t *value_cache, size_t seqs, size_t layers, size_t tokens, size_t base_position,
+                           size_t context_tokens, size_t kv_heads, size_t head_dim, hipStream_t stream) {
+    RopeAppendArgs a = {};
+    a.q = nullptr;
+    a.k = const_cast<float *>(k);  // read only: write_back = 0
+    a.v = const_cast<float *>(v);
+    a.k_bias = k_bias;
+    a.v_bias = v_bias;
+    a.cos_t = rope_cos;
+    a.sin_t = rope_sin;
+    a.key_cache = reinterpret_cast<f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<f16 *>(value_cache);
+    a.write_back = 0;
+    a.layers = (int)layers;
+    a.tokens = (int)tokens;
+    a.ctx = (int)context_tokens;
+    a.heads = 0;
+    a.kv_heads = (int)kv_heads;
+    a.head_dim = (int)head_dim;
+    for (size_t s = 0; s < seqs; ++s) {
+        a.base[s] = (int)base_position;
+    }
+    const size_t items = kv_heads * head_dim;
+    const dim3 grid((unsigned)((items + 255) / 256), (unsigned)tokens, (unsigned)(seqs * layers));
+    rope_kv_append_kernel<<<grid, 256, 0, stream>>>(a);
+    return launch_status();
+}
 
 te_status launch_rope_rows(float *values, size_t heads, size_t head_dim, const float *cos_row,
                            const float *sin_row, hipStream_t stream) {
@@ -181,6 +216,7 @@ extern "C" te_status te_hip_rope_kv_append_f16(
     a.key_cache = reinterpret_cast<f16 *>(key_cache);
     a.value_cache = reinterpret_cast<f16 *>(value_cache);
     a.q_half = reinterpret_cast<f16 *>(q_half);
+    a.write_back = 1;
     a.layers = (int)layers;
     a.tokens = (int)tokens;
     a.ctx = (int)context_tokens;

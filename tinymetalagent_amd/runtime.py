@@ -185,6 +185,8 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_hip_attention_decode_step_splitk_f16",
          [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _szp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _sz, _vp])
     _sig(lib, "te_hip_attention_prefill_f16", [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp])
+    _sig(lib, "te_hip_attention_prefill_step_f16",
+         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp])
     _sig(lib, "te_hip_attention_qk_mma_f32", [_f32p, _f32p, _sz, _sz, _sz, _f32p])
     _sig(lib, "te_hip_attention_tile_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p])
     _sig(lib, "te_hip_attention_stream_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p])
