@@ -196,6 +196,30 @@ class Timer:
         return {"median": q(0.5), "p10": q(0.1), "p90": q(0.9)}
 
 
+def mfma_ceilings(torch, timer) -> dict:
+    """fp16 MFMA rates this device sustains, measured in the same run as the
+    prefill kernel: a register-operand MFMA loop (te_hip_calibrate_mfma_f16: no
+    memory, no LDS) and the vendor library's dense fp16 GEMM (hipBLASLt through
+    torch.matmul, 8192^3).  The prefill fraction is reported against both."""
+    from tinymetalagent_amd.runtime import check, load_library
+
+    lib = load_library()
+    blocks, iters = 512, 1000
+    sink = torch.empty(blocks * 512, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    check(lib.te_hip_calibrate_mfma_f16(blocks, iters, sink.data_ptr(), stream))
+    loop_ms = timer(lambda i: lib.te_hip_calibrate_mfma_f16(blocks, iters, sink.data_ptr(), stream), 10)
+    loop_flop = blocks * 8 * iters * 8 * 16 * 16 * 32 * 2
+    n = 8192
+    a = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    c = torch.empty(n, n, device="cuda", dtype=torch.float16)
+    gemm_ms = timer(lambda i: torch.matmul(a, b, out=c), 10)
+    del a, b, c, sink
+    return {"register_mfma_loop_tflops": round(loop_flop / (loop_ms * 1e-3) / 1e12, 1),
+            "hipblaslt_fp16_gemm_8192_tflops": round(2.0 * n ** 3 / (gemm_ms * 1e-3) / 1e12, 1)}
+
+
 def cpu_baseline(q_layer, k_layer, v_layer, heads, kv, d, ctx_len: int, layers: int, seconds: float) -> dict:
     """Reference CPU decode attention on one layer, one pinned core, median of reps."""
     import oracle
@@ -470,6 +494,7 @@ def main():
     dec = decode_case(torch, A, timer, heads=H, kv=KV, d=D, layers=LAYERS, positions=[args.ctx], reps=K,
                       keep_cpu_sample=not args.no_cpu_baseline, warmup=args.warmup, per_layer=True)
     pre = prefill_case(torch, A, timer, heads=H, kv=KV, d=D, tokens=4096, reps=max(5, K // 5))
+    ceil = mfma_ceilings(torch, timer)
     us_per_layer = dec["step_ms"] * 1e3 / LAYERS
     line = {
         "metric": METRIC,
@@ -531,6 +556,9 @@ def main():
             "roofline": {"bound": "mfma", "kernel": "prefill_causal_f16_kernel<128>",
                          "achieved": round(pre["tflops"], 1), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": r(pre["tflops"] / FP16_MFMA_PEAK_TFLOPS), "flops_per_launch": pre["flops"]},
+            # achievable fp16 MFMA rates measured in this run (see mfma_ceilings)
+            "ceilings": dict(ceil, frac_of_register_mfma_loop=r(pre["tflops"] / ceil["register_mfma_loop_tflops"]),
+                             frac_of_hipblaslt_gemm=r(pre["tflops"] / ceil["hipblaslt_fp16_gemm_8192_tflops"])),
         },
     }
     if not args.quick:

@@ -239,6 +239,15 @@ TE_API te_status te_hip_attention_causal_mma_f32(const float *query, const float
                                                  size_t q_rows, size_t k_cols, size_t head_dim, size_t q_base,
                                                  float *out);
 
+/*
+ * Measurement only, no counterpart in the reference: `blocks` workgroups of 8
+ * waves each run `iters` rounds of 8 independent fp16 16x16x32 MFMAs on
+ * register operands (blocks*8*iters*8*16384 FLOP), so a benchmark can report
+ * the MFMA rate the device sustains next to the data-sheet peak.  `out` holds
+ * blocks*512 floats.  blocks in [1, 65535], iters in [1, 2^20].  Asynchronous.
+ */
+TE_API te_status te_hip_calibrate_mfma_f16(size_t blocks, size_t iters, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

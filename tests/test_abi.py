@@ -137,6 +137,9 @@ def test_backend_guard_conventions(lib):
                 buf, None) == 3  # head_dim 80
     assert step(buf, buf, buf, None, None, None, buf, buf, buf, buf, 65, 1, 4, 0, 8, 2, 1, 128,
                 buf, None) == 3  # more than 64 sequences
+    assert lib.te_hip_calibrate_mfma_f16(0, 10, buf, None) == 1  # no workgroups
+    assert lib.te_hip_calibrate_mfma_f16(1, 0, buf, None) == 1  # no iterations
+    assert lib.te_hip_calibrate_mfma_f16(1, 10, None, None) == 1  # no output
     q = np.ones(8 * 64, np.float32).ctypes.data_as(ctypes.POINTER(ctypes.c_float))
     assert lib.te_hip_attention_qk_mma_f32(None, q, 8, 8, 64, q) in ok
     assert lib.te_hip_attention_qk_mma_f32(q, q, 4, 8, 64, q) == 3

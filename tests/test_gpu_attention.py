@@ -615,3 +615,14 @@ def test_decode_step_graph_replay():
         assert torch.equal(out, eager), f"replay {rep} differs from the eager launches"
         assert torch.equal(kc, kc_eager) and torch.equal(vc, vc_eager)
     print(f"graph of {2 * layers} launches: 4 replays identical to eager")
+
+
+def test_calibration_kernel_runs():
+    """The measurement-only MFMA loop behind bench.py's ceilings launches and
+    writes every output element (the buffer starts as NaN)."""
+    lib = R.load_library()
+    blocks, iters = 4, 3
+    out = torch.full((blocks * 512,), float("nan"), dtype=torch.float32, device="cuda")
+    R.check(lib.te_hip_calibrate_mfma_f16(blocks, iters, out.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()

@@ -191,6 +191,7 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_hip_attention_tile_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p])
     _sig(lib, "te_hip_attention_stream_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p])
     _sig(lib, "te_hip_attention_causal_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _f32p])
+    _sig(lib, "te_hip_calibrate_mfma_f16", [_sz, _sz, _vp, _vp])
 
 
 def strerror(status: int) -> str:
