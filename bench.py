@@ -101,19 +101,27 @@ def profile_sequence(torch, A) -> None:
     dev = "cuda"
     H, KV, D, LAYERS, L = 16, 2, 128, 36, 8192
     g = torch.Generator(device=dev).manual_seed(42)
-    kc = torch.randn((1, LAYERS, L + 1, KV, D), generator=g, device=dev).half()
-    vc = torch.randn((1, LAYERS, L + 1, KV, D), generator=g, device=dev).half()
+    # four KV sets (1.2 GB) rotated as in the timed runs, so the 256 MB MALL
+    # cannot serve a launch from the previous one
+    sets = [(torch.randn((1, LAYERS, L + 1, KV, D), generator=g, device=dev).half(),
+             torch.randn((1, LAYERS, L + 1, KV, D), generator=g, device=dev).half()) for _ in range(4)]
     q = torch.randn((1, LAYERS, 1, H, D), generator=g, device=dev) / math.sqrt(D)
     k = torch.randn((1, LAYERS, 1, KV, D), generator=g, device=dev)
     v = torch.randn((1, LAYERS, 1, KV, D), generator=g, device=dev)
     cos, sin = A.rope_table(L + 1, D, THETA)
     ws = A.decode_workspace(1, LAYERS, H, KV, D, position=L)
     out = torch.empty((1, LAYERS, H, D), dtype=torch.float32, device=dev)
-    settle(torch, lambda: A.decode_step(q, k, v, cos, sin, kc, vc, position=L, out=out, workspace=ws))
-    for _ in range(5):
+    count = iter(range(1 << 30))
+
+    def step():
+        kc, vc = sets[next(count) % 4]
         A.decode_step(q, k, v, cos, sin, kc, vc, position=L, out=out, workspace=ws)
+
+    settle(torch, step)
+    for _ in range(5):
+        step()
     torch.cuda.synchronize()
-    del kc, vc
+    del sets
     Lp = 4096
     qh = torch.randn((1, 1, Lp, H, D), generator=g, device=dev).half()
     kp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
@@ -128,7 +136,8 @@ def profile_sequence(torch, A) -> None:
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("profile sequence done: decode step (0.25 s of steps, then 5 more; 3B, L=8192, 36 layers), "
+    print("profile sequence done: decode step (0.25 s of steps, then 5 more; 3B, L=8192, 36 layers, "
+          "4 rotated KV sets), "
           "prefill (0.25 s, then 5 more; L=4096), copy x3 (536870912 B read + written)")
 
 
@@ -409,10 +418,11 @@ def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_s
     return res
 
 
-def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, reps=10):
+def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, reps=10, split=False):
     """Causal prefill of `chunks` chunks of `tokens` tokens starting at position `base`
     (one layer): per chunk RoPE + fp16 append of the chunk, then attention over
-    positions 0..base+(c+1)*tokens-1.  Returns the attention-kernel time summed over chunks."""
+    positions 0..base+(c+1)*tokens-1.  Returns the attention-kernel time summed over
+    chunks; with `split`, also the key-split entry point (partials + merge launch)."""
     dev = "cuda"
     ctx = base + chunks * tokens
     g = torch.Generator(device=dev).manual_seed(43)
@@ -444,10 +454,29 @@ def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, rep
     rope_ms = timer(rope, reps, warmup=1)
     step_ms = timer(step_fused, reps, warmup=2)
     flops = sum(prefill_flops(heads, d, tokens, base + c * tokens) for c in range(chunks))
+    res = dict(attention_ms=attn_ms, rope_append_ms=rope_ms, step_ms=step_ms, flops=flops,
+               tflops=flops / (attn_ms * 1e-3) / 1e12)
+    if split:
+        ws = [A.prefill_workspace(1, 1, tokens, heads, kv, d, base_position=base + c * tokens, context_tokens=ctx)
+              for c in range(chunks)]
+
+        def attn_split(i):
+            for c in range(chunks):
+                A.attention_prefill_split(qh[c], kc, vc, base_position=base + c * tokens, out=out, workspace=ws[c])
+
+        res["split_ms"] = timer(attn_split, reps, warmup=2)
+        res["split_tflops"] = flops / (res["split_ms"] * 1e-3) / 1e12
+        res["splits"] = [1 if w is None else w.numel() // (tokens * heads * (d + 2) * 4) for w in ws]
+        del ws
     del kc, vc, q0, k0, v0, q, k, v, qh, out
     torch.cuda.empty_cache()
-    return dict(attention_ms=attn_ms, rope_append_ms=rope_ms, step_ms=step_ms, flops=flops,
-                tflops=flops / (attn_ms * 1e-3) / 1e12)
+    return res
+
+
+def split_fields(p) -> dict:
+    """The key-split entry point's figures of a prefill_case(split=True) result."""
+    return dict(attention_us=r(p["split_ms"] * 1e3, 2), tflops=round(p["split_tflops"], 1),
+                frac=r(p["split_tflops"] / FP16_MFMA_PEAK_TFLOPS), splits=p["splits"])
 
 
 def r(x, n=4):
@@ -583,18 +612,22 @@ def main():
         c = decode_case(torch, A, timer, heads=14, kv=2, d=64, layers=1, positions=[512], reps=reps)
         cfgs["0p5b_decode_pos512_1layer"] = dict(step_us=r(c["step_ms"] * 1e3, 2), splitk_us=r(c["splitk_ms"] * 1e3, 2))
         for L in (512, 2048):
-            p = prefill_case(torch, A, timer, heads=16, kv=2, d=128, tokens=L, reps=20)
+            p = prefill_case(torch, A, timer, heads=16, kv=2, d=128, tokens=L, reps=20, split=True)
             cfgs[f"3b_prefill_L{L}"] = dict(attention_us=r(p["attention_ms"] * 1e3, 2), tflops=round(p["tflops"], 1),
-                                            frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS))
-        p = prefill_case(torch, A, timer, heads=12, kv=2, d=128, tokens=2048, base=0, chunks=8, reps=3)
+                                            frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
+                                            split_entry=split_fields(p))
+        p = prefill_case(torch, A, timer, heads=12, kv=2, d=128, tokens=2048, base=0, chunks=8, reps=3, split=True)
         cfgs["1p5b_chunked_prefill_16k_from0"] = dict(chunks=8, chunk_tokens=2048, attention_ms=r(p["attention_ms"], 3),
                                                      tflops=round(p["tflops"], 1),
-                                                     frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS))
-        p = prefill_case(torch, A, timer, heads=12, kv=2, d=128, tokens=2048, base=131072, chunks=8, reps=2)
+                                                     frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
+                                                     split_entry=split_fields(p))
+        p = prefill_case(torch, A, timer, heads=12, kv=2, d=128, tokens=2048, base=131072, chunks=8, reps=2,
+                         split=True)
         cfgs["1p5b_chunked_prefill_16k_after128k"] = dict(chunks=8, chunk_tokens=2048, base=131072,
                                                          attention_ms=r(p["attention_ms"], 3),
                                                          tflops=round(p["tflops"], 1),
-                                                         frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS))
+                                                         frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
+                                                         split_entry=split_fields(p))
         line["configs"] = cfgs
     if not args.no_cpu_baseline:
         ql, kl, vl = dec["cpu_sample"]

@@ -197,6 +197,28 @@ TE_API te_status te_hip_attention_prefill_f16(
     float *out, void *stream);
 
 /*
+ * Key-split prefill: te_hip_attention_prefill_f16 for launches whose tile
+ * pairs alone would leave compute units idle (short prompts, few heads, or a
+ * chunk after a long cache).  Each (tile pair, head) is split over S key
+ * ranges; every split writes unnormalised partial rows to `workspace`, and a
+ * second launch merges them into `out`.  S is chosen from the shape and the
+ * device's compute-unit count; S == 1 is the plain kernel and then the
+ * workspace is not touched (it may be NULL).
+ * te_hip_attention_prefill_workspace_bytes returns the bytes needed (0 when
+ * S == 1 or the arguments are invalid): S*seqs*layers*tokens*heads*(head_dim+2)
+ * floats.  Arguments otherwise as te_hip_attention_prefill_f16.
+ * INVALID_ARGUMENT when the workspace is missing or too small.
+ */
+TE_API size_t te_hip_attention_prefill_workspace_bytes(size_t seqs, size_t layers, size_t tokens,
+                                                       size_t base_position, size_t context_tokens, size_t heads,
+                                                       size_t kv_heads, size_t head_dim);
+TE_API te_status te_hip_attention_prefill_split_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Fused prefill step: te_hip_rope_kv_append_f16 (tokens tokens at base_position)
  * followed by te_hip_attention_prefill_f16, as two launches: bias + RoPE + fp16
  * append of the chunk's k/v, then the causal attention, whose prologue applies

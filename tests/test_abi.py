@@ -126,6 +126,16 @@ def test_backend_guard_conventions(lib):
     assert lib.te_hip_attention_prefill_f16(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None) in ok
     assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 6, 8, 2, 1, 128, buf, None) == 1
     assert lib.te_hip_attention_prefill_f16(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None) == 3
+    assert lib.te_hip_attention_prefill_workspace_bytes(1, 1, 4, 6, 8, 2, 1, 128) == 0  # chunk past the cache
+    assert lib.te_hip_attention_prefill_workspace_bytes(1, 1, 4, 0, 8, 2, 1, 80) == 0  # head_dim 80
+    need = lib.te_hip_attention_prefill_workspace_bytes(1, 1, 300, 0, 300, 16, 2, 128)
+    assert need % (300 * 16 * 130 * 4) == 0  # splits x rows x heads x (head_dim + 2) floats
+    split = lib.te_hip_attention_prefill_split_f16
+    assert split(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None, 0, None) in ok
+    assert split(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None, 0, None) == 3  # head_dim 80
+    if need:
+        assert split(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, None, 0, None) == 1  # workspace missing
+        assert split(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, ws, need - 1, None) == 1  # too small
     step = lib.te_hip_attention_prefill_step_f16
     assert step(buf, None, buf, None, None, None, buf, buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128,
                 buf, None) == 1  # no k_new

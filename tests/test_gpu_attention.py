@@ -418,6 +418,48 @@ def test_prefill_vs_oracle(oracle_mod, h, kv, d, tokens, base):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("seqs,layers,h,kv,d,tokens,base", [
+    (1, 1, 16, 2, 128, 300, 0),      # 3 tiles: the lone middle tile and a pair, several splits
+    (1, 1, 16, 2, 128, 130, 200),    # chunk after a cached prefix
+    (1, 1, 16, 2, 128, 1, 0),        # one row
+    (1, 1, 14, 2, 64, 200, 37),      # head_dim 64
+    (2, 3, 12, 2, 128, 129, 1000),   # several (seq, layer) units, long prefix
+    (1, 1, 16, 2, 128, 2048, 0),     # BASELINE config 3 at L=2048
+])
+def test_prefill_split_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens, base):
+    """Key-split prefill (partials in a workspace, then the merge launch)
+    against the oracle for every row; the split count is the library's own
+    choice for the shape on this device and is printed.  Also the plain
+    kernel on the same inputs, and the workspace query."""
+    ctx = base + tokens + 3
+    tag = f"pfs{seqs}{layers}{h}{d}{tokens}{base}"
+    kc = S.to_f16_bits(S.normal(41, tag + "k", (seqs, layers, ctx, kv, d)))
+    vc = S.to_f16_bits(S.normal(41, tag + "v", (seqs, layers, ctx, kv, d)))
+    q16 = S.to_f16_bits(S.normal(41, tag + "q", (seqs, layers, tokens, h, d)))
+    lib = R.load_library()
+    nbytes = lib.te_hip_attention_prefill_workspace_bytes(seqs, layers, tokens, base, ctx, h, kv, d)
+    splits = nbytes // (seqs * layers * tokens * h * (d + 2) * 4) if nbytes else 1
+    assert nbytes == 0 or nbytes == splits * seqs * layers * tokens * h * (d + 2) * 4
+    qd, kd, vd = f16_dev(q16), f16_dev(kc), f16_dev(vc)
+    got = A.attention_prefill_split(qd, kd, vd, base_position=base).cpu().numpy()
+    plain = A.attention_prefill(qd, kd, vd, base_position=base).cpu().numpy()
+    worst = 0.0
+    for s_ in range(seqs):
+        for l_ in range(layers):
+            want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q16[s_, l_]).reshape(tokens, h, d),
+                                                kc[s_, l_].copy(), vc[s_, l_].copy(), tokens, base, ctx, h, kv, d)
+            worst = max(worst, maxabs(got[s_, l_], want.reshape(tokens, h, d)))
+    drift = float(np.abs(got - plain).max())
+    print(f"split prefill {seqs}x{layers} H{h} d{d} L{tokens} base{base}: {splits} splits, "
+          f"max abs err {worst:.3e}, vs plain kernel {drift:.3e}")
+    assert worst <= TOL
+    assert drift <= TOL
+    if nbytes:
+        with pytest.raises(R.TinyEngineError):
+            A.attention_prefill_split(qd, kd, vd, base_position=base,
+                                      workspace=torch.empty(nbytes - 4, dtype=torch.uint8, device=DEV))
+
+
 def test_prefill_several_sequences_and_layers(oracle_mod):
     """seqs x layers (seq, layer) units in one launch, each with its own data,
     chunk at base 50: every row of every unit against the oracle."""

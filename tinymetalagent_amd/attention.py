@@ -179,6 +179,34 @@ def attention_prefill(q_half, key_cache, value_cache, *, base_position: int = 0,
     return out
 
 
+def prefill_workspace(seqs: int, layers: int, tokens: int, heads: int, kv_heads: int, head_dim: int, *,
+                      base_position: int = 0, context_tokens: int, device="cuda") -> torch.Tensor | None:
+    """Workspace for attention_prefill_split (None when the launch does not split)."""
+    n = load_library().te_hip_attention_prefill_workspace_bytes(seqs, layers, tokens, base_position, context_tokens,
+                                                                heads, kv_heads, head_dim)
+    return None if n == 0 else torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def attention_prefill_split(q_half, key_cache, value_cache, *, base_position: int = 0, out: torch.Tensor | None = None,
+                            workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """attention_prefill with the key-split launch (partials in `workspace`, then a merge)."""
+    seqs, layers, tokens, heads, head_dim = q_half.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    _dtype(q_half, torch.float16, "q_half")
+    _dtype(key_cache, torch.float16, "key_cache")
+    _dtype(value_cache, torch.float16, "value_cache")
+    if out is None:
+        out = torch.empty(q_half.shape, dtype=torch.float32, device=q_half.device)
+    if workspace is None:
+        workspace = prefill_workspace(seqs, layers, tokens, heads, kv_heads, head_dim, base_position=base_position,
+                                      context_tokens=ctx, device=q_half.device)
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load_library().te_hip_attention_prefill_split_f16(
+        _ptr(q_half), _ptr(key_cache), _ptr(value_cache), seqs, layers, tokens, base_position, ctx, heads, kv_heads,
+        head_dim, _ptr(out), _ptr(workspace), nbytes, _stream(stream)))
+    return out
+
+
 def prefill_step(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_cache, *, base_position: int = 0,
                  q_bias=None, k_bias=None, v_bias=None, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Fused prefill step: bias + RoPE + fp16 append of the chunk's k/v, then causal

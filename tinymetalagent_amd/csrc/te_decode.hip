@@ -45,7 +45,7 @@
 namespace {
 
 constexpr int kTile = 32;               // positions per MFMA step
-constexpr int kWavesPerCU = 8;          // resident split-K waves per CU (2 per SIMD at its register use)
+constexpr int kTargetWaves2PerCU = 7;    // split-K waves per CU the chunking aims at, x2 (3.5)
 constexpr int kMaxCombineChunks = 4096;
 
 struct DecodeArgs {
@@ -633,11 +633,15 @@ int device_compute_units() {
 
 DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
                                size_t kv_heads) {
-    // One launch should give every resident wave slot about one chunk: the
-    // chunk is the total number of 32-position tiles over all (seq, layer,
-    // kv_head) streams divided by the slot count (CUs x kWavesPerCU), at least
-    // two tiles so the prefetch pipeline has work.  Balancing on the total
-    // rather than the longest sequence keeps ragged batches even.
+    // The chunk is the total number of 32-position tiles over all (seq,
+    // layer, kv_head) streams divided by a target of 3.5 single-wave
+    // workgroups per CU (at least two tiles, so the prefetch pipeline has
+    // work), then evened out so the longest stream's chunks are equal.
+    // Measured on MI355X (3B at 2K/8K/32K, 1.5B at 128K, 7B ragged x8): HBM
+    // efficiency is highest with about that many concurrent streams -- the
+    // 8 resident waves per CU the registers allow run 4-8 % slower -- and a
+    // short last chunk per stream costs a partly idle tail.  Balancing on the
+    // total rather than the longest sequence keeps ragged batches even.
     // TE_HIP_DECODE_CHUNK (a multiple of 32) overrides the choice.
     DecodeGeometry g;
     size_t max_n = 0, total_tiles = 0;
@@ -646,8 +650,14 @@ DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t 
         max_n = n > max_n ? n : max_n;
         total_tiles += layers * kv_heads * ((n + kTile - 1) / kTile);
     }
-    const size_t slots = (size_t)device_compute_units() * kWavesPerCU;
-    size_t tiles = (total_tiles + slots - 1) / slots;
+    const size_t target = (size_t)device_compute_units() * kTargetWaves2PerCU / 2;
+    size_t tiles = (total_tiles + target - 1) / target;
+    if (tiles < 2) {
+        tiles = 2;
+    }
+    const size_t max_tiles = (max_n + kTile - 1) / kTile;
+    const size_t n_longest = (max_tiles + tiles - 1) / tiles;  // chunks of the longest stream
+    tiles = (max_tiles + n_longest - 1) / n_longest;           // equal chunks for it
     if (tiles < 2) {
         tiles = 2;
     }

@@ -80,6 +80,9 @@ struct DecodeGeometry {
     int max_chunks;  // chunks of the longest sequence
 };
 
+// Compute units of the current device (256 when the query fails).
+int device_compute_units();
+
 DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
                                size_t kv_heads);
 

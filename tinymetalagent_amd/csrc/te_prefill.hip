@@ -36,6 +36,9 @@
 #include "te_hip_common.h"
 
 #include <math.h>
+#include <stdlib.h>
+
+#include <algorithm>
 
 #include <type_traits>
 
@@ -46,6 +49,7 @@ constexpr int BN = 64;    // keys per block
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr float kLazyLog2 = 8.0f;
+constexpr int kMaxPrefillSplits = 32;
 
 struct PrefillArgs {
     const f16 *q;            // fp16 rotated queries, or null when q32 is given
@@ -65,6 +69,9 @@ struct PrefillArgs {
     int group;
     int n_qtiles;
     float qscale;  // log2(e)/sqrt(D), applied to the fp32 scores
+    int splits;      // key splits: blockIdx.z = (seq*layers + layer) * splits + split
+    float *part_o;   // splits > 1: unnormalised O per (split, seq*layer, row, head), else null
+    float *part_ml;  // splits > 1: (m, l) per (split, seq*layer, row, head)
 };
 
 // Fused prefill step: query row `row` of (sl, layer) for head h, bias + RoPE at
@@ -191,7 +198,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
 
     const int pair = blockIdx.x;
     const int h = blockIdx.y;
-    const int sl = blockIdx.z;
+    const int sl = blockIdx.z / a.splits;
+    const int split = blockIdx.z % a.splits;
     const int kvh = h / a.group;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -235,12 +243,26 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     const int v_key = 4 * g + (c >> 2);
     const int v_off = HL::offset(v_key, 0) + 8 * (c & 3);        // + 16 rows (hi), 32 rows (ks), 32 B per t
 
-    stage_load(0, tile_kmax(long_tile), st0);  // every tile's first step is staged in st0
+    // Key split `split` of a tile takes its steps [lo, lo + cnt) (of 128 keys);
+    // with one split that is every step.  A tile's first step is staged in st0.
+    auto tile_steps = [&](int qt) __attribute__((always_inline)) { return (tile_kmax(qt) / BN + 2) / 2; };
+    auto split_lo = [&](int n) __attribute__((always_inline)) { return (int)((long long)split * n / a.splits); };
+    auto split_cnt = [&](int n) __attribute__((always_inline)) {
+        return (int)((long long)(split + 1) * n / a.splits) - split_lo(n);
+    };
+    if (split_cnt(tile_steps(long_tile)) > 0) {
+        stage_load(split_lo(tile_steps(long_tile)), tile_kmax(long_tile), st0);
+    }
     for (int ti = 0; ti < n_tiles_wg; ++ti) {
         const int qt = ti == 0 ? long_tile : pair;
         const int wr0 = qt * BM + 32 * (wave & 3);  // first row of this wave
         const int kmax = tile_kmax(qt);
-        const int n_steps = (kmax / BN + 2) / 2;    // ceil(blocks / 2)
+        const int n_all = tile_steps(qt);            // ceil(blocks / 2)
+        const int lo = split_lo(n_all);
+        const int cnt = split_cnt(n_all);
+        const int n_next = ti + 1 < n_tiles_wg ? tile_steps(pair) : 0;
+        const int lo_next = split_lo(n_next);
+        const int cnt_next = split_cnt(n_next);
 
         // Q^T operand for the wave's two 16-row blocks.
         f16x8 qop[2][KK];
@@ -397,18 +419,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         // Steps alternate st0 / st1 (the loop is unrolled by two so every
         // buffer reference is static); an odd step count gets one empty step,
         // so a tile always ends on st1, whose last step is done before the
-        // next tile's first DMA (into st0) is issued.
-        auto body = [&](auto tag, int step) {
+        // next tile's first DMA (into st0) is issued.  j counts this split's
+        // steps; the step index is lo + j.
+        auto body = [&](auto tag, int j) {
             constexpr int B = decltype(tag)::value;
             const unsigned char *cur = B == 0 ? st0 : st1;
             unsigned char *nxt = B == 0 ? st1 : st0;
-            if (step + 1 < n_steps) {
-                stage_load(step + 1, kmax, nxt);
-            } else if (B == 1 && ti + 1 < n_tiles_wg) {
-                stage_load(0, tile_kmax(pair), nxt);  // the next tile's first step, in flight across the merge
+            if (j + 1 < cnt) {
+                stage_load(lo + j + 1, kmax, nxt);
+            } else if (B == 1 && cnt_next > 0) {
+                stage_load(lo_next, tile_kmax(pair), nxt);  // the next tile's first step, in flight across the merge
             }
-            const int kb0 = (2 * step + half) * BN;
-            if (step < n_steps && wave_active && kb0 <= wave_max_pos) {
+            const int kb0 = (2 * (lo + j) + half) * BN;
+            if (j < cnt && wave_active && kb0 <= wave_max_pos) {
                 if (kb0 + BN - 1 > wave_min_pos) {
                     compute(std::true_type(), kb0, cur + half * HB, cur + (2 + half) * HB);  // diagonal block
                 } else {
@@ -420,9 +443,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         };
         stage_wait();
         __syncthreads();
-        for (int step = 0; step < n_steps; step += 2) {
-            body(std::integral_constant<int, 0>(), step);
-            body(std::integral_constant<int, 1>(), step + 1);
+        for (int j = 0; j < cnt; j += 2) {
+            body(std::integral_constant<int, 0>(), j);
+            body(std::integral_constant<int, 1>(), j + 1);
+        }
+        if (cnt == 0 && cnt_next > 0) {
+            stage_load(lo_next, tile_kmax(pair), st0);  // nothing of this tile was staged: st0 is free
         }
 
         // ---- merge the two key halves through LDS, normalise, store ----
@@ -451,7 +477,23 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             const float s2 = m2 == mn ? 1.0f : fast_exp2(m2 - mn);
             const float ltot = xor_sum_16_32(lsum * s1 + l2 * s2);
             const int row = wr0 + 16 * nb + c;
-            if (row < a.tokens) {
+            if (row < a.tokens && a.part_o != nullptr) {
+                // key split: O relative to the row maximum mn, unnormalised, with (mn, l)
+                const size_t pi = ((size_t)blockIdx.z * a.tokens + row) * a.heads + h;
+                float *prow = a.part_o + pi * D;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    float4 v;
+                    v.x = ob[t][0] * s1 + src[(4 * t + 0) * 64] * s2;
+                    v.y = ob[t][1] * s1 + src[(4 * t + 1) * 64] * s2;
+                    v.z = ob[t][2] * s1 + src[(4 * t + 2) * 64] * s2;
+                    v.w = ob[t][3] * s1 + src[(4 * t + 3) * 64] * s2;
+                    *reinterpret_cast<float4 *>(prow + 16 * t + 4 * g) = v;
+                }
+                if (g == 0) {
+                    *reinterpret_cast<float2 *>(a.part_ml + 2 * pi) = make_float2(mn, ltot);
+                }
+            } else if (row < a.tokens) {
                 const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
                 const float w1 = s1 * inv;
                 const float w2 = s2 * inv;
@@ -482,6 +524,43 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     }
 }
 
+// Key-split merge: out[row][h] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s
+// over the splits of one (seq*layer); M = max_s m_s.  A split that saw no
+// unmasked key of the row has m_s = -inf and weight 0 (split 0 always holds
+// key 0).  Thread (item, col) handles 4 dims of one (row, head).
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float *part_o, const float *part_ml, int splits,
+                                                           int items, float *out) {
+    constexpr int COLS = D / 4;
+    constexpr int ITEMS = 256 / COLS;
+    const int item = blockIdx.x * ITEMS + (int)threadIdx.x / COLS;
+    const int col = threadIdx.x % COLS;
+    if (item >= items) {
+        return;
+    }
+    const size_t sl = blockIdx.y;
+    float m = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) {
+        m = fmaxf(m, part_ml[2 * ((sl * splits + sp) * items + item)]);
+    }
+    float den = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int sp = 0; sp < splits; ++sp) {
+        const size_t pi = (sl * splits + sp) * items + item;
+        const float2 ml = *reinterpret_cast<const float2 *>(part_ml + 2 * pi);
+        const float w = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - m);
+        const float4 o = reinterpret_cast<const float4 *>(part_o + pi * D)[col];
+        den += w * ml.y;
+        acc.x += w * o.x;
+        acc.y += w * o.y;
+        acc.z += w * o.z;
+        acc.w += w * o.w;
+    }
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    reinterpret_cast<float4 *>(out + (sl * items + item) * D)[col] =
+        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+}
+
 }  // namespace
 
 namespace {
@@ -497,8 +576,11 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
     a.group = (int)(heads / kv_heads);
     a.n_qtiles = (int)((tokens + BM - 1) / BM);
     a.qscale = TE_LOG2E / sqrtf((float)head_dim);
+    if (a.splits < 1) {
+        a.splits = 1;
+    }
     const int n_pairs = (a.n_qtiles + 1) / 2;
-    const dim3 grid((unsigned)n_pairs, (unsigned)heads, (unsigned)(seqs * layers));
+    const dim3 grid((unsigned)n_pairs, (unsigned)heads, (unsigned)(seqs * layers * a.splits));
     hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
         prefill_causal_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
@@ -506,6 +588,53 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
         prefill_causal_f16_kernel<64><<<grid, kThreads, 0, strm>>>(a);
     }
     return te_hip::launch_status();
+}
+
+// Key splits for a launch whose tile pairs alone leave CUs idle.  One
+// workgroup fills a CU (its LDS), every pair carries the same causal work
+// (~ the steps of tiles n-1-i and i), and a launch of W workgroups runs in
+// ceil(W / CUs) rounds, so S splits take ceil(S*W0 / CUs) * ceil(steps / S)
+// step times (a step, 128 keys for 256 rows, is ~2.5 us).  The merge costs a
+// launch (~2 steps) plus writing and reading every split's partial rows,
+// priced at 8 TB/s (fitted on MI355X over 3B L = 512..4096 and 1.5B 2K chunks
+// at bases 0..131072: it picks the fastest measured S or one within 4 %).
+// The smallest S with the least time wins; S = 1 whenever the pairs fill the
+// device.  TE_HIP_PREFILL_SPLITS (1..32) overrides the choice.
+int prefill_splits(size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t heads,
+                   size_t head_dim) {
+    const size_t n_qtiles = (tokens + BM - 1) / BM;
+    const size_t w0 = (n_qtiles + 1) / 2 * heads * seqs * layers;
+    const size_t cus = (size_t)te_hip::device_compute_units();
+    auto tile_steps = [&](size_t qt) {
+        const size_t kmax = base_position + std::min(qt * BM + BM, tokens) - 1;
+        return (kmax / BN + 2) / 2;
+    };
+    const size_t steps = tile_steps(n_qtiles - 1) + (n_qtiles > 1 ? tile_steps(0) : 0);
+    const char *env = getenv("TE_HIP_PREFILL_SPLITS");
+    if (env != nullptr) {
+        const long v = strtol(env, nullptr, 10);
+        if (v >= 1 && v <= kMaxPrefillSplits && (size_t)v * seqs * layers <= 65535) {
+            return (int)v;
+        }
+    }
+    // partial bytes of one split, written then read, in step times
+    const double split_steps = (double)(seqs * layers * tokens * heads * (head_dim + 2) * sizeof(float)) * 2.0 /
+                               (8.0e12 * 2.5e-6);
+    int best = 1;
+    double best_t = (double)((w0 + cus - 1) / cus * steps);
+    for (int sp = 2; sp <= kMaxPrefillSplits && (size_t)sp <= steps; ++sp) {
+        const double t =
+            (double)((sp * w0 + cus - 1) / cus * ((steps + sp - 1) / sp)) + 2.0 + split_steps * (double)sp;
+        if (t < best_t && (size_t)sp * seqs * layers <= 65535) {
+            best_t = t;
+            best = sp;
+        }
+    }
+    return best;
+}
+
+size_t prefill_workspace(int splits, size_t seqs, size_t layers, size_t tokens, size_t heads, size_t head_dim) {
+    return splits <= 1 ? 0 : (size_t)splits * seqs * layers * tokens * heads * (head_dim + 2) * sizeof(float);
 }
 
 te_status check_prefill_args(size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
@@ -545,6 +674,61 @@ extern "C" te_status te_hip_attention_prefill_f16(
     a.value_cache = reinterpret_cast<const f16 *>(value_cache);
     a.out = out;
     return launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
+}
+
+extern "C" size_t te_hip_attention_prefill_workspace_bytes(size_t seqs, size_t layers, size_t tokens,
+                                                          size_t base_position, size_t context_tokens, size_t heads,
+                                                          size_t kv_heads, size_t head_dim) {
+    if (check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim) !=
+        TE_STATUS_OK) {
+        return 0;
+    }
+    const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
+    return prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
+}
+
+extern "C" te_status te_hip_attention_prefill_split_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    if (q_half == nullptr || key_cache == nullptr || value_cache == nullptr || out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_status st = check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
+    const size_t need = prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    PrefillArgs a = {};
+    a.q = reinterpret_cast<const f16 *>(q_half);
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
+    a.out = out;
+    a.splits = splits;
+    if (splits > 1) {
+        const size_t parts = (size_t)splits * seqs * layers * tokens * heads;
+        a.part_o = static_cast<float *>(workspace);
+        a.part_ml = a.part_o + parts * head_dim;
+    }
+    st = launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
+    if (st != TE_STATUS_OK || splits == 1) {
+        return st;
+    }
+    const int items = (int)(tokens * heads);
+    const int per_block = 256 / (int)(head_dim / 4);
+    const dim3 grid((unsigned)((items + per_block - 1) / per_block), (unsigned)(seqs * layers));
+    hipStream_t strm = te_hip::as_stream(stream);
+    if (head_dim == 128) {
+        prefill_merge_kernel<128><<<grid, 256, 0, strm>>>(a.part_o, a.part_ml, splits, items, out);
+    } else {
+        prefill_merge_kernel<64><<<grid, 256, 0, strm>>>(a.part_o, a.part_ml, splits, items, out);
+    }
+    return te_hip::launch_status();
 }
 
 extern "C" te_status te_hip_attention_prefill_step_f16(
