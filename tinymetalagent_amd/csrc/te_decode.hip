@@ -32,8 +32,8 @@
 //               straight to the partial with 16-byte stores.
 // The next tile's loads are issued before the current tile is consumed (two
 // register tiles, 32 KB in flight per wave).  The chunk length is chosen from
-// the total tile count so one launch gives every wave slot about one chunk,
-// which also balances ragged sequence lengths.
+// the total tile count (about 3.5 single-wave workgroups per CU, chunks evened
+// out per stream), which also balances ragged sequence lengths.
 //
 // HBM bytes per (seq, layer), the roofline unit: 2*(pos+1)*kv_heads*D*2 B of
 // K/V + heads*D*4 B of q; partials add (chunks*heads*(D+2)*4 B) x2.

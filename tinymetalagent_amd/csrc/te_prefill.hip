@@ -6,14 +6,16 @@
 // (metal_kernels.metal.inc:2767-2775), which also defines chunked prefill.
 //
 // Work decomposition.  Query rows are cut into tiles of BM (128) rows.  One
-// workgroup = 8 waves = the PAIR of tiles (n-1-i, i) of one head: waves 0-3 own
-// the long tile n-1-i, waves 4-7 the short tile i (32 rows per wave, two
-// 16-row MFMA column blocks).  The short tile's key range is a prefix of the
-// long tile's, so one LDS stream of K/V blocks serves both (256 rows per
-// staged block while both are active), and every workgroup does the same
-// causal work ((n+1) tiles' worth of blocks).  K/V blocks of BN (64) positions
-// of the head's KV group are double-buffered in LDS: the global loads of block
-// b+1 are in flight while block b is consumed, one barrier per block.
+// workgroup = 8 waves (two per SIMD) = the PAIR of tiles (n-1-i, i) of one
+// head, processed one after the other, so every workgroup does the same causal
+// work ((n+1) tiles' worth of key blocks).  Within a tile, wave w owns 32 rows
+// (32*(w&3), two 16-row MFMA column blocks) and key half w>>2: a step of 128
+// keys is two BN (64) key blocks, block 2*step + half for each wave, and the
+// two halves' softmax states merge through LDS at the end of the tile.  The
+// K/V of each step reach LDS by global_load_lds DMA, double-buffered: the
+// DMA of step s+1 is in flight while step s is consumed, one barrier per step.
+// A key split (te_hip_attention_prefill_split_f16) gives each workgroup a
+// range of the steps and writes unnormalised partial rows instead.
 //
 //   S^T[64 keys x 32 rows] = K[64 x D] . Q^T[D x 32]            fp16 MFMA 16x16x32
 //   O^T[D x 32 rows]      += V^T[D x 64] . P^T[64 x 32]         fp16 MFMA 16x16x32
