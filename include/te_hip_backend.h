@@ -262,6 +262,31 @@ TE_API te_status te_hip_attention_causal_mma_f32(const float *query, const float
                                                  float *out);
 
 /*
+ * Decode-layer vector operations around attention (device pointers, async on
+ * `stream`).  te_hip_matvec_f32 replaces te_metal_matvec_f32
+ * (metal_backend.h:13-22) for weights already in HBM: `weights` points at the
+ * tensor data (the GGUF mapping + tensor offset of the reference, uploaded),
+ * out[r] = sum_c W[r][c] * input[c] for a [rows][cols] tensor of GGUF type
+ * ggml_type: 0 = F32 (cols % 4 == 0), 2 = Q4_0 and 8 = Q8_0 (cols % 32 == 0;
+ * rows of cols/32 blocks of 18 / 34 bytes, ops.c:15-21); other types ->
+ * UNSUPPORTED.  Results equal the reference's te_model_matvec_f32 within fp32
+ * rounding of the row's terms (the summation order differs).
+ * The others are the reference ops.c functions (te_rmsnorm_f32 :272-293,
+ * te_swiglu_f32 :397-406, te_add_f32 :408-416, te_argmax_f32 :418-433) on
+ * device arrays, with the same argument checks; te_hip_rmsnorm_f32 normalises
+ * `rows` rows of `len` each; te_hip_argmax_f32 writes the index to DEVICE
+ * memory.  The argmax is exact (first maximum, NaN never taken); add is exact;
+ * RMSNorm sums squares in fp64 like the reference; SwiGLU uses the device expf.
+ */
+TE_API te_status te_hip_matvec_f32(const void *weights, uint32_t ggml_type, const float *input, size_t cols,
+                                   size_t rows, float *out, void *stream);
+TE_API te_status te_hip_rmsnorm_f32(const float *input, const float *weight, size_t rows, size_t len,
+                                    float epsilon, float *out, void *stream);
+TE_API te_status te_hip_swiglu_f32(const float *gate, const float *up, size_t len, float *out, void *stream);
+TE_API te_status te_hip_add_f32(const float *lhs, const float *rhs, size_t len, float *out, void *stream);
+TE_API te_status te_hip_argmax_f32(const float *values, size_t len, uint32_t *out_index, void *stream);
+
+/*
  * Measurement only, no counterpart in the reference: `blocks` workgroups of 8
  * waves each run `iters` rounds of 8 independent fp16 16x16x32 MFMAs on
  * register operands (blocks*8*iters*8*16384 FLOP), so a benchmark can report

@@ -24,6 +24,8 @@ REF_LIB = HERE / "_ref" / "libte_ref_ops.so"
 REFERENCE_TREE = Path(os.environ.get("TE_REFERENCE_TREE", "/root/reference"))
 
 _f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _szp = ctypes.POINTER(ctypes.c_size_t)
 _sz = ctypes.c_size_t
@@ -70,6 +72,11 @@ def lib() -> ctypes.CDLL:
                                                  _sz, _f32p]
         l.orc_attention_prefill.argtypes = [_f32p, _u16p, _u16p, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz,
                                             _sz, _f32p]
+        _bind_vector_ops(l, "orc_")
+        l.orc_ggml_row_bytes.argtypes = [ctypes.c_uint32, _sz]
+        l.orc_ggml_row_bytes.restype = _sz
+        l.orc_dequantize_row_f32.argtypes = [_u8p, ctypes.c_uint32, _sz, _sz, _f32p]
+        l.orc_matvec_f32.argtypes = [_u8p, ctypes.c_uint32, _f32p, _sz, _sz, _f32p]
         _oracle = l
     return _oracle
 
@@ -83,8 +90,19 @@ def ref_lib() -> ctypes.CDLL | None:
         l.te_rope_f32.restype = ctypes.c_int
         l.te_attention_decode_f32.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _f32p]
         l.te_attention_decode_f32.restype = ctypes.c_int
+        _bind_vector_ops(l, "te_")
         _ref = l
     return _ref
+
+
+def _bind_vector_ops(l: ctypes.CDLL, prefix: str) -> None:
+    for name, args in (("rmsnorm_f32", [_f32p, _f32p, _sz, ctypes.c_float, _f32p]),
+                       ("swiglu_f32", [_f32p, _f32p, _sz, _f32p]),
+                       ("add_f32", [_f32p, _f32p, _sz, _f32p]),
+                       ("argmax_f32", [_f32p, _sz, _u32p])):
+        fn = getattr(l, prefix + name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
 
 
 def _check(status: int, what: str) -> None:
@@ -190,3 +208,69 @@ def attention_prefill(query, key_cache, value_cache, tokens, base_position, cont
         tokens, base_position, context_tokens, heads, kv_heads, head_dim, row_begin, row_end, row_step,
         _p(out, _f32p)), "attention_prefill")
     return out.reshape(tokens, heads, head_dim)
+
+
+# ---- decode-layer vector operations ------------------------------------------
+
+def _vec_lib(use_ref: bool):
+    return (ref_lib(), "te_") if use_ref else (lib(), "orc_")
+
+
+def rmsnorm_f32(x, weight, epsilon, *, use_ref=False):
+    l, pre = _vec_lib(use_ref)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    out = np.empty_like(x)
+    _check(getattr(l, pre + "rmsnorm_f32")(_p(x, _f32p), _p(w, _f32p), x.size, ctypes.c_float(epsilon),
+                                          _p(out, _f32p)), "rmsnorm_f32")
+    return out
+
+
+def swiglu_f32(gate, up, *, use_ref=False):
+    l, pre = _vec_lib(use_ref)
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.empty_like(g)
+    _check(getattr(l, pre + "swiglu_f32")(_p(g, _f32p), _p(u, _f32p), g.size, _p(out, _f32p)), "swiglu_f32")
+    return out
+
+
+def add_f32(lhs, rhs, *, use_ref=False):
+    l, pre = _vec_lib(use_ref)
+    a = np.ascontiguousarray(lhs, dtype=np.float32)
+    b = np.ascontiguousarray(rhs, dtype=np.float32)
+    out = np.empty_like(a)
+    _check(getattr(l, pre + "add_f32")(_p(a, _f32p), _p(b, _f32p), a.size, _p(out, _f32p)), "add_f32")
+    return out
+
+
+def argmax_f32(values, *, use_ref=False) -> int:
+    l, pre = _vec_lib(use_ref)
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    idx = ctypes.c_uint32(0)
+    _check(getattr(l, pre + "argmax_f32")(_p(v, _f32p), v.size, ctypes.byref(idx)), "argmax_f32")
+    return int(idx.value)
+
+
+GGML_F32, GGML_Q4_0, GGML_Q8_0 = 0, 2, 8
+
+
+def ggml_row_bytes(ggml_type: int, cols: int) -> int:
+    return int(lib().orc_ggml_row_bytes(ggml_type, cols))
+
+
+def dequantize_rows(data, ggml_type: int, cols: int, rows: int) -> np.ndarray:
+    """All rows of a tensor as fp32 [rows][cols]."""
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty((rows, cols), dtype=np.float32)
+    for r in range(rows):
+        _check(lib().orc_dequantize_row_f32(_p(d, _u8p), ggml_type, cols, r, _p(out[r], _f32p)), "dequantize_row")
+    return out
+
+
+def matvec_f32(data, ggml_type: int, x, cols: int, rows: int) -> np.ndarray:
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(rows, dtype=np.float32)
+    _check(lib().orc_matvec_f32(_p(d, _u8p), ggml_type, _p(x, _f32p), cols, rows, _p(out, _f32p)), "matvec_f32")
+    return out

@@ -370,3 +370,167 @@ int orc_attention_prefill(const float *query, const uint16_t *key_cache, const u
     free(vf);
     return status;
 }
+
+/* ---- decode-layer vector operations ---- */
+
+/* Restates te_rmsnorm_f32 (reference c/src/ops.c:272-293): sum of squares in
+ * double, one float scale 1/sqrtf(mean + eps), then input * scale * weight. */
+int orc_rmsnorm_f32(const float *input, const float *weight, size_t len, float epsilon, float *out) {
+    if (input == NULL || weight == NULL || out == NULL || len == 0u || epsilon <= 0.0f) {
+        return ORC_INVALID_ARGUMENT;
+    }
+    double sum_squares = 0.0;
+    for (size_t i = 0; i < len; ++i) {
+        const double value = (double)input[i];
+        sum_squares += value * value;
+    }
+    const float scale = 1.0f / sqrtf((float)(sum_squares / (double)len) + epsilon);
+    for (size_t i = 0; i < len; ++i) {
+        out[i] = input[i] * scale * weight[i];
+    }
+    return ORC_OK;
+}
+
+/* Restates te_swiglu_f32 (ops.c:397-406): silu(gate) * up with
+ * silu(g) = g / (1 + expf(-g)). */
+int orc_swiglu_f32(const float *gate, const float *up, size_t len, float *out) {
+    if (gate == NULL || up == NULL || out == NULL || len == 0u) {
+        return ORC_INVALID_ARGUMENT;
+    }
+    for (size_t i = 0; i < len; ++i) {
+        const float silu = gate[i] / (1.0f + expf(-gate[i]));
+        out[i] = silu * up[i];
+    }
+    return ORC_OK;
+}
+
+/* Restates te_add_f32 (ops.c:408-416). */
+int orc_add_f32(const float *lhs, const float *rhs, size_t len, float *out) {
+    if (lhs == NULL || rhs == NULL || out == NULL || len == 0u) {
+        return ORC_INVALID_ARGUMENT;
+    }
+    for (size_t i = 0; i < len; ++i) {
+        out[i] = lhs[i] + rhs[i];
+    }
+    return ORC_OK;
+}
+
+/* Restates te_argmax_f32 (ops.c:418-433): the first index whose value is
+ * greater than every earlier one, starting from -FLT_MAX; NaN is never taken,
+ * and an all -inf / NaN vector gives index 0. */
+int orc_argmax_f32(const float *values, size_t len, uint32_t *out_index) {
+    if (values == NULL || out_index == NULL || len == 0u || len > UINT32_MAX) {
+        return ORC_INVALID_ARGUMENT;
+    }
+    float best = -FLT_MAX;
+    uint32_t best_index = 0;
+    for (size_t i = 0; i < len; ++i) {
+        if (values[i] > best) {
+            best = values[i];
+            best_index = (uint32_t)i;
+        }
+    }
+    *out_index = best_index;
+    return ORC_OK;
+}
+
+static uint16_t orc_read_u16_le(const uint8_t *b) { return (uint16_t)(b[0] | (b[1] << 8)); }
+
+static float orc_read_f32_le(const uint8_t *b) {
+    const uint32_t bits = (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
+    float v;
+    memcpy(&v, &bits, sizeof(v));
+    return v;
+}
+
+/* Bytes of one row (ops.c:217-264: blocks_per_row * block bytes, or cols * 4). */
+size_t orc_ggml_row_bytes(uint32_t ggml_type, size_t cols) {
+    switch (ggml_type) {
+        case ORC_GGML_Q4_0:
+            return cols % 32u == 0u ? cols / 32u * 18u : 0u;
+        case ORC_GGML_Q8_0:
+            return cols % 32u == 0u ? cols / 32u * 34u : 0u;
+        case ORC_GGML_F32:
+            return cols * sizeof(float);
+        default:
+            return 0u;
+    }
+}
+
+/* Restates te_dequantize_q4_0_row / _q8_0_row / _f32_row (ops.c:505-582). */
+int orc_dequantize_row_f32(const uint8_t *data, uint32_t ggml_type, size_t cols, size_t row, float *out) {
+    const size_t row_bytes = orc_ggml_row_bytes(ggml_type, cols);
+    if (data == NULL || out == NULL || row_bytes == 0u) {
+        return ORC_UNSUPPORTED;
+    }
+    const uint8_t *r = data + row * row_bytes;
+    if (ggml_type == ORC_GGML_F32) {
+        for (size_t col = 0; col < cols; ++col) {
+            out[col] = orc_read_f32_le(r + col * sizeof(float));
+        }
+        return ORC_OK;
+    }
+    for (size_t block = 0; block < cols / 32u; ++block) {
+        if (ggml_type == ORC_GGML_Q4_0) {
+            const uint8_t *src = r + block * 18u;
+            const float scale = orc_f16_to_f32(orc_read_u16_le(src));
+            const uint8_t *qs = src + 2u;
+            for (size_t j = 0; j < 16u; ++j) {
+                out[block * 32u + j] = ((float)(qs[j] & 0x0fu) - 8.0f) * scale;
+                out[block * 32u + j + 16u] = ((float)(qs[j] >> 4u) - 8.0f) * scale;
+            }
+        } else {
+            const uint8_t *src = r + block * 34u;
+            const float scale = orc_f16_to_f32(orc_read_u16_le(src));
+            const int8_t *qs = (const int8_t *)(src + 2u);
+            for (size_t j = 0; j < 32u; ++j) {
+                out[block * 32u + j] = (float)qs[j] * scale;
+            }
+        }
+    }
+    return ORC_OK;
+}
+
+/* Restates te_model_matvec_f32's row loop (ops.c:177-269, te_matvec_worker
+ * :828-845) with the portable dot products te_q4_0_dot_row / te_q8_0_dot_row /
+ * te_f32_dot_row (ops.c:584-629, the non-NEON branches): one fp32 sum per row,
+ * element by element in column order, each term (code * scale) * x. */
+int orc_matvec_f32(const uint8_t *data, uint32_t ggml_type, const float *input, size_t cols, size_t rows,
+                   float *out) {
+    const size_t row_bytes = orc_ggml_row_bytes(ggml_type, cols);
+    if (data == NULL || input == NULL || out == NULL || row_bytes == 0u) {
+        return ORC_UNSUPPORTED;
+    }
+    for (size_t row = 0; row < rows; ++row) {
+        const uint8_t *r = data + row * row_bytes;
+        float sum = 0.0f;
+        if (ggml_type == ORC_GGML_F32) {
+            for (size_t col = 0; col < cols; ++col) {
+                sum += orc_read_f32_le(r + col * sizeof(float)) * input[col];
+            }
+        } else if (ggml_type == ORC_GGML_Q4_0) {
+            for (size_t block = 0; block < cols / 32u; ++block) {
+                const uint8_t *src = r + block * 18u;
+                const float scale = orc_f16_to_f32(orc_read_u16_le(src));
+                const uint8_t *qs = src + 2u;
+                const float *x = input + block * 32u;
+                for (size_t j = 0; j < 16u; ++j) {
+                    sum += (((float)(qs[j] & 0x0fu) - 8.0f) * scale) * x[j];
+                    sum += (((float)(qs[j] >> 4u) - 8.0f) * scale) * x[j + 16u];
+                }
+            }
+        } else {
+            for (size_t block = 0; block < cols / 32u; ++block) {
+                const uint8_t *src = r + block * 34u;
+                const float scale = orc_f16_to_f32(orc_read_u16_le(src));
+                const int8_t *qs = (const int8_t *)(src + 2u);
+                const float *x = input + block * 32u;
+                for (size_t j = 0; j < 32u; ++j) {
+                    sum += ((float)qs[j] * scale) * x[j];
+                }
+            }
+        }
+        out[row] = sum;
+    }
+    return ORC_OK;
+}

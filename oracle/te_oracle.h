@@ -26,6 +26,12 @@
  *                         bit-exact vs orc_rope_cached
  *   orc_attention_decode_f16kv / orc_attention_prefill  compositions of the
  *                         pinned functions above (row t == decode at base+t)
+ *   orc_rmsnorm_f32, orc_swiglu_f32, orc_add_f32, orc_argmax_f32
+ *                         compiled reference ops.c (bit-exact), closed forms
+ *   orc_dequantize_row_f32  closed forms: every 4-bit / 8-bit code times the
+ *                         block scale, exhaustively per code
+ *   orc_matvec_f32        fp64 brute force over the dequantized rows, and
+ *                         equality with dequantize + te_f32 dot for F32
  */
 #ifndef TE_ORACLE_H
 #define TE_ORACLE_H
@@ -70,6 +76,25 @@ int orc_attention_prefill(const float *query, const uint16_t *key_cache, const u
                           size_t tokens, size_t base_position, size_t context_tokens, size_t heads,
                           size_t kv_heads, size_t head_dim, size_t row_begin, size_t row_end,
                           size_t row_step, float *out);
+
+/* Decode-layer vector operations (reference c/src/ops.c:272-433). */
+int orc_rmsnorm_f32(const float *input, const float *weight, size_t len, float epsilon, float *out);
+int orc_swiglu_f32(const float *gate, const float *up, size_t len, float *out);
+int orc_add_f32(const float *lhs, const float *rhs, size_t len, float *out);
+int orc_argmax_f32(const float *values, size_t len, uint32_t *out_index);
+
+/* GGUF tensor types of the reference matvec (ops.c:15-21): F32 = 0, Q4_0 = 2
+ * (18-byte blocks of 32: f16 scale + 16 bytes of 4-bit codes, low nibbles are
+ * elements 0-15, high nibbles 16-31, value (code - 8) * scale), Q8_0 = 8
+ * (34-byte blocks: f16 scale + 32 int8 codes).  Rows are `cols` elements,
+ * stored back to back. */
+#define ORC_GGML_F32 0u
+#define ORC_GGML_Q4_0 2u
+#define ORC_GGML_Q8_0 8u
+size_t orc_ggml_row_bytes(uint32_t ggml_type, size_t cols);
+int orc_dequantize_row_f32(const uint8_t *data, uint32_t ggml_type, size_t cols, size_t row, float *out);
+int orc_matvec_f32(const uint8_t *data, uint32_t ggml_type, const float *input, size_t cols, size_t rows,
+                   float *out);
 
 #ifdef __cplusplus
 }

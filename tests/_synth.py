@@ -52,3 +52,27 @@ def outlier_keys(seed: int, tag: str, shape, channels: int = 3, spike: float = 2
         signs = r.choice(np.array([-1.0, 1.0], dtype=np.float32), size=shape[:-2] + (channels,))
         k[..., h, ch] += spike * signs
     return k
+
+
+def ggml_tensor(seed: int, tag: str, ggml_type: int, rows: int, cols: int, scale: float = 0.02) -> np.ndarray:
+    """Random GGUF tensor bytes [rows * row_bytes] in the block formats of the
+    reference matvec (ops.c:15-21): F32 = 0 (plain floats), Q4_0 = 2 (f16 scale +
+    16 bytes of 4-bit codes), Q8_0 = 8 (f16 scale + 32 int8 codes).  Scales are
+    positive and negative fp16 values around `scale`; codes are uniform."""
+    r = rng(seed, tag)
+    if ggml_type == 0:
+        return (r.standard_normal((rows, cols)) * scale).astype(np.float32).reshape(-1).view(np.uint8).copy()
+    blocks = rows * (cols // 32)
+    d = (r.standard_normal(blocks) * scale).astype(np.float16).view(np.uint16)
+    if ggml_type == 2:
+        codes = r.integers(0, 256, size=(blocks, 16), dtype=np.uint8)
+        out = np.empty((blocks, 18), dtype=np.uint8)
+    elif ggml_type == 8:
+        codes = r.integers(0, 256, size=(blocks, 32), dtype=np.uint8)
+        out = np.empty((blocks, 34), dtype=np.uint8)
+    else:
+        raise ValueError(ggml_type)
+    out[:, 0] = d & 0xFF
+    out[:, 1] = d >> 8
+    out[:, 2:] = codes
+    return out.reshape(-1)

@@ -71,7 +71,12 @@ def test_defaults_and_capabilities():
     o = runtime._RuntimeOptions(abi_version=3, context_tokens=8192)
     runtime.check(lib.te_make_kernel_plan(ctypes.byref(o), ctypes.byref(plan)))
     assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), runtime.TE_OP_CAUSAL_ATTENTION) == 1
-    assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), 0) == 0
+    for op in (0, 4, 7, 8, 9):  # matvec, RMSNorm, SwiGLU, residual add, argmax
+        assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), op) == 1
+    for op in (1, 3, 10, 12):  # matmul, decode token, sampling, tokenize: not in this build
+        assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), op) == 0
+    for quant, want in ((1, 1), (2, 1), (4, 1), (8, 1), (5, 0), (11, 0)):  # F32 F16 Q4_0 Q8_0 | Q4_1 Q4_K
+        assert lib.te_kernel_plan_supports_quant(ctypes.byref(plan), quant) == want
     assert plan.max_context_tokens == 8192
     o.abi_version = 2
     assert lib.te_make_kernel_plan(ctypes.byref(o), ctypes.byref(plan)) == runtime.TE_STATUS_UNSUPPORTED
@@ -89,6 +94,27 @@ def test_public_attention_argument_checks(lib):
     assert lib.te_attention_decode_f32(p, p, p, 0, 3, 2, 4, p) == 1
     assert lib.te_attention_decode_f32(None, p, p, 0, 2, 1, 4, p) == 1
     assert lib.te_attention_decode_f32(p, p, p, 2 ** 64 - 1, 2, 1, 4, p) == 3
+
+
+def test_public_vector_op_argument_checks(lib):
+    """The reference checks of ops.c:272-433 before any device work."""
+    f = np.ones(8, np.float32)
+    p = f.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    idx = ctypes.c_uint32(0)
+    assert lib.te_rmsnorm_f32(None, p, 8, ctypes.c_float(1e-6), p) == 1
+    assert lib.te_rmsnorm_f32(p, p, 0, ctypes.c_float(1e-6), p) == 1
+    assert lib.te_rmsnorm_f32(p, p, 8, ctypes.c_float(0.0), p) == 1  # epsilon <= 0
+    assert lib.te_swiglu_f32(p, None, 8, p) == 1
+    assert lib.te_add_f32(p, p, 0, p) == 1
+    assert lib.te_argmax_f32(p, 0, ctypes.byref(idx)) == 1
+    assert lib.te_argmax_f32(p, 8, None) == 1
+    buf = ctypes.c_void_p(0x1000)  # never dereferenced: every call fails its checks first
+    assert lib.te_hip_matvec_f32(buf, 2, buf, 48, 4, buf, None) == 3  # cols not a multiple of 32
+    assert lib.te_hip_matvec_f32(buf, 14, buf, 64, 4, buf, None) == 3  # Q8_K: not here
+    assert lib.te_hip_matvec_f32(buf, 0, buf, 6, 4, buf, None) == 3  # F32 cols % 4
+    assert lib.te_hip_matvec_f32(buf, 2, buf, 64, 0, buf, None) == 1
+    assert lib.te_hip_rmsnorm_f32(buf, buf, 1, 8, ctypes.c_float(-1.0), buf, None) == 1
+    assert lib.te_hip_argmax_f32(buf, 0, buf, None) == 1
 
 
 def test_backend_guard_conventions(lib):

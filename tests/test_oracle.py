@@ -326,3 +326,80 @@ def test_decode_f16kv_indexing(oracle_mod):
             want = oracle_mod.attention_decode_f32(q[s, layer].reshape(-1), S.f16_bits_to_f32(kc[s, layer]),
                                                    S.f16_bits_to_f32(vc[s, layer]), positions[s], h, kv, d)
             assert np.array_equal(bits(out[s, layer].reshape(-1)), bits(want))
+
+
+# ------------------------------------------------- decode-layer vector ops ---
+
+def _vec_inputs(n, seed=60):
+    x = S.normal(seed, f"vec{n}x", (n,))
+    y = S.normal(seed, f"vec{n}y", (n,), 3.0)
+    return x, y
+
+
+@pytest.mark.parametrize("n", [1, 7, 896, 2048, 11008])
+def test_vector_ops_match_compiled_reference(oracle_mod, n):
+    """orc_rmsnorm/swiglu/add/argmax bit-identical to the reference's own
+    compiled ops.c te_* functions on the same inputs."""
+    if oracle_mod.ref_lib() is None:
+        pytest.skip("reference ops.c not built here")
+    x, y = _vec_inputs(n)
+    w = S.normal(61, f"vec{n}w", (n,), 0.5) + 1.0
+    for eps in (1e-6, 1e-5):
+        assert np.array_equal(oracle_mod.rmsnorm_f32(x, w, eps), oracle_mod.rmsnorm_f32(x, w, eps, use_ref=True))
+    assert np.array_equal(oracle_mod.swiglu_f32(y, x), oracle_mod.swiglu_f32(y, x, use_ref=True))
+    assert np.array_equal(oracle_mod.add_f32(x, y), oracle_mod.add_f32(x, y, use_ref=True))
+    assert oracle_mod.argmax_f32(y) == oracle_mod.argmax_f32(y, use_ref=True)
+
+
+def test_vector_ops_closed_forms(oracle_mod):
+    # RMSNorm of a constant vector c with unit weights is c / sqrt(c^2 + eps) per element
+    x = np.full(64, 3.0, np.float32)
+    got = oracle_mod.rmsnorm_f32(x, np.ones(64, np.float32), 1e-6)
+    assert np.allclose(got, 3.0 / np.sqrt(9.0 + 1e-6), rtol=1e-6)
+    # silu(0) = 0, silu(g) -> g for large g, silu(g) -> 0 for very negative g
+    g = np.array([0.0, 30.0, -30.0], np.float32)
+    assert np.allclose(oracle_mod.swiglu_f32(g, np.ones(3, np.float32)), [0.0, 30.0, 0.0], atol=1e-9)
+    # argmax: first of equal maxima; NaN never taken; all -inf -> 0; -FLT_MAX -> 0
+    assert oracle_mod.argmax_f32(np.array([1, 5, 5, 2], np.float32)) == 1
+    assert oracle_mod.argmax_f32(np.array([np.nan, 1, np.nan, 3], np.float32)) == 3
+    assert oracle_mod.argmax_f32(np.full(5, -np.inf, np.float32)) == 0
+    assert oracle_mod.argmax_f32(np.array([np.finfo(np.float32).min] * 3, np.float32)) == 0
+    assert oracle_mod.argmax_f32(np.array([-np.inf, np.finfo(np.float32).min, -1e38], np.float32)) == 2
+
+
+@pytest.mark.parametrize("ggml_type", [2, 8])
+def test_dequantize_every_code(oracle_mod, ggml_type):
+    """Each 4-bit / 8-bit code at each position of a block dequantizes to
+    (code - 8) * d (Q4_0: low nibble = element j, high nibble = element j+16) or
+    int8(code) * d (Q8_0), for d = 0.5, -3.25 and an fp16 subnormal."""
+    for dbits in (0x3800, 0xC280, 0x0001):
+        d = float(np.uint16(dbits).view(np.float16))
+        if ggml_type == 2:
+            codes = np.arange(256, dtype=np.uint8)[:, None].repeat(16, 1)  # one block per byte value
+            blk = np.empty((256, 18), np.uint8)
+            want = np.empty((256, 32), np.float32)
+            want[:, :16] = ((codes & 0x0F).astype(np.float32) - 8.0) * np.float32(d)
+            want[:, 16:] = ((codes >> 4).astype(np.float32) - 8.0) * np.float32(d)
+        else:
+            codes = np.arange(256, dtype=np.uint8)[:, None].repeat(32, 1)
+            blk = np.empty((256, 34), np.uint8)
+            want = codes.view(np.int8).astype(np.float32) * np.float32(d)
+        blk[:, 0] = dbits & 0xFF
+        blk[:, 1] = dbits >> 8
+        blk[:, 2:] = codes
+        got = oracle_mod.dequantize_rows(blk.reshape(-1), ggml_type, 32, 256)
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("ggml_type,rows,cols", [(0, 5, 64), (2, 7, 96), (8, 6, 128), (2, 3, 2048), (8, 2, 11008)])
+def test_matvec_vs_fp64(oracle_mod, ggml_type, rows, cols):
+    """orc_matvec_f32 against an fp64 dot of the dequantized rows: within the
+    sequential fp32 error bound cols * 2^-24 * sum |w x| (plus one ulp)."""
+    data = S.ggml_tensor(62, f"mv{ggml_type}{rows}{cols}", ggml_type, rows, cols)
+    x = S.normal(62, f"mvx{cols}", (cols,))
+    got = oracle_mod.matvec_f32(data, ggml_type, x, cols, rows)
+    w = oracle_mod.dequantize_rows(data, ggml_type, cols, rows).astype(np.float64)
+    exact = w @ x.astype(np.float64)
+    bound = cols * 2.0 ** -24 * (np.abs(w) @ np.abs(x.astype(np.float64))) + np.abs(exact) * 2.0 ** -23
+    assert np.all(np.abs(got - exact) <= bound)
+    assert oracle_mod.ggml_row_bytes(ggml_type, cols) * rows == data.size

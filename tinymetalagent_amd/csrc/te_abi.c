@@ -7,10 +7,12 @@
  * the agent layer matches the exact text "unsupported"
  * (python/tinyagent/engine.py:46, :62).
  *
- * Entry points outside the attention step (GGUF model loading, tokenizer,
- * quantized matvec, element-wise ops, full generation) keep the reference's
- * argument checks and then return TE_STATUS_UNSUPPORTED, the reference's
- * "path not available here" status (qwen.c:1162-1165).  They exist so that an
+ * Entry points outside this build (GGUF model loading, tokenizer, the
+ * model-level matvec, full generation) keep the reference's argument checks
+ * and then return TE_STATUS_UNSUPPORTED, the reference's "path not available
+ * here" status (qwen.c:1162-1165).  The element-wise ops (te_rmsnorm_f32,
+ * te_swiglu_f32, te_add_f32, te_argmax_f32) run on the GPU in
+ * te_hip_runtime.hip.  They exist so that an
  * unchanged ctypes binding resolves all of its symbols
  * (python/tinyengine/runtime.py:271-378).
  */
@@ -83,10 +85,19 @@ te_runtime_options te_default_options(void) {
     return options;
 }
 
-/* The attention-step operations this build implements on the GPU. */
+/* The operations this build implements on the GPU: the attention step and the
+ * decode-layer vector operations around it (matvec, RMSNorm, SwiGLU, residual
+ * add, argmax). */
 static uint64_t te_hip_op_mask(void) {
     return (1ull << TE_OP_ROPE) | (1ull << TE_OP_CAUSAL_ATTENTION) | (1ull << TE_OP_KV_CACHE) |
-           (1ull << TE_OP_BATCHED_PREFILL);
+           (1ull << TE_OP_BATCHED_PREFILL) | (1ull << TE_OP_MATVEC) | (1ull << TE_OP_RMSNORM) |
+           (1ull << TE_OP_SWIGLU) | (1ull << TE_OP_RESIDUAL_ADD) | (1ull << TE_OP_ARGMAX);
+}
+
+/* Weight / cache formats: fp32 and fp16 data, GGUF Q4_0 and Q8_0 matvec. */
+static uint64_t te_hip_quant_mask(void) {
+    return (1ull << TE_QUANT_F32) | (1ull << TE_QUANT_F16) | (1ull << TE_QUANT_GGUF_Q4_0) |
+           (1ull << TE_QUANT_GGUF_Q8_0);
 }
 
 te_status te_detect_arch(te_arch_info *out_info) {
@@ -114,14 +125,15 @@ te_status te_get_capabilities(te_capabilities *out_capabilities) {
     }
     memset(out_capabilities, 0, sizeof(*out_capabilities));
     out_capabilities->abi_version = TE_ABI_VERSION;
-    out_capabilities->known_quant_mask[0] = (1ull << TE_QUANT_F32) | (1ull << TE_QUANT_F16);
-    out_capabilities->optimized_quant_mask[0] = 1ull << TE_QUANT_F16;
+    out_capabilities->known_quant_mask[0] = te_hip_quant_mask();
+    out_capabilities->optimized_quant_mask[0] = te_hip_quant_mask();
     out_capabilities->vector_op_mask = te_hip_op_mask();
     out_capabilities->optimization_flags = TE_OPT_ARCH_SPECIALIZED | TE_OPT_GPU_RESIDENT_KV | TE_OPT_BATCHED_PREFILL;
     out_capabilities->preferred_alignment_bytes = 256u;
     snprintf(out_capabilities->backend_name, sizeof(out_capabilities->backend_name), "%s", "hip-gfx950");
     snprintf(out_capabilities->notes, sizeof(out_capabilities->notes), "%s",
-             "attention step on MI355X: RoPE, fp16 KV append, split-K GQA decode, MFMA causal prefill");
+             "MI355X: RoPE, fp16 KV append, split-K GQA decode, MFMA causal prefill; Q4_0/Q8_0/F32 matvec, "
+             "RMSNorm, SwiGLU, add, argmax");
     return TE_STATUS_OK;
 }
 
@@ -135,8 +147,8 @@ te_status te_make_kernel_plan(const te_runtime_options *options, te_kernel_plan 
     memset(out_plan, 0, sizeof(*out_plan));
     out_plan->abi_version = TE_ABI_VERSION;
     out_plan->target_arch = TE_ARCH_AMD_GFX950;
-    out_plan->quant_mask[0] = (1ull << TE_QUANT_F32) | (1ull << TE_QUANT_F16);
-    out_plan->optimized_quant_mask[0] = 1ull << TE_QUANT_F16;
+    out_plan->quant_mask[0] = te_hip_quant_mask();
+    out_plan->optimized_quant_mask[0] = te_hip_quant_mask();
     out_plan->vector_op_mask = te_hip_op_mask();
     out_plan->optimization_flags = TE_OPT_ARCH_SPECIALIZED | TE_OPT_GPU_RESIDENT_KV | TE_OPT_BATCHED_PREFILL;
     out_plan->dot_threads = 64u; /* wavefront width */
@@ -275,27 +287,6 @@ te_status te_model_matvec_f32(const te_model *model, const char *name, const flo
 
 void te_model_free(te_model *model) {
     (void)model; /* no model can be created by this build */
-}
-
-te_status te_rmsnorm_f32(const float *input, const float *weight, size_t len, float epsilon, float *out) {
-    (void)epsilon;
-    return (input == NULL || weight == NULL || out == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
-                                                                         : TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_swiglu_f32(const float *gate, const float *up, size_t len, float *out) {
-    return (gate == NULL || up == NULL || out == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
-                                                                    : TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_add_f32(const float *lhs, const float *rhs, size_t len, float *out) {
-    return (lhs == NULL || rhs == NULL || out == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
-                                                                    : TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_argmax_f32(const float *values, size_t len, uint32_t *out_index) {
-    return (values == NULL || out_index == NULL || len == 0u) ? TE_STATUS_INVALID_ARGUMENT
-                                                              : TE_STATUS_UNSUPPORTED;
 }
 
 /* ---- context and generation: reference tinyengine.c:374-440 ---- */

@@ -83,6 +83,16 @@ struct DecodeGeometry {
 // Compute units of the current device (256 when the query fails).
 int device_compute_units();
 
+// Decode-layer vector operations (te_vecops.hip); arguments already checked.
+size_t ggml_row_bytes(uint32_t ggml_type, size_t cols);  // 0 = type / cols not supported
+te_status launch_matvec(const void *weights, uint32_t ggml_type, const float *input, size_t cols, size_t rows,
+                        float *out, hipStream_t stream);
+te_status launch_rmsnorm(const float *input, const float *weight, size_t rows, size_t len, float epsilon, float *out,
+                         hipStream_t stream);
+te_status launch_swiglu(const float *gate, const float *up, size_t len, float *out, hipStream_t stream);
+te_status launch_add(const float *lhs, const float *rhs, size_t len, float *out, hipStream_t stream);
+te_status launch_argmax(const float *values, size_t len, uint32_t *out_index, hipStream_t stream);
+
 DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
                                size_t kv_heads);
 

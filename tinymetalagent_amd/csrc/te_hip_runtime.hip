@@ -246,6 +246,107 @@ extern "C" te_status te_rope_f32(float *values, size_t heads, size_t head_dim, s
     return d2h(values, g_rt.buf[0].ptr, n * sizeof(float));
 }
 
+// Public decode-layer vector operations (reference ops.c:272-293, :397-433) on
+// the GPU: host arrays are copied in, the te_hip_* kernel runs, the result is
+// copied back; synchronous, serialized by the library mutex like te_rope_f32.
+namespace {
+
+te_status host_vector_op(const float *a, const float *b, size_t len, float *out,
+                         te_status (*launch)(const float *, const float *, size_t, float *, hipStream_t)) {
+    size_t bytes = 0;
+    if (!mul_ok(len, sizeof(float), &bytes) || len > ((size_t)1 << 31)) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!probe_locked()) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    te_status st;
+    if ((st = g_rt.buf[0].ensure(bytes)) != TE_STATUS_OK || (st = g_rt.buf[1].ensure(bytes)) != TE_STATUS_OK ||
+        (st = g_rt.buf[2].ensure(bytes)) != TE_STATUS_OK) {
+        return st;
+    }
+    if ((st = h2d(g_rt.buf[0].ptr, a, bytes)) != TE_STATUS_OK || (st = h2d(g_rt.buf[1].ptr, b, bytes)) != TE_STATUS_OK) {
+        return st;
+    }
+    if ((st = launch(g_rt.buf[0].as<float>(), g_rt.buf[1].as<float>(), len, g_rt.buf[2].as<float>(), g_rt.stream)) !=
+        TE_STATUS_OK) {
+        return st;
+    }
+    return d2h(out, g_rt.buf[2].ptr, bytes);
+}
+
+}  // namespace
+
+extern "C" te_status te_rmsnorm_f32(const float *input, const float *weight, size_t len, float epsilon, float *out) {
+    if (input == nullptr || weight == nullptr || out == nullptr || len == 0 || epsilon <= 0.0f) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    size_t bytes = 0;
+    if (!mul_ok(len, sizeof(float), &bytes) || len > 0x7fffffffu) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!probe_locked()) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    te_status st;
+    if ((st = g_rt.buf[0].ensure(bytes)) != TE_STATUS_OK || (st = g_rt.buf[1].ensure(bytes)) != TE_STATUS_OK ||
+        (st = g_rt.buf[2].ensure(bytes)) != TE_STATUS_OK) {
+        return st;
+    }
+    if ((st = h2d(g_rt.buf[0].ptr, input, bytes)) != TE_STATUS_OK ||
+        (st = h2d(g_rt.buf[1].ptr, weight, bytes)) != TE_STATUS_OK) {
+        return st;
+    }
+    st = te_hip::launch_rmsnorm(g_rt.buf[0].as<float>(), g_rt.buf[1].as<float>(), 1, len, epsilon,
+                                g_rt.buf[2].as<float>(), g_rt.stream);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    return d2h(out, g_rt.buf[2].ptr, bytes);
+}
+
+extern "C" te_status te_swiglu_f32(const float *gate, const float *up, size_t len, float *out) {
+    if (gate == nullptr || up == nullptr || out == nullptr || len == 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    return host_vector_op(gate, up, len, out, te_hip::launch_swiglu);
+}
+
+extern "C" te_status te_add_f32(const float *lhs, const float *rhs, size_t len, float *out) {
+    if (lhs == nullptr || rhs == nullptr || out == nullptr || len == 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    return host_vector_op(lhs, rhs, len, out, te_hip::launch_add);
+}
+
+extern "C" te_status te_argmax_f32(const float *values, size_t len, uint32_t *out_index) {
+    if (values == nullptr || out_index == nullptr || len == 0 || len > 0xffffffffu) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    size_t bytes = 0;
+    if (!mul_ok(len, sizeof(float), &bytes)) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!probe_locked()) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    te_status st;
+    if ((st = g_rt.buf[0].ensure(bytes)) != TE_STATUS_OK || (st = g_rt.buf[1].ensure(sizeof(uint32_t))) != TE_STATUS_OK) {
+        return st;
+    }
+    if ((st = h2d(g_rt.buf[0].ptr, values, bytes)) != TE_STATUS_OK) {
+        return st;
+    }
+    if ((st = te_hip::launch_argmax(g_rt.buf[0].as<float>(), len, g_rt.buf[1].as<uint32_t>(), g_rt.stream)) !=
+        TE_STATUS_OK) {
+        return st;
+    }
+    return d2h(out_index, g_rt.buf[1].ptr, sizeof(uint32_t));
+}
+
 // Public te_attention_decode_f32 (reference ops.c:323-395) on the GPU: the fp32
 // cache prefix 0..position is uploaded and attended by a chunked fp32 kernel
 // plus the split-K combine kernel.

@@ -167,6 +167,10 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     # Attention step, public (include/tinyengine.h).
     _sig(lib, "te_rope_f32", [_f32p, _sz, _sz, _sz, ctypes.c_float])
     _sig(lib, "te_attention_decode_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _f32p])
+    _sig(lib, "te_rmsnorm_f32", [_f32p, _f32p, _sz, ctypes.c_float, _f32p])
+    _sig(lib, "te_swiglu_f32", [_f32p, _f32p, _sz, _f32p])
+    _sig(lib, "te_add_f32", [_f32p, _f32p, _sz, _f32p])
+    _sig(lib, "te_argmax_f32", [_f32p, _sz, ctypes.POINTER(ctypes.c_uint32)])
     # HIP backend slot (include/te_hip_backend.h).
     _sig(lib, "te_hip_available", [], _int)
     _sig(lib, "te_hip_device_info", [ctypes.c_char_p, _sz, ctypes.POINTER(ctypes.c_uint32)])
@@ -195,6 +199,11 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_hip_attention_stream_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _f32p])
     _sig(lib, "te_hip_attention_causal_mma_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _f32p])
     _sig(lib, "te_hip_calibrate_mfma_f16", [_sz, _sz, _vp, _vp])
+    _sig(lib, "te_hip_matvec_f32", [_vp, ctypes.c_uint32, _vp, _sz, _sz, _vp, _vp])
+    _sig(lib, "te_hip_rmsnorm_f32", [_vp, _vp, _sz, _sz, ctypes.c_float, _vp, _vp])
+    _sig(lib, "te_hip_swiglu_f32", [_vp, _vp, _sz, _vp, _vp])
+    _sig(lib, "te_hip_add_f32", [_vp, _vp, _sz, _vp, _vp])
+    _sig(lib, "te_hip_argmax_f32", [_vp, _sz, _vp, _vp])
 
 
 def strerror(status: int) -> str:
@@ -279,6 +288,38 @@ def attention_decode_f32(query: np.ndarray, key_cache: np.ndarray, value_cache: 
     check(load_library().te_attention_decode_f32(_f32(q), _f32(k), _f32(v), position, heads, kv_heads, head_dim,
                                                  _f32(out)))
     return out
+
+
+def rmsnorm_f32(x: np.ndarray, weight: np.ndarray, epsilon: float) -> np.ndarray:
+    """Public te_rmsnorm_f32 (host arrays, runs on the GPU)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    out = np.empty_like(x)
+    check(load_library().te_rmsnorm_f32(_f32(x), _f32(w), x.size, ctypes.c_float(epsilon), _f32(out)))
+    return out
+
+
+def swiglu_f32(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.empty_like(g)
+    check(load_library().te_swiglu_f32(_f32(g), _f32(u), g.size, _f32(out)))
+    return out
+
+
+def add_f32(lhs: np.ndarray, rhs: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(lhs, dtype=np.float32)
+    b = np.ascontiguousarray(rhs, dtype=np.float32)
+    out = np.empty_like(a)
+    check(load_library().te_add_f32(_f32(a), _f32(b), a.size, _f32(out)))
+    return out
+
+
+def argmax_f32(values: np.ndarray) -> int:
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    idx = ctypes.c_uint32(0)
+    check(load_library().te_argmax_f32(_f32(v), v.size, ctypes.byref(idx)))
+    return int(idx.value)
 
 
 def _mma(name: str, *args) -> None:
