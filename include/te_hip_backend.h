@@ -269,8 +269,14 @@ TE_API te_status te_hip_attention_causal_mma_f32(const float *query, const float
  * out[r] = sum_c W[r][c] * input[c] for a [rows][cols] tensor of GGUF type
  * ggml_type: 0 = F32 (cols % 4 == 0), 2 = Q4_0 and 8 = Q8_0 (cols % 32 == 0;
  * rows of cols/32 blocks of 18 / 34 bytes, ops.c:15-21); other types ->
- * UNSUPPORTED.  Results equal the reference's te_model_matvec_f32 within fp32
- * rounding of the row's terms (the summation order differs).
+ * UNSUPPORTED; `weights` must be 4-byte aligned (16 for F32) and `input`
+ * 16-byte aligned, else UNSUPPORTED (16-byte aligned quantized weights take
+ * the fastest kernel).  F32 results equal the reference's te_model_matvec_f32
+ * within fp32 rounding of the row's terms (the summation order differs).  For
+ * Q4_0 / Q8_0 rows with an even block count, each 32-value block of `input`
+ * is rounded to 22-bit integers relative to its largest magnitude and the
+ * products are summed exactly: error <= 2^-22 max|block| per value plus fp32
+ * rounding of the block sums; a NaN or inf input value gives NaN rows.
  * The others are the reference ops.c functions (te_rmsnorm_f32 :272-293,
  * te_swiglu_f32 :397-406, te_add_f32 :408-416, te_argmax_f32 :418-433) on
  * device arrays, with the same argument checks; te_hip_rmsnorm_f32 normalises

@@ -8,18 +8,15 @@
 // Matvec.  Row r of a [rows][cols] tensor is cols/32 blocks stored back to back
 // (ops.c:15-21): Q4_0 = f16 scale d + 16 bytes whose low nibbles are elements
 // 0-15 and high nibbles 16-31, value (code - 8) * d; Q8_0 = f16 d + 32 int8
-// codes, value code * d; F32 rows are plain floats.  One wave owns R rows; lane
-// l takes blocks l, l + 64, ... of every row, so the wave reads each row as one
-// contiguous stream, and the lane's 32 input values (and their sum) serve all R
-// rows.  Per block, with u = the code read as an unsigned byte or nibble:
-//   Q4_0: d * (sum_j u_j x_j - 8 sum_j x_j)
-//   Q8_0: d * (sum_j u_j x_j - 128 sum_j x_j),  u = code ^ 0x80 (code + 128)
-// so each element costs one byte -> float conversion and one FMA.  Blocks are
-// 18 / 34 bytes, so a block starts 0 or 2 bytes past a 4-byte boundary: the
-// lane reads the covering dwords (never a byte past the block's last
-// dword-pair) and funnel-shifts.  The lane sums are reduced across the wave.
-// Summation order differs from the reference's sequential loop: results agree
-// within fp32 rounding of the row's terms, not bit for bit.
+// codes, value code * d; F32 rows are plain floats.  Quantized rows with an even
+// block count (every Qwen2.5 shape) take the pair kernels below: the input is
+// rounded per 32-value block to 22-bit integers and the products are summed
+// exactly with integer dot instructions.  F32 rows and odd block counts take
+// matvec_kernel: one wave owns R rows, lane l takes blocks l, l + 64, ... and
+// converts each code to float (one v_cvt_f32_ubyteN + one FMA per element,
+// with the offset factored out: d * (sum_j u_j x_j - off sum_j x_j)).
+// Summation order differs from the reference's sequential loop: the results
+// agree within the rounding bounds stated with each kernel, not bit for bit.
 //
 // HBM bytes per launch (the roofline unit): rows * row_bytes + cols * 4 + rows * 4.
 #include "te_hip_common.h"
@@ -33,6 +30,13 @@ constexpr uint32_t kGgmlF32 = 0;
 constexpr uint32_t kGgmlQ4_0 = 2;
 constexpr uint32_t kGgmlQ8_0 = 8;
 constexpr int kMatvecWaves = 4;
+constexpr int kPairWaves = 12;                     // pair kernel: one 12-wave workgroup per CU (3 per SIMD)
+constexpr int kPairThreads = 64 * kPairWaves;
+constexpr int kStageBatch = 4;                      // input float4 loads in flight per thread while staging
+constexpr size_t kMaxPairLdsBytes = 160 * 1024;     // staged digit planes (gfx950 LDS per CU)
+constexpr size_t kPairLdsBytes = 13 * 16;           // LDS per block pair: 12 uint4 of digit planes + scales
+template <uint32_t TYPE>
+constexpr int kDigitPlanes = TYPE == kGgmlQ4_0 ? 6 : 3;  // balanced base-16 / base-256 digits of 22-bit X
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -171,6 +175,429 @@ __global__ __launch_bounds__(64 * kMatvecWaves) void matvec_kernel(const unsigne
     }
 }
 
+// Quantized rows with an even block count (every Qwen2.5 shape), as exact
+// integer dot products.
+//
+// Input staging.  The workgroup scales each 32-value block of the input by a
+// power of two, 2^e with e = 22 - ceil(log2 max|x|), so the block's largest
+// magnitude lies in [2^21, 2^22), and rounds it to integers X (error <= 2^-22 of
+// the block max; the block's own 2^-e is kept).  X is written in balanced
+// digits: six base-16 digits in [-8, 7] (Q4_0) or three base-256 digits in
+// [-128, 127] (Q8_0), X = sum_t D_t 16^t (256^t).  Digit plane t of a block is
+// packed like the weights: for Q4_0 dword k holds elements 4k..4k+3 in its even
+// nibbles and 16+4k..19+4k in its odd ones (the Q4_0 byte layout); for Q8_0 dword
+// k holds elements 4k..4k+3, one per byte.  A block's planes are 24 dwords; a
+// pair is 13 float4 in LDS (12 of planes, then the two 2^-e), and 13 is odd, so
+// 16 lanes reading 16 consecutive pairs hit 16 distinct bank groups.
+//
+// Product.  Q4_0 codes n become signed nibbles n - 8 = n ^ 8; Q8_0 codes are
+// signed bytes already.  v_dot8c_i32_i4 / v_dot4c_i32_i8 of a weight dword and a
+// digit dword accumulate S_t = sum_j w_j D_tj exactly; per block |S_t| <= 2^11
+// (Q4_0) / 2^19 (Q8_0), so the planes combine in int32 into two parts below
+// 2^24 (Q4_0: S0 + 16 S1 + 256 S2 and S3 + 16 S4 + 256 S5; Q8_0: S0 + 256 S1
+// and S2), which convert to float exactly (Q4_0) or with one rounding (Q8_0)
+// and meet in one FMA.  The block adds d * 2^-e * that sum to the row.  Every
+// element costs 6 / 8 (Q4_0) or 3 / 4 (Q8_0) integer dot instructions.
+
+// Stage the input's digit planes and block scales (layout above) into LDS for
+// the whole workgroup; the caller synchronises.
+template <uint32_t TYPE>
+__device__ __forceinline__ void stage_digit_planes(const float *input, int pairs, uint32_t *xs_lds) {
+    const int nthreads = (int)blockDim.x;
+// Stage the input: coalesced float4 reads, kStageBatch per thread issued
+// before any is used.  Float4 i is block i / 8 (of pair i / 16), slice i % 8;
+// a block's 8 slices sit in 8 consecutive lanes, which share its max and its
+// digit dwords.  pairs * 16 is a multiple of 8, so those lanes agree on the bound.
+const int n4 = pairs * 16;
+for (int base = 0; base < n4; base += kStageBatch * nthreads) {
+    float4 v[kStageBatch];
+    // waves whose slice of a batch row starts past the input skip it (uniform branch)
+    const int wave_first = base + (int)(threadIdx.x & ~63u);
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+        const int i = base + u * nthreads + (int)threadIdx.x;
+        v[u] = i < n4 ? reinterpret_cast<const float4 *>(input)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+        if (wave_first + u * nthreads >= n4) {
+            break;
+        }
+        const int i = base + u * nthreads + (int)threadIdx.x;
+        const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        float m = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
+        int bad = !(isfinite(xv[0]) && isfinite(xv[1]) && isfinite(xv[2]) && isfinite(xv[3]));
+#pragma unroll
+        for (int o = 1; o <= 4; o <<= 1) {
+            m = fmaxf(m, __shfl_xor(m, o, 64));
+            bad |= __shfl_xor(bad, o, 64);
+        }
+        int ex = 0;
+        frexpf(m, &ex);  // m < 2^ex <= 2 m
+        // blocks whose max is below 2^-104 keep an absolute error of 2^-127
+        const int e = bad || m == 0.0f ? 0 : min(22 - ex, 126);
+        const int f = i & 7;
+        uint32_t planes[kDigitPlanes<TYPE>] = {};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int xq = bad ? 0 : (int)rintf(ldexpf(xv[j], e));  // |xq| <= 2^22
+#pragma unroll
+            for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
+                if (TYPE == kGgmlQ4_0) {
+                    const int d = ((xq + 8) & 15) - 8;
+                    xq = (xq - d) >> 4;
+                    planes[t] |= (uint32_t)(d & 15) << (8 * j + ((f & 4) ? 4 : 0));
+                } else {
+                    const int d = ((xq + 128) & 255) - 128;
+                    xq = (xq - d) >> 8;
+                    planes[t] |= (uint32_t)(d & 255) << (8 * j);
+                }
+            }
+        }
+        if (TYPE == kGgmlQ4_0) {
+            // slices f and f + 4 fill the even and odd nibbles of dword f
+#pragma unroll
+            for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
+                planes[t] |= __shfl_xor(planes[t], 4, 64);
+            }
+        }
+        if (i < n4) {
+            const int p = i >> 4, c = (i >> 3) & 1;
+            uint32_t *slot = xs_lds + p * 52 + c * 24;
+            if (TYPE == kGgmlQ4_0) {
+                if (f < 4) {
+#pragma unroll
+                    for (int t = 0; t < 6; ++t) {
+                        slot[4 * t + f] = planes[t];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 3; ++t) {
+                    slot[8 * t + f] = planes[t];
+                }
+            }
+            if (f == 0) {
+                // a non-finite input makes the block's rows NaN
+                xs_lds[p * 52 + 48 + c] = __float_as_uint(bad ? __builtin_nanf("") : ldexpf(1.0f, -e));
+            }
+        }
+    }
+}
+}
+
+// acc + the row's block pair (PW dwords w) against the lane's digit planes xq
+// (48 dwords) and the two block scales sc0, sc1 (2^-e).
+template <uint32_t TYPE>
+__device__ __forceinline__ float pair_dot(const uint32_t *w, const uint32_t (&xq)[48], float sc0, float sc1,
+                                          float acc) {
+    float d0, d1, dot0, dot1;
+    if (TYPE == kGgmlQ4_0) {
+        // block 0: scale = w0 low half, codes = bytes 2..17; block 1: scale = w4 high half, codes = w5..w8
+        d0 = f16_bits_to_f32(w[0] & 0xffffu);
+        d1 = f16_bits_to_f32(w[4] >> 16);
+        int s0[6] = {}, s1[6] = {};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q0 = __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2) ^ 0x88888888u;
+            const uint32_t q1 = w[5 + k] ^ 0x88888888u;
+#pragma unroll
+            for (int t = 0; t < 6; ++t) {
+                s0[t] = __builtin_amdgcn_sdot8((int)q0, (int)xq[4 * t + k], s0[t], false);
+                s1[t] = __builtin_amdgcn_sdot8((int)q1, (int)xq[24 + 4 * t + k], s1[t], false);
+            }
+        }
+        dot0 = fmaf((float)(s0[3] + s0[4] * 16 + s0[5] * 256), 4096.0f, (float)(s0[0] + s0[1] * 16 + s0[2] * 256));
+        dot1 = fmaf((float)(s1[3] + s1[4] * 16 + s1[5] * 256), 4096.0f, (float)(s1[0] + s1[1] * 16 + s1[2] * 256));
+    } else {
+        // block 0: scale = w0 low half, codes = bytes 2..33; block 1: scale = w8 high half, codes = w9..w16
+        d0 = f16_bits_to_f32(w[0] & 0xffffu);
+        d1 = f16_bits_to_f32(w[8] >> 16);
+        int s0[3] = {}, s1[3] = {};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t q0 = __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2);
+            const uint32_t q1 = w[9 + k];
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                s0[t] = __builtin_amdgcn_sdot4((int)q0, (int)xq[8 * t + k], s0[t], false);
+                s1[t] = __builtin_amdgcn_sdot4((int)q1, (int)xq[24 + 8 * t + k], s1[t], false);
+            }
+        }
+        dot0 = fmaf((float)s0[2], 65536.0f, (float)(s0[0] + s0[1] * 256));
+        dot1 = fmaf((float)s1[2], 65536.0f, (float)(s1[0] + s1[1] * 256));
+    }
+    acc = fmaf(d0 * sc0, dot0, acc);
+    return fmaf(d1 * sc1, dot1, acc);
+}
+
+// Both pair kernels cut the rows into tiles of 64 / LPR row groups x NR rows;
+// each wave walks tiles gwave, gwave + waves, ..., and lane li of a group takes
+// block PAIRS li, li + LPR, ... of its NR rows.  A pair is 36 (Q4_0) or 68 (Q8_0)
+// bytes on a dword boundary.
+//
+// Strided pair kernel (weights not 16-byte aligned, or row groups longer than
+// the streamed kernel's LDS tile): each lane reads its pairs straight from HBM
+// as whole dwords, and the next (tile, pair step)'s weights are loaded into a
+// second register set before the current one is computed.
+template <uint32_t TYPE, int LPR, int NR>
+__global__ __launch_bounds__(kPairThreads) void matvec_pairs_kernel(const unsigned char *weights,
+                                                                       const float *input, int cols, int rows,
+                                                                       size_t row_bytes, float *out, int tiles) {
+    constexpr int PW = TYPE == kGgmlQ4_0 ? 9 : 17;  // dwords per block pair
+    constexpr int G = 64 / LPR;                      // row groups per wave
+    extern __shared__ uint4 xs_lds4[];  // [pairs][13] uint4: block 0 planes, block 1 planes, scales
+    uint32_t *const xs_lds = reinterpret_cast<uint32_t *>(xs_lds4);
+    const int lane = threadIdx.x & 63;
+    const int grp = lane / LPR;
+    const int li = lane % LPR;
+    // tile t goes to wave t mod waves; consecutive tiles land on different CUs
+    const int gwave = (int)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    const int nwaves = gridDim.x * kPairWaves;
+    const int pairs = cols / 64;
+    const int steps = (pairs + LPR - 1) / LPR;  // pair steps per tile
+
+    uint32_t wa[NR][PW], wb[NR][PW];
+    // Loads are never skipped: past the last tile a wave re-reads the last one
+    // (unused), so the loop below has no branch around a load and the compiler
+    // keeps the next step's loads outstanding while the current one is summed.
+    auto load = [&](uint32_t(&w)[NR][PW], int tile, int step) {
+        tile = min(tile, tiles - 1);
+        const int p = min(li + step * LPR, pairs - 1);  // lanes past the last pair re-read it, unused
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int row = min((tile * G + grp) * NR + r, rows - 1);  // rows past the end: never stored
+            // plain loads: the three loads of a lane's pair share cache lines with the
+            // neighbouring lanes' pairs (nontemporal loads re-fetched them: 1.3-2x slower)
+            const uint32_t *src =
+                reinterpret_cast<const uint32_t *>(weights + (size_t)row * row_bytes + (size_t)p * 4 * PW);
+#pragma unroll
+            for (int k = 0; k < PW; ++k) {
+                w[r][k] = src[k];
+            }
+        }
+    };
+    if (gwave < tiles) {
+        load(wa, gwave, 0);
+    }
+
+    stage_digit_planes<TYPE>(input, pairs, xs_lds);
+    __syncthreads();
+    if (gwave >= tiles) {
+        return;
+    }
+
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        acc[r] = 0.0f;
+    }
+    uint32_t xq[48];  // digit planes of the lane's pair: block c, plane t, dword k at 24c + (4|8)t + k
+    float sc0 = 0.0f, sc1 = 0.0f;
+    int x_step = -1;
+    // sum of one pair step of NR rows into acc; the digit planes are re-read from
+    // LDS only when the step changes (never when a tile is one step)
+    auto compute = [&](const uint32_t(&w)[NR][PW], int step) {
+        const int p = li + step * LPR;
+        if (step != x_step) {
+            x_step = step;
+            const int pp = min(p, pairs - 1);
+#pragma unroll
+            for (int k = 0; k < 12; ++k) {
+                const uint4 v = xs_lds4[pp * 13 + k];
+                xq[4 * k] = v.x;
+                xq[4 * k + 1] = v.y;
+                xq[4 * k + 2] = v.z;
+                xq[4 * k + 3] = v.w;
+            }
+            const uint4 s = xs_lds4[pp * 13 + 12];
+            sc0 = __uint_as_float(s.x);
+            sc1 = __uint_as_float(s.y);
+        }
+        if (p >= pairs) {
+            return;
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            acc[r] = pair_dot<TYPE>(w[r], xq, sc0, sc1, acc[r]);
+        }
+    };
+    auto finish_tile = [&](int tile) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            float v = acc[r];
+#pragma unroll
+            for (int o = LPR / 2; o >= 1; o >>= 1) {
+                v += __shfl_xor(v, o, 64);
+            }
+            const int row = (tile * G + grp) * NR + r;
+            if (li == 0 && row < rows) {
+                out[row] = v;
+            }
+            acc[r] = 0.0f;
+        }
+    };
+    // (tile, step) walk; wave-uniform, so every branch below is scalar
+    int tile = gwave, step = 0;
+    auto advance = [&](int &t, int &s) {
+        if (++s == steps) {
+            s = 0;
+            t += nwaves;
+        }
+    };
+    for (;;) {
+        int tn = tile, sn = step;
+        advance(tn, sn);
+        load(wb, tn, sn);
+        compute(wa, step);
+        if (sn == 0) {
+            finish_tile(tile);
+        }
+        if (tn >= tiles) {
+            break;
+        }
+        tile = tn;
+        step = sn;
+        advance(tn, sn);
+        load(wa, tn, sn);
+        compute(wb, step);
+        if (sn == 0) {
+            finish_tile(tile);
+        }
+        if (tn >= tiles) {
+            break;
+        }
+        tile = tn;
+        step = sn;
+    }
+}
+
+// Streamed pair kernel.  A tile's rows are one contiguous byte range.  The wave
+// reads it as 16-byte chunks, lane l taking chunks l, l + 64, ... (every load
+// instruction covers 1 KB contiguous; nontemporal, the weights are read once
+// per token), writes them to its own LDS buffer, and each lane reads its pairs
+// from there.  The next tile's chunks load into registers while the current
+// tile is summed from LDS; a wave's LDS operations complete in order, so the
+// next tile is stored over the buffer after the current one's reads with no
+// barrier.  CH chunk loads per lane: CH KB >= the tile plus 15 bytes of
+// misalignment (tiles start on dword, not 16-byte, boundaries).
+template <uint32_t TYPE, int LPR, int NR, int CH>
+__global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsigned char *weights,
+                                                                    const float *input, int cols, int rows,
+                                                                    size_t row_bytes, float *out, int tiles,
+                                                                    size_t total_chunks) {
+    constexpr int PW = TYPE == kGgmlQ4_0 ? 9 : 17;  // dwords per block pair
+    constexpr int G = 64 / LPR;                      // row groups per wave
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    extern __shared__ uint4 lds4[];  // [pairs][13] digit planes + scales, then one CH KB tile buffer per wave
+    uint32_t *const xs_lds = reinterpret_cast<uint32_t *>(lds4);
+    const int lane = threadIdx.x & 63;
+    const int grp = lane / LPR;
+    const int li = lane % LPR;
+    const int wave = (int)(threadIdx.x >> 6);
+    // tile t goes to wave t mod waves; consecutive tiles land on different CUs
+    const int gwave = wave * gridDim.x + blockIdx.x;
+    const int nwaves = gridDim.x * (int)(blockDim.x >> 6);
+    const int pairs = cols / 64;
+    const int steps = (pairs + LPR - 1) / LPR;  // pair steps per tile
+    const size_t tile_bytes = (size_t)G * NR * row_bytes;
+    uint4 *const buf = lds4 + pairs * 13 + wave * CH * 64;
+    const u32x4 *const w16 = reinterpret_cast<const u32x4 *>(weights);
+
+    u32x4 ck[CH] = {};
+    auto load = [&](int tile) {
+        const size_t b = (size_t)tile * tile_bytes;
+        const size_t c0 = b >> 4;
+        const size_t c1 = min((b + tile_bytes + 15) >> 4, total_chunks);
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const size_t c = c0 + lane + 64 * i;
+            if (c < c1) {
+                ck[i] = __builtin_nontemporal_load(w16 + c);
+            }
+        }
+    };
+    if (gwave < tiles) {
+        load(gwave);
+    }
+    stage_digit_planes<TYPE>(input, pairs, xs_lds);
+    __syncthreads();
+    if (gwave >= tiles) {
+        return;
+    }
+
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        acc[r] = 0.0f;
+    }
+    uint32_t xq[48];
+    float sc0 = 0.0f, sc1 = 0.0f;
+    auto read_planes = [&](int p) {
+#pragma unroll
+        for (int k = 0; k < 12; ++k) {
+            const uint4 v = lds4[p * 13 + k];
+            xq[4 * k] = v.x;
+            xq[4 * k + 1] = v.y;
+            xq[4 * k + 2] = v.z;
+            xq[4 * k + 3] = v.w;
+        }
+        const uint4 s = lds4[p * 13 + 12];
+        sc0 = __uint_as_float(s.x);
+        sc1 = __uint_as_float(s.y);
+    };
+    if (steps == 1) {
+        read_planes(min(li, pairs - 1));
+    }
+    for (int tile = gwave;;) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            buf[lane + 64 * i] = make_uint4(ck[i].x, ck[i].y, ck[i].z, ck[i].w);
+        }
+        const int tn = tile + nwaves;
+        if (tn < tiles) {
+            load(tn);
+        }
+        const unsigned char *tb = reinterpret_cast<const unsigned char *>(buf) + (((size_t)tile * tile_bytes) & 15);
+        for (int step = 0; step < steps; ++step) {
+            const int p = li + step * LPR;
+            if (steps > 1) {
+                read_planes(min(p, pairs - 1));
+            }
+            if (p < pairs) {
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const uint32_t *src =
+                        reinterpret_cast<const uint32_t *>(tb + (size_t)(grp * NR + r) * row_bytes + (size_t)p * 4 * PW);
+                    uint32_t w[PW];
+#pragma unroll
+                    for (int k = 0; k < PW; ++k) {
+                        w[k] = src[k];
+                    }
+                    acc[r] = pair_dot<TYPE>(w, xq, sc0, sc1, acc[r]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            float v = acc[r];
+#pragma unroll
+            for (int o = LPR / 2; o >= 1; o >>= 1) {
+                v += __shfl_xor(v, o, 64);
+            }
+            const int row = (tile * G + grp) * NR + r;
+            if (li == 0 && row < rows) {
+                out[row] = v;
+            }
+            acc[r] = 0.0f;
+        }
+        if (tn >= tiles) {
+            break;
+        }
+        tile = tn;
+    }
+}
+
 // One workgroup per row: sum of squares in fp64 (as the reference), the scale
 // 1/sqrtf(mean + eps) in fp32, then x * scale * w.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *input, const float *weight, int len, float eps,
@@ -272,13 +699,145 @@ size_t ggml_row_bytes(uint32_t ggml_type, size_t cols) {
 te_status launch_matvec(const void *weights, uint32_t ggml_type, const float *input, size_t cols, size_t rows,
                         float *out, hipStream_t stream) {
     const size_t row_bytes = ggml_row_bytes(ggml_type, cols);
-    // Each row takes R = 1, 2 or 4 waves' worth of rows so large tensors
-    // amortise the input loads while small ones still fill the device.
+    const unsigned char *w = static_cast<const unsigned char *>(weights);
     const size_t waves_wanted = (size_t)device_compute_units() * 16;
+    const size_t pair_lds_bytes = cols / 64 * kPairLdsBytes;
+    if (ggml_type != kGgmlF32 && cols % 64 == 0 && pair_lds_bytes <= kMaxPairLdsBytes) {
+        // block pairs: lanes per row from the pair count; rows per group so that the
+        // tiles give every CU at least 8 waves where the rows allow (Q8_0 stays at two
+        // rows: four double-buffered 68-byte pairs do not fit 3 waves per SIMD)
+        const size_t pairs = cols / 64;
+        const int lpr = pairs >= 64 ? 64 : pairs >= 32 ? 32 : 16;
+        const size_t groups = 64 / lpr;
+        const size_t cus = (size_t)device_compute_units();
+        const size_t want = cus * 8;
+        if (((size_t)weights & 15u) == 0 && rows * row_bytes % 16 == 0 && getenv("TE_HIP_GEMV_STRIDED") == nullptr) {
+            // streamed: row-group tiles of at most 12 KB (measured best of 4 / 8 / 12 KB at
+            // lm_head: more bytes in flight per wave), as many rows as keep every CU at 8
+            // waves; waves per workgroup as the LDS allows
+            int snr = 1;
+            size_t tile_cap = 12288;
+            if (const char *env = getenv("TE_HIP_GEMV_TILE")) {  // tuning override: bytes per row-group tile
+                tile_cap = (size_t)atoi(env) >= 1024 ? (size_t)atoi(env) : tile_cap;
+            }
+            for (int cand = 2; cand <= (ggml_type == kGgmlQ4_0 ? 4 : 2); cand *= 2) {
+                if (groups * cand * row_bytes + 15 <= tile_cap && rows >= cand * groups * want) {
+                    snr = cand;
+                }
+            }
+            const size_t tile_bytes = groups * snr * row_bytes;
+            const int ch = tile_bytes + 15 <= 4096 ? 4 : tile_bytes + 15 <= 8192 ? 8 : 12;
+            const size_t waves_fit = tile_bytes + 15 <= 12288 ? (kMaxPairLdsBytes - pair_lds_bytes) / (ch * 1024) : 0;
+            if (waves_fit >= 4) {
+                const int wpg = waves_fit < (size_t)kPairWaves ? (int)waves_fit : kPairWaves;
+                const size_t lds = pair_lds_bytes + (size_t)wpg * ch * 1024;
+                const size_t stiles = (rows + groups * snr - 1) / (groups * snr);
+                const dim3 sgrid((unsigned)(stiles < cus ? stiles : cus));
+                const size_t total_chunks = rows * row_bytes / 16;
+#define TE_STREAM(T, L, N, C)                                                                                     \
+    do {                                                                                                          \
+        if (lds > 65536 &&                                                                                        \
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, C>),                \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {            \
+            return TE_STATUS_RUNTIME_ERROR;                                                                       \
+        }                                                                                                         \
+        matvec_stream_kernel<T, L, N, C><<<sgrid, dim3(64 * wpg), lds, stream>>>(                                 \
+            w, input, (int)cols, (int)rows, row_bytes, out, (int)stiles, total_chunks);                           \
+    } while (0)
+#define TE_STREAM_CH(T, L, N)       \
+    do {                            \
+        if (ch == 4) {              \
+            TE_STREAM(T, L, N, 4);  \
+        } else if (ch == 8) {       \
+            TE_STREAM(T, L, N, 8);  \
+        } else {                    \
+            TE_STREAM(T, L, N, 12); \
+        }                           \
+    } while (0)
+#define TE_STREAM_NR(T, L)                                       \
+    do {                                                         \
+        if (snr == 4) {                                          \
+            TE_STREAM_CH(T, L, (T == kGgmlQ4_0 ? 4 : 2));        \
+        } else if (snr == 2) {                                   \
+            TE_STREAM_CH(T, L, 2);                               \
+        } else {                                                 \
+            TE_STREAM_CH(T, L, 1);                               \
+        }                                                        \
+    } while (0)
+#define TE_STREAM_LPR(T)          \
+    do {                          \
+        if (lpr == 64) {          \
+            TE_STREAM_NR(T, 64);  \
+        } else if (lpr == 32) {   \
+            TE_STREAM_NR(T, 32);  \
+        } else {                  \
+            TE_STREAM_NR(T, 16);  \
+        }                         \
+    } while (0)
+                if (ggml_type == kGgmlQ4_0) {
+                    TE_STREAM_LPR(kGgmlQ4_0);
+                } else {
+                    TE_STREAM_LPR(kGgmlQ8_0);
+                }
+#undef TE_STREAM_LPR
+#undef TE_STREAM_NR
+#undef TE_STREAM_CH
+#undef TE_STREAM
+                return launch_status();
+            }
+        }
+        int nr = rows >= 4 * groups * want && ggml_type == kGgmlQ4_0 ? 4 : rows >= 2 * groups * want ? 2 : 1;
+        if (const char *env = getenv("TE_HIP_GEMV_NR")) {  // tuning override: rows per lane group
+            const int v = atoi(env);
+            nr = v == 1 || v == 2 || (v == 4 && ggml_type == kGgmlQ4_0) ? v : nr;
+        }
+        const size_t tiles = (rows + groups * nr - 1) / (groups * nr);
+        const dim3 grid((unsigned)(tiles < cus ? tiles : cus));
+        const dim3 block(kPairThreads);
+#define TE_PAIRS(T, L, N)                                                                                         \
+    do {                                                                                                          \
+        if (pair_lds_bytes > 65536 &&                                                                             \
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&matvec_pairs_kernel<T, L, N>),                    \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)pair_lds_bytes) != hipSuccess) { \
+            return TE_STATUS_RUNTIME_ERROR;                                                                       \
+        }                                                                                                         \
+        matvec_pairs_kernel<T, L, N><<<grid, block, pair_lds_bytes, stream>>>(w, input, (int)cols, (int)rows,     \
+                                                                             row_bytes, out, (int)tiles);         \
+    } while (0)
+#define TE_PAIRS_NR(T, L)                                    \
+    do {                                                     \
+        if (nr == 4) {                                       \
+            TE_PAIRS(T, L, (T == kGgmlQ4_0 ? 4 : 2));        \
+        } else if (nr == 2) {                                \
+            TE_PAIRS(T, L, 2);                               \
+        } else {                                             \
+            TE_PAIRS(T, L, 1);                               \
+        }                                                    \
+    } while (0)
+#define TE_PAIRS_LPR(T)          \
+    do {                         \
+        if (lpr == 64) {         \
+            TE_PAIRS_NR(T, 64);  \
+        } else if (lpr == 32) {  \
+            TE_PAIRS_NR(T, 32);  \
+        } else {                 \
+            TE_PAIRS_NR(T, 16);  \
+        }                        \
+    } while (0)
+        if (ggml_type == kGgmlQ4_0) {
+            TE_PAIRS_LPR(kGgmlQ4_0);
+        } else {
+            TE_PAIRS_LPR(kGgmlQ8_0);
+        }
+#undef TE_PAIRS_LPR
+#undef TE_PAIRS_NR
+#undef TE_PAIRS
+        return launch_status();
+    }
+    // F32, and quantized rows with an odd block count: one block (or float4) per lane step
     const int R = rows >= 4 * waves_wanted ? 4 : rows >= 2 * waves_wanted ? 2 : 1;
     const size_t rows_per_wg = (size_t)R * kMatvecWaves;
     const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg));
-    const unsigned char *w = static_cast<const unsigned char *>(weights);
 #define TE_MATVEC_LAUNCH(T)                                                                                   \
     do {                                                                                                      \
         if (R == 4) {                                                                                         \
@@ -339,6 +898,10 @@ extern "C" te_status te_hip_matvec_f32(const void *weights, uint32_t ggml_type, 
     }
     if (te_hip::ggml_row_bytes(ggml_type, cols) == 0 || cols > (1u << 24) || rows > (1u << 30)) {
         return TE_STATUS_UNSUPPORTED;  // other GGUF types, cols not a multiple of the block
+    }
+    // dword (quantized) / float4 (F32) weight reads and float4 input reads
+    if (((size_t)weights & (ggml_type == 0 ? 15u : 3u)) != 0 || ((size_t)input & 15u) != 0) {
+        return TE_STATUS_UNSUPPORTED;
     }
     return te_hip::launch_matvec(weights, ggml_type, input, cols, rows, out, te_hip::as_stream(stream));
 }
