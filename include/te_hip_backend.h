@@ -293,6 +293,52 @@ TE_API te_status te_hip_add_f32(const float *lhs, const float *rhs, size_t len, 
 TE_API te_status te_hip_argmax_f32(const float *values, size_t len, uint32_t *out_index, void *stream);
 
 /*
+ * One decode token through every layer (and, with out_token_id, the final
+ * norm, lm_head and argmax): replaces te_metal_decode_all_layers_f32
+ * (metal_backend.h:239-276, called by te_qwen_decode_all_layers_exact,
+ * qwen.c:1464-1640), with the same arguments and per-layer order as the CPU
+ * loop of te_qwen_forward_token (qwen.c:907-1087).  Differences from the Metal
+ * slot, all device-resident:
+ *   - `mapping` is the model file's bytes (or its tensor data) in HBM,
+ *     mapping_len bytes; the *_offsets arrays (host, `layers` entries each) and
+ *     head_offset are byte offsets into it, as the reference's absolute tensor
+ *     offsets.  Weights are [rows][cols] GGUF tensors of ggml_type (F32, Q4_0
+ *     or Q8_0; the head may have its own type); 16-byte aligned quantized
+ *     tensors take the fused kernels, 4-byte aligned ones a slower path.
+ *   - key_cache / value_cache are the HIP path's fp16 caches [layers]
+ *     [context_tokens][kv]; the new token's k / v are appended at `position`.
+ *   - rope_cos / rope_sin are the full tables [context_tokens][head_dim / 2]
+ *     (te_hip_rope_table_f32), not the position's row.
+ *   - hidden_in / out are device [hidden] (out may equal hidden_in: the
+ *     reference passes hidden_buf for both); out_token_id is a device uint32.
+ *   - workspace: device scratch of te_hip_decode_all_layers_workspace_bytes
+ *     (same position, sizes, and vocab or 0 without a head), 256-byte aligned.
+ * Asynchronous on `stream`; per layer six launches (RMSNorm + QKV, the fused
+ * decode step's two, Wo + residual, RMSNorm + gate/up, SwiGLU + down +
+ * residual).  Checks: null pointers, layers == 0, position >=
+ * context_tokens, epsilon <= 0, a tensor past mapping_len, a short workspace ->
+ * INVALID_ARGUMENT; hidden != heads * head_dim, kv != kv_heads * head_dim,
+ * head_dim not 64 / 128, other GGUF types, misaligned tensors or vectors ->
+ * UNSUPPORTED.  Numerics: each projection as te_hip_matvec_f32, RMSNorm as
+ * te_hip_rmsnorm_f32, SwiGLU as te_hip_swiglu_f32, attention as
+ * te_hip_attention_decode_step_f16.
+ */
+TE_API size_t te_hip_decode_all_layers_workspace_bytes(size_t position, size_t hidden, size_t kv, size_t heads,
+                                                       size_t kv_heads, size_t head_dim, size_t ffn, size_t vocab);
+TE_API te_status te_hip_decode_all_layers_f16(
+    const void *mapping, size_t mapping_len,
+    const uint64_t *q_offsets, const uint64_t *k_offsets, const uint64_t *v_offsets,
+    const uint64_t *output_offsets, const uint64_t *gate_offsets, const uint64_t *up_offsets,
+    const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weights, const float *ffn_norm_weights,
+    const float *q_biases, const float *k_biases, const float *v_biases,
+    const float *rope_cos, const float *rope_sin, uint16_t *key_cache, uint16_t *value_cache,
+    size_t position, size_t context_tokens, size_t hidden, size_t kv, size_t heads, size_t kv_heads,
+    size_t head_dim, size_t ffn, float epsilon, float *out,
+    uint64_t head_offset, uint32_t head_ggml_type, const float *output_norm_weight, size_t vocab,
+    uint32_t *out_token_id, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Measurement only, no counterpart in the reference: `blocks` workgroups of 8
  * waves each run `iters` rounds of 8 independent fp16 16x16x32 MFMAs on
  * register operands (blocks*8*iters*8*16384 FLOP), so a benchmark can report

@@ -274,3 +274,52 @@ def matvec_f32(data, ggml_type: int, x, cols: int, rows: int) -> np.ndarray:
     out = np.empty(rows, dtype=np.float32)
     _check(lib().orc_matvec_f32(_p(d, _u8p), ggml_type, _p(x, _f32p), cols, rows, _p(out, _f32p)), "matvec_f32")
     return out
+
+
+# ---- one decode token through every layer -----------------------------------
+
+def decode_all_layers(mapping, offsets, layers, ggml_type, hidden_in, attn_norm, ffn_norm, q_bias, k_bias, v_bias,
+                      cos, sin, key_cache, value_cache, position, context_tokens, hidden, kv, heads, kv_heads,
+                      head_dim, ffn, epsilon, head=None, output_norm=None, vocab=0):
+    """The reference's per-token layer loop (qwen.c:907-1087, te_qwen_forward_token)
+    composed from this package's restated functions, on the HIP path's fp16 cache:
+    per layer rmsnorm -> q/k/v matvec -> bias + RoPE + fp16 append
+    (rope_kv_append_f16) -> decode attention (attention_decode_f16kv) -> Wo +
+    residual -> rmsnorm -> gate/up -> SwiGLU -> Wd + residual; then, with
+    `head` = (offset, type), the greedy projection rmsnorm(output_norm) -> head
+    matvec -> argmax (qwen.c:1337-1375).  `mapping` is the model bytes (uint8),
+    `offsets` a dict of per-layer byte offsets (q, k, v, output, gate, up, down);
+    key_cache / value_cache are fp16 bits [layers][context][kv] and are updated
+    in place.  Returns (hidden, token or None, logits or None)."""
+    mp = np.ascontiguousarray(mapping, dtype=np.uint8)
+
+    def w(off, rows, cols, t=ggml_type):
+        n = rows * ggml_row_bytes(t, cols)
+        return mp[off:off + n]
+
+    x = np.array(hidden_in, dtype=np.float32, copy=True)
+    for l in range(layers):
+        norm = rmsnorm_f32(x, attn_norm[l], epsilon)
+        q = matvec_f32(w(offsets["q"][l], hidden, hidden), ggml_type, norm, hidden, hidden)
+        k = matvec_f32(w(offsets["k"][l], kv, hidden), ggml_type, norm, hidden, kv)
+        v = matvec_f32(w(offsets["v"][l], kv, hidden), ggml_type, norm, hidden, kv)
+        kc = key_cache[l]
+        vc = value_cache[l]
+        rope_kv_append_f16(q, k, v, np.ascontiguousarray(q_bias[l]), np.ascontiguousarray(k_bias[l]),
+                           np.ascontiguousarray(v_bias[l]), cos, sin, kc, vc, 1, 1, 1, None, position,
+                           context_tokens, heads, kv_heads, head_dim)
+        attn = attention_decode_f16kv(q, kc, vc, None, position, 1, 1, context_tokens, heads, kv_heads,
+                                      head_dim).reshape(-1)
+        proj = matvec_f32(w(offsets["output"][l], hidden, hidden), ggml_type, attn, hidden, hidden)
+        x = add_f32(x, proj)
+        norm = rmsnorm_f32(x, ffn_norm[l], epsilon)
+        gate = matvec_f32(w(offsets["gate"][l], ffn, hidden), ggml_type, norm, hidden, ffn)
+        up = matvec_f32(w(offsets["up"][l], ffn, hidden), ggml_type, norm, hidden, ffn)
+        proj = matvec_f32(w(offsets["down"][l], hidden, ffn), ggml_type, swiglu_f32(gate, up), ffn, hidden)
+        x = add_f32(x, proj)
+    if head is None:
+        return x, None, None
+    head_off, head_type = head
+    norm = rmsnorm_f32(x, output_norm, epsilon)
+    logits = matvec_f32(w(head_off, vocab, hidden, head_type), head_type, norm, hidden, vocab)
+    return x, argmax_f32(logits), logits

@@ -76,3 +76,53 @@ def ggml_tensor(seed: int, tag: str, ggml_type: int, rows: int, cols: int, scale
     out[:, 1] = d >> 8
     out[:, 2:] = codes
     return out.reshape(-1)
+
+
+def synthetic_model(seed: int, ggml_type: int, layers: int, heads: int, kv_heads: int, head_dim: int, ffn: int,
+                    vocab: int, context_tokens: int, position: int, head_type: int | None = None,
+                    misalign: int = 0) -> dict:
+    """A random Qwen2-shaped decode state: the tensor bytes of every layer's
+    seven projections and of the head packed into one `mapping` (each tensor
+    32-byte aligned as GGUF data, plus `misalign` bytes), per-layer norm weights
+    and biases, the input hidden state, and fp16 KV caches [layers][context][kv]
+    holding random history at positions below `position` (zeros above).
+    Block scales keep every projection's output near unit variance."""
+    hidden, kv = heads * head_dim, kv_heads * head_dim
+    head_type = ggml_type if head_type is None else head_type
+    code_std = {0: 1.0, 2: 4.6, 8: 74.0}
+
+    def tensor(tag, t, rows, cols):
+        return ggml_tensor(seed, tag, t, rows, cols, scale=1.0 / (code_std[t] * np.sqrt(cols)))
+
+    parts, offsets, cursor = [], {n: [] for n in ("q", "k", "v", "output", "gate", "up", "down")}, 0
+
+    def place(data):
+        nonlocal cursor
+        pad = (-cursor) % 32 + misalign
+        parts.append(np.zeros(pad, np.uint8))
+        cursor += pad
+        off = cursor
+        parts.append(data)
+        cursor += data.size
+        return off
+
+    shapes = {"q": (hidden, hidden), "k": (kv, hidden), "v": (kv, hidden), "output": (hidden, hidden),
+              "gate": (ffn, hidden), "up": (ffn, hidden), "down": (hidden, ffn)}
+    for l in range(layers):
+        for n, (rows, cols) in shapes.items():
+            offsets[n].append(place(tensor(f"w{n}{l}", ggml_type, rows, cols)))
+    head_off = place(tensor("head", head_type, vocab, hidden))
+    parts.append(np.zeros(64, np.uint8))
+    kc = np.zeros((layers, context_tokens, kv), np.uint16)
+    vc = np.zeros_like(kc)
+    kc[:, :position] = to_f16_bits(normal(seed, "kh", (layers, position, kv)))
+    vc[:, :position] = to_f16_bits(normal(seed, "vh", (layers, position, kv)))
+    return {
+        "mapping": np.concatenate(parts), "offsets": offsets, "head": (head_off, head_type),
+        "attn_norm": normal(seed, "an", (layers, hidden), 0.1) + 1.0,
+        "ffn_norm": normal(seed, "fn", (layers, hidden), 0.1) + 1.0,
+        "output_norm": normal(seed, "on", (hidden,), 0.1) + 1.0,
+        "q_bias": normal(seed, "qb", (layers, hidden), 0.1), "k_bias": normal(seed, "kb", (layers, kv), 0.1),
+        "v_bias": normal(seed, "vb", (layers, kv), 0.1), "hidden_in": normal(seed, "x", (hidden,)),
+        "key_cache": kc, "value_cache": vc, "hidden": hidden, "kv": kv,
+    }

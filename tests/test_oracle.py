@@ -403,3 +403,68 @@ def test_matvec_vs_fp64(oracle_mod, ggml_type, rows, cols):
     bound = cols * 2.0 ** -24 * (np.abs(w) @ np.abs(x.astype(np.float64))) + np.abs(exact) * 2.0 ** -23
     assert np.all(np.abs(got - exact) <= bound)
     assert oracle_mod.ggml_row_bytes(ggml_type, cols) * rows == data.size
+
+
+def test_decode_all_layers_composition_fp64(oracle_mod):
+    """The oracle's per-token layer loop against an fp64 numpy forward pass of the
+    same Qwen2 decode step (pre-norm attention block with q/k/v biases and
+    half-split RoPE, GQA over the fp16 cache, SwiGLU MLP, residuals, final norm,
+    head, argmax).  A misplaced residual, norm weight, bias or gate/up swap
+    moves the result far past the fp32-vs-fp64 agreement asserted here."""
+    import _synth as S
+    layers, heads, kv_heads, d, ffn, vocab, ctx, pos = 2, 4, 2, 64, 128, 60, 8, 5
+    m = S.synthetic_model(83, 8, layers, heads, kv_heads, d, ffn, vocab, ctx, pos)
+    hidden, kv, eps = m["hidden"], m["kv"], 1e-6
+    cos, sin = oracle_mod.rope_table(ctx, d, 1.0e6)
+    kc, vc = m["key_cache"].copy(), m["value_cache"].copy()
+    got_h, got_tok, got_logits = oracle_mod.decode_all_layers(
+        m["mapping"], m["offsets"], layers, 8, m["hidden_in"], m["attn_norm"], m["ffn_norm"], m["q_bias"],
+        m["k_bias"], m["v_bias"], cos, sin, kc, vc, pos, ctx, hidden, kv, heads, kv_heads, d, ffn, eps,
+        head=m["head"], output_norm=m["output_norm"], vocab=vocab)
+
+    mp = m["mapping"]
+
+    def W(name, l, rows, cols):
+        off = m["offsets"][name][l] if l is not None else m["head"][0]
+        n = rows * oracle_mod.ggml_row_bytes(8, cols)
+        return oracle_mod.dequantize_rows(mp[off:off + n], 8, cols, rows).astype(np.float64)
+
+    def norm(x, w):
+        return x / np.sqrt(np.mean(x * x) + eps) * w
+
+    def rope(x, nh):
+        x = x.reshape(nh, d).copy()
+        c, s = cos[pos].astype(np.float64), sin[pos].astype(np.float64)
+        a, b = x[:, :d // 2].copy(), x[:, d // 2:].copy()
+        x[:, :d // 2], x[:, d // 2:] = a * c - b * s, b * c + a * s
+        return x.reshape(-1)
+
+    x = m["hidden_in"].astype(np.float64)
+    kref = m["key_cache"].view(np.float16).astype(np.float64)
+    vref = m["value_cache"].view(np.float16).astype(np.float64)
+    for l in range(layers):
+        n = norm(x, m["attn_norm"][l])
+        q = rope(W("q", l, hidden, hidden) @ n + m["q_bias"][l], heads)
+        k = rope(W("k", l, kv, hidden) @ n + m["k_bias"][l], kv_heads)
+        v = W("v", l, kv, hidden) @ n + m["v_bias"][l]
+        kref[l, pos] = k.astype(np.float16).astype(np.float64)
+        vref[l, pos] = v.astype(np.float16).astype(np.float64)
+        attn = np.empty(hidden)
+        for h in range(heads):
+            g = h // (heads // kv_heads)
+            ks = kref[l, :pos + 1, g * d:(g + 1) * d]
+            sc = ks @ q[h * d:(h + 1) * d] / np.sqrt(d)
+            p = np.exp(sc - sc.max())
+            attn[h * d:(h + 1) * d] = (p / p.sum()) @ vref[l, :pos + 1, g * d:(g + 1) * d]
+        x = x + W("output", l, hidden, hidden) @ attn
+        n = norm(x, m["ffn_norm"][l])
+        gate, up = W("gate", l, ffn, hidden) @ n, W("up", l, ffn, hidden) @ n
+        x = x + W("down", l, hidden, ffn) @ (gate / (1.0 + np.exp(-gate)) * up)
+    logits = W("head", None, vocab, hidden) @ norm(x, m["output_norm"])
+    assert np.allclose(got_h, x, rtol=0, atol=2e-4 * np.abs(x).max())
+    assert np.allclose(got_logits, logits, rtol=0, atol=2e-4 * np.abs(logits).max())
+    assert got_tok == int(np.argmax(logits))
+    # the slot written into the cache is k / v rounded to fp16 once (within one fp16 step of fp64's)
+    for got, want in ((kc, kref), (vc, vref)):
+        g = got[:, pos].view(np.float16).astype(np.float64)
+        assert np.all(np.abs(g - want[:, pos]) <= 2.0 ** -10 * np.abs(want[:, pos]) + 2.0 ** -24)

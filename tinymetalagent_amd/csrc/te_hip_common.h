@@ -93,6 +93,24 @@ te_status launch_swiglu(const float *gate, const float *up, size_t len, float *o
 te_status launch_add(const float *lhs, const float *rhs, size_t len, float *out, hipStream_t stream);
 te_status launch_argmax(const float *values, size_t len, uint32_t *out_index, hipStream_t stream);
 
+// One weight matrix of a fused GEMV launch: out[r] = W[r] . x' (+ resid[r] when
+// resid is set; resid may equal out), r < rows.
+struct GemvSeg {
+    const void *w;
+    float *out;
+    const float *resid;
+    size_t rows;
+};
+enum GemvPre { kGemvPlain = 0, kGemvRmsNorm = 1, kGemvSwiGLU = 2 };
+// Up to three matrices of one type and width `cols` against one input x' =
+// x (plain), RMSNorm(x) * norm_w (as te_rmsnorm_f32) or silu(x) * x2 (as
+// te_swiglu_f32).  One streamed launch when the weights allow it; otherwise the
+// pre-operation into `xtmp` (cols floats), then te_hip_matvec_f32 per matrix
+// (into `ytmp`, rows floats, when it has a residual) and the residual add.
+te_status launch_gemv(uint32_t ggml_type, GemvPre pre, const GemvSeg *segs, int nseg, size_t cols, const float *x,
+                      const float *x2, const float *norm_w, float eps, float *xtmp, float *ytmp,
+                      hipStream_t stream);
+
 DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
                                size_t kv_heads);
 

@@ -35,6 +35,8 @@ constexpr int kPairThreads = 64 * kPairWaves;
 constexpr int kStageBatch = 4;                      // input float4 loads in flight per thread while staging
 constexpr size_t kMaxPairLdsBytes = 160 * 1024;     // staged digit planes (gfx950 LDS per CU)
 constexpr size_t kPairLdsBytes = 13 * 16;           // LDS per block pair: 12 uint4 of digit planes + scales
+constexpr int kStreamChunks = 10;                   // streamed kernel: 16-byte chunk loads per lane per tile
+constexpr size_t kStreamTileBytes = kStreamChunks * 1024;  // its LDS tile buffer per wave
 template <uint32_t TYPE>
 constexpr int kDigitPlanes = TYPE == kGgmlQ4_0 ? 6 : 3;  // balanced base-16 / base-256 digits of 22-bit X
 
@@ -199,91 +201,142 @@ __global__ __launch_bounds__(64 * kMatvecWaves) void matvec_kernel(const unsigne
 // and meet in one FMA.  The block adds d * 2^-e * that sum to the row.  Every
 // element costs 6 / 8 (Q4_0) or 3 / 4 (Q8_0) integer dot instructions.
 
-// Stage the input's digit planes and block scales (layout above) into LDS for
-// the whole workgroup; the caller synchronises.
-template <uint32_t TYPE>
-__device__ __forceinline__ void stage_digit_planes(const float *input, int pairs, uint32_t *xs_lds) {
-    const int nthreads = (int)blockDim.x;
-// Stage the input: coalesced float4 reads, kStageBatch per thread issued
-// before any is used.  Float4 i is block i / 8 (of pair i / 16), slice i % 8;
-// a block's 8 slices sit in 8 consecutive lanes, which share its max and its
-// digit dwords.  pairs * 16 is a multiple of 8, so those lanes agree on the bound.
-const int n4 = pairs * 16;
-for (int base = 0; base < n4; base += kStageBatch * nthreads) {
-    float4 v[kStageBatch];
-    // waves whose slice of a batch row starts past the input skip it (uniform branch)
-    const int wave_first = base + (int)(threadIdx.x & ~63u);
-#pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
-        const int i = base + u * nthreads + (int)threadIdx.x;
-        v[u] = i < n4 ? reinterpret_cast<const float4 *>(input)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+// Input pre-operations applied while staging (the decode layer fuses them
+// into its projections): kPreNone stages x; kPreRmsNorm stages x * scale * w
+// with scale = 1 / sqrtf(mean(x^2) + eps) as the reference te_rmsnorm_f32
+// (ops.c:272-293; squares summed in fp64, here per workgroup over the whole
+// vector); kPreSwiGLU stages silu(x) * x2 as te_swiglu_f32 (ops.c:397-406).
+enum : int { kPreNone = 0, kPreRmsNorm = 1, kPreSwiGLU = 2 };
+
+struct StageInput {
+    const float *x;
+    const float *x2;      // kPreSwiGLU: the up projection
+    const float *norm_w;  // kPreRmsNorm: the norm weight
+    float eps;            // kPreRmsNorm
+};
+
+// The RMSNorm scale of in.x[0, n) (n % 4 == 0) for the whole workgroup.
+__device__ __forceinline__ float workgroup_rms_scale(const StageInput &in, int n) {
+    __shared__ double part[kPairWaves];
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
+        const float4 v = reinterpret_cast<const float4 *>(in.x)[i];
+        ss += (double)v.x * v.x;
+        ss += (double)v.y * v.y;
+        ss += (double)v.z * v.z;
+        ss += (double)v.w * v.w;
     }
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
-        if (wave_first + u * nthreads >= n4) {
-            break;
-        }
-        const int i = base + u * nthreads + (int)threadIdx.x;
-        const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-        float m = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
-        int bad = !(isfinite(xv[0]) && isfinite(xv[1]) && isfinite(xv[2]) && isfinite(xv[3]));
+    for (int o = 32; o >= 1; o >>= 1) {
+        ss += __shfl_xor(ss, o, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    double total = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+        total += part[w];
+    }
+    return 1.0f / sqrtf((float)(total / (double)n) + in.eps);
+}
+
+// Stage the (pre-operated) input's digit planes and block scales (layout above)
+// into LDS for the whole workgroup; the caller synchronises.  Coalesced float4
+// reads, kStageBatch per thread issued before any is used.  Float4 i is block
+// i / 8 (of pair i / 16), slice i % 8; a block's 8 slices sit in 8 consecutive
+// lanes, which share its max and its digit dwords (pairs * 16 is a multiple of
+// 8, so those lanes agree on the bound).
+template <uint32_t TYPE, int PRE>
+__device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pairs, uint32_t *xs_lds) {
+    const int nthreads = (int)blockDim.x;
+    const int n4 = pairs * 16;
+    const float scale = PRE == kPreRmsNorm ? workgroup_rms_scale(in, n4 * 4) : 1.0f;
+    for (int base = 0; base < n4; base += kStageBatch * nthreads) {
+        float4 v[kStageBatch];
+        // waves whose slice of a batch row starts past the input skip it (uniform branch)
+        const int wave_first = base + (int)(threadIdx.x & ~63u);
 #pragma unroll
-        for (int o = 1; o <= 4; o <<= 1) {
-            m = fmaxf(m, __shfl_xor(m, o, 64));
-            bad |= __shfl_xor(bad, o, 64);
-        }
-        int ex = 0;
-        frexpf(m, &ex);  // m < 2^ex <= 2 m
-        // blocks whose max is below 2^-104 keep an absolute error of 2^-127
-        const int e = bad || m == 0.0f ? 0 : min(22 - ex, 126);
-        const int f = i & 7;
-        uint32_t planes[kDigitPlanes<TYPE>] = {};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int xq = bad ? 0 : (int)rintf(ldexpf(xv[j], e));  // |xq| <= 2^22
-#pragma unroll
-            for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                if (TYPE == kGgmlQ4_0) {
-                    const int d = ((xq + 8) & 15) - 8;
-                    xq = (xq - d) >> 4;
-                    planes[t] |= (uint32_t)(d & 15) << (8 * j + ((f & 4) ? 4 : 0));
-                } else {
-                    const int d = ((xq + 128) & 255) - 128;
-                    xq = (xq - d) >> 8;
-                    planes[t] |= (uint32_t)(d & 255) << (8 * j);
-                }
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int i = base + u * nthreads + (int)threadIdx.x;
+            v[u] = i < n4 ? reinterpret_cast<const float4 *>(in.x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (PRE == kPreRmsNorm && i < n4) {
+                const float4 w = reinterpret_cast<const float4 *>(in.norm_w)[i];
+                v[u] = make_float4(v[u].x * scale * w.x, v[u].y * scale * w.y, v[u].z * scale * w.z,
+                                   v[u].w * scale * w.w);
+            } else if (PRE == kPreSwiGLU && i < n4) {
+                const float4 up = reinterpret_cast<const float4 *>(in.x2)[i];
+                const float4 g = v[u];
+                v[u] = make_float4(g.x / (1.0f + expf(-g.x)) * up.x, g.y / (1.0f + expf(-g.y)) * up.y,
+                                   g.z / (1.0f + expf(-g.z)) * up.z, g.w / (1.0f + expf(-g.w)) * up.w);
             }
         }
-        if (TYPE == kGgmlQ4_0) {
-            // slices f and f + 4 fill the even and odd nibbles of dword f
 #pragma unroll
-            for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                planes[t] |= __shfl_xor(planes[t], 4, 64);
+        for (int u = 0; u < kStageBatch; ++u) {
+            if (wave_first + u * nthreads >= n4) {
+                break;
             }
-        }
-        if (i < n4) {
-            const int p = i >> 4, c = (i >> 3) & 1;
-            uint32_t *slot = xs_lds + p * 52 + c * 24;
-            if (TYPE == kGgmlQ4_0) {
-                if (f < 4) {
+            const int i = base + u * nthreads + (int)threadIdx.x;
+            const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            float m = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
+            int bad = !(isfinite(xv[0]) && isfinite(xv[1]) && isfinite(xv[2]) && isfinite(xv[3]));
 #pragma unroll
-                    for (int t = 0; t < 6; ++t) {
-                        slot[4 * t + f] = planes[t];
+            for (int o = 1; o <= 4; o <<= 1) {
+                m = fmaxf(m, __shfl_xor(m, o, 64));
+                bad |= __shfl_xor(bad, o, 64);
+            }
+            int ex = 0;
+            frexpf(m, &ex);  // m < 2^ex <= 2 m
+            // blocks whose max is below 2^-104 keep an absolute error of 2^-127
+            const int e = bad || m == 0.0f ? 0 : min(22 - ex, 126);
+            const int f = i & 7;
+            uint32_t planes[kDigitPlanes<TYPE>] = {};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int xq = bad ? 0 : (int)rintf(ldexpf(xv[j], e));  // |xq| <= 2^22
+#pragma unroll
+                for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
+                    if (TYPE == kGgmlQ4_0) {
+                        const int d = ((xq + 8) & 15) - 8;
+                        xq = (xq - d) >> 4;
+                        planes[t] |= (uint32_t)(d & 15) << (8 * j + ((f & 4) ? 4 : 0));
+                    } else {
+                        const int d = ((xq + 128) & 255) - 128;
+                        xq = (xq - d) >> 8;
+                        planes[t] |= (uint32_t)(d & 255) << (8 * j);
                     }
                 }
-            } else {
+            }
+            if (TYPE == kGgmlQ4_0) {
+                // slices f and f + 4 fill the even and odd nibbles of dword f
 #pragma unroll
-                for (int t = 0; t < 3; ++t) {
-                    slot[8 * t + f] = planes[t];
+                for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
+                    planes[t] |= __shfl_xor(planes[t], 4, 64);
                 }
             }
-            if (f == 0) {
-                // a non-finite input makes the block's rows NaN
-                xs_lds[p * 52 + 48 + c] = __float_as_uint(bad ? __builtin_nanf("") : ldexpf(1.0f, -e));
+            if (i < n4) {
+                const int p = i >> 4, c = (i >> 3) & 1;
+                uint32_t *slot = xs_lds + p * 52 + c * 24;
+                if (TYPE == kGgmlQ4_0) {
+                    if (f < 4) {
+#pragma unroll
+                        for (int t = 0; t < 6; ++t) {
+                            slot[4 * t + f] = planes[t];
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 3; ++t) {
+                        slot[8 * t + f] = planes[t];
+                    }
+                }
+                if (f == 0) {
+                    // a non-finite input makes the block's rows NaN
+                    xs_lds[p * 52 + 48 + c] = __float_as_uint(bad ? __builtin_nanf("") : ldexpf(1.0f, -e));
+                }
             }
         }
     }
-}
 }
 
 // acc + the row's block pair (PW dwords w) against the lane's digit planes xq
@@ -381,7 +434,7 @@ __global__ __launch_bounds__(kPairThreads) void matvec_pairs_kernel(const unsign
         load(wa, gwave, 0);
     }
 
-    stage_digit_planes<TYPE>(input, pairs, xs_lds);
+    stage_digit_planes<TYPE, kPreNone>(StageInput{input, nullptr, nullptr, 0.0f}, pairs, xs_lds);
     __syncthreads();
     if (gwave >= tiles) {
         return;
@@ -481,11 +534,30 @@ __global__ __launch_bounds__(kPairThreads) void matvec_pairs_kernel(const unsign
 // next tile is stored over the buffer after the current one's reads with no
 // barrier.  CH chunk loads per lane: CH KB >= the tile plus 15 bytes of
 // misalignment (tiles start on dword, not 16-byte, boundaries).
-template <uint32_t TYPE, int LPR, int NR, int CH>
-__global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsigned char *weights,
-                                                                    const float *input, int cols, int rows,
-                                                                    size_t row_bytes, float *out, int tiles,
-                                                                    size_t total_chunks) {
+// One weight matrix of a streamed launch: out[r] = W[r] . x' (+ resid[r] when
+// resid is set; resid may be out) for r < rows.  A launch takes up to three
+// matrices of the same type and width, one input; their row tiles are numbered
+// one after another.
+struct StreamSeg {
+    const unsigned char *w;
+    float *out;
+    const float *resid;
+    size_t total_chunks;  // rows * row_bytes / 16
+    int rows;
+    int tiles;
+};
+
+struct StreamArgs {
+    StreamSeg seg[3];
+    int nseg;
+    int tiles;  // all segments
+    int cols;
+    size_t row_bytes;
+    StageInput in;
+};
+
+template <uint32_t TYPE, int LPR, int NR, int CH, int PRE>
+__global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const StreamArgs a) {
     constexpr int PW = TYPE == kGgmlQ4_0 ? 9 : 17;  // dwords per block pair
     constexpr int G = 64 / LPR;                      // row groups per wave
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -494,21 +566,45 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsig
     const int lane = threadIdx.x & 63;
     const int grp = lane / LPR;
     const int li = lane % LPR;
-    const int wave = (int)(threadIdx.x >> 6);
+    // the wave index through readfirstlane: the compiler then keeps every
+    // tile-derived value (segment fields included) in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     // tile t goes to wave t mod waves; consecutive tiles land on different CUs
     const int gwave = wave * gridDim.x + blockIdx.x;
     const int nwaves = gridDim.x * (int)(blockDim.x >> 6);
-    const int pairs = cols / 64;
+    const int pairs = a.cols / 64;
     const int steps = (pairs + LPR - 1) / LPR;  // pair steps per tile
-    const size_t tile_bytes = (size_t)G * NR * row_bytes;
+    const size_t tile_bytes = (size_t)G * NR * a.row_bytes;
     uint4 *const buf = lds4 + pairs * 13 + wave * CH * 64;
-    const u32x4 *const w16 = reinterpret_cast<const u32x4 *>(weights);
 
+    // Segment of global tile t, as values chosen by scalar selects: indexing the
+    // kernel-argument array (or taking a reference into it) with a run-time index
+    // makes the compiler read it with vector loads and wait on them in the loop.
+    auto seg_of = [&](int t, int &local) {
+        const int t0 = a.seg[0].tiles, t1 = a.seg[1].tiles;
+        const int s = t < t0 ? 0 : (a.nseg > 2 && t >= t0 + t1) ? 2 : 1;
+        local = s == 0 ? t : s == 1 ? t - t0 : t - t0 - t1;
+        StreamSeg g;
+        g.w = s == 0 ? a.seg[0].w : s == 1 ? a.seg[1].w : a.seg[2].w;
+        g.out = s == 0 ? a.seg[0].out : s == 1 ? a.seg[1].out : a.seg[2].out;
+        g.resid = s == 0 ? a.seg[0].resid : s == 1 ? a.seg[1].resid : a.seg[2].resid;
+        g.total_chunks = s == 0 ? a.seg[0].total_chunks : s == 1 ? a.seg[1].total_chunks : a.seg[2].total_chunks;
+        g.rows = s == 0 ? a.seg[0].rows : s == 1 ? a.seg[1].rows : a.seg[2].rows;
+        return g;
+    };
+
+    // A tile's loads: its weight chunks and (residual launches) the residuals of
+    // its rows, issued together one tile ahead, so the wait for them at the next
+    // tile's start never waits for loads issued later.
     u32x4 ck[CH] = {};
+    float res[NR];
     auto load = [&](int tile) {
-        const size_t b = (size_t)tile * tile_bytes;
+        int local;
+        const StreamSeg sg = seg_of(tile, local);
+        const size_t b = (size_t)local * tile_bytes;
         const size_t c0 = b >> 4;
-        const size_t c1 = min((b + tile_bytes + 15) >> 4, total_chunks);
+        const size_t c1 = min((b + tile_bytes + 15) >> 4, sg.total_chunks);
+        const u32x4 *w16 = reinterpret_cast<const u32x4 *>(sg.w);
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const size_t c = c0 + lane + 64 * i;
@@ -516,13 +612,18 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsig
                 ck[i] = __builtin_nontemporal_load(w16 + c);
             }
         }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int row = (local * G + grp) * NR + r;
+            res[r] = sg.resid != nullptr && li == 0 && row < sg.rows ? sg.resid[row] : 0.0f;
+        }
     };
-    if (gwave < tiles) {
+    if (gwave < a.tiles) {
         load(gwave);
     }
-    stage_digit_planes<TYPE>(input, pairs, xs_lds);
+    stage_digit_planes<TYPE, PRE>(a.in, pairs, xs_lds);
     __syncthreads();
-    if (gwave >= tiles) {
+    if (gwave >= a.tiles) {
         return;
     }
 
@@ -554,11 +655,19 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsig
         for (int i = 0; i < CH; ++i) {
             buf[lane + 64 * i] = make_uint4(ck[i].x, ck[i].y, ck[i].z, ck[i].w);
         }
+        float res_cur[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            res_cur[r] = res[r];
+        }
+        int local;
+        const StreamSeg sg = seg_of(tile, local);
         const int tn = tile + nwaves;
-        if (tn < tiles) {
+        if (tn < a.tiles) {
             load(tn);
         }
-        const unsigned char *tb = reinterpret_cast<const unsigned char *>(buf) + (((size_t)tile * tile_bytes) & 15);
+        const unsigned char *tb =
+            reinterpret_cast<const unsigned char *>(buf) + (((size_t)local * tile_bytes) & 15);
         for (int step = 0; step < steps; ++step) {
             const int p = li + step * LPR;
             if (steps > 1) {
@@ -567,8 +676,8 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsig
             if (p < pairs) {
 #pragma unroll
                 for (int r = 0; r < NR; ++r) {
-                    const uint32_t *src =
-                        reinterpret_cast<const uint32_t *>(tb + (size_t)(grp * NR + r) * row_bytes + (size_t)p * 4 * PW);
+                    const uint32_t *src = reinterpret_cast<const uint32_t *>(
+                        tb + (size_t)(grp * NR + r) * a.row_bytes + (size_t)p * 4 * PW);
                     uint32_t w[PW];
 #pragma unroll
                     for (int k = 0; k < PW; ++k) {
@@ -585,13 +694,14 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const unsig
             for (int o = LPR / 2; o >= 1; o >>= 1) {
                 v += __shfl_xor(v, o, 64);
             }
-            const int row = (tile * G + grp) * NR + r;
-            if (li == 0 && row < rows) {
-                out[row] = v;
+            const int row = (local * G + grp) * NR + r;
+            if (li == 0 && row < sg.rows) {
+                // the residual add of the reference's te_add_f32(hidden, proj)
+                sg.out[row] = sg.resid != nullptr ? res_cur[r] + v : v;
             }
             acc[r] = 0.0f;
         }
-        if (tn >= tiles) {
+        if (tn >= a.tiles) {
             break;
         }
         tile = tn;
@@ -696,6 +806,115 @@ size_t ggml_row_bytes(uint32_t ggml_type, size_t cols) {
     }
 }
 
+// Streamed GEMV launch over a.seg[0, a.nseg) with input pre-operation `pre`
+// (a.cols, a.in and each segment's w / out / resid / rows set by the caller;
+// the tile shape, tile counts and chunk bounds are filled in here).  *launched
+// stays false, with OK, when the shapes do not suit the streamed kernel: a
+// weight tensor not 16-byte aligned or not a multiple of 16 bytes long, a row
+// group longer than the 10 KB tile, or staged input leaving LDS for fewer than
+// 4 waves.
+te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t stream, bool *launched) {
+    *launched = false;
+    const size_t cols = (size_t)a.cols;
+    if ((ggml_type != kGgmlQ4_0 && ggml_type != kGgmlQ8_0) || cols % 64 != 0 || a.nseg < 1 || a.nseg > 3) {
+        return TE_STATUS_OK;
+    }
+    const size_t row_bytes = ggml_row_bytes(ggml_type, cols);
+    const size_t pairs = cols / 64;
+    const size_t plane_bytes = pairs * kPairLdsBytes;
+    size_t rows_total = 0;
+    for (int s = 0; s < a.nseg; ++s) {
+        const size_t rows = (size_t)a.seg[s].rows;
+        if (((size_t)a.seg[s].w & 15u) != 0 || rows * row_bytes % 16 != 0) {
+            return TE_STATUS_OK;
+        }
+        rows_total += rows;
+    }
+    const int lpr = pairs >= 64 ? 64 : pairs >= 32 ? 32 : 16;
+    const size_t groups = 64 / lpr;
+    const size_t cus = (size_t)device_compute_units();
+    const size_t want = cus * 8;
+    // tiles of at most 10 KB (larger tiles measured faster at lm_head, 4 / 8 / 12 KB: more bytes
+    // in flight per wave), as many rows as keep every CU at 8 waves
+    size_t tile_cap = kStreamTileBytes;
+    if (const char *env = getenv("TE_HIP_GEMV_TILE")) {  // tuning override: bytes per row-group tile
+        tile_cap = (size_t)atoi(env) >= 1024 && (size_t)atoi(env) <= kStreamTileBytes ? (size_t)atoi(env) : tile_cap;
+    }
+    int nr = 1;
+    for (int cand = 2; cand <= (ggml_type == kGgmlQ4_0 ? 4 : 2); cand *= 2) {
+        if (groups * cand * row_bytes + 15 <= tile_cap && rows_total >= cand * groups * want) {
+            nr = cand;
+        }
+    }
+    const size_t waves_fit = groups * row_bytes + 15 <= kStreamTileBytes && plane_bytes < kMaxPairLdsBytes
+                                 ? (kMaxPairLdsBytes - plane_bytes) / kStreamTileBytes
+                                 : 0;
+    if (waves_fit < 4) {
+        return TE_STATUS_OK;
+    }
+    const int wpg = waves_fit < (size_t)kPairWaves ? (int)waves_fit : kPairWaves;
+    const size_t lds = plane_bytes + (size_t)wpg * kStreamTileBytes;
+    a.row_bytes = row_bytes;
+    a.tiles = 0;
+    for (int s = 0; s < a.nseg; ++s) {
+        const size_t rows = (size_t)a.seg[s].rows;
+        a.seg[s].tiles = (int)((rows + groups * nr - 1) / (groups * nr));
+        a.seg[s].total_chunks = rows * row_bytes / 16;
+        a.tiles += a.seg[s].tiles;
+    }
+    const dim3 grid((unsigned)((size_t)a.tiles < cus ? (size_t)a.tiles : cus));
+#define TE_STREAM(T, L, N, P)                                                                                      \
+    do {                                                                                                           \
+        if (lds > 65536 &&                                                                                         \
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, kStreamChunks, P>),  \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {             \
+            return TE_STATUS_RUNTIME_ERROR;                                                                        \
+        }                                                                                                          \
+        matvec_stream_kernel<T, L, N, kStreamChunks, P><<<grid, dim3(64 * wpg), lds, stream>>>(a);                 \
+    } while (0)
+#define TE_STREAM_PRE(T, L, N)                \
+    do {                                      \
+        if (pre == kPreRmsNorm) {             \
+            TE_STREAM(T, L, N, kPreRmsNorm);  \
+        } else if (pre == kPreSwiGLU) {       \
+            TE_STREAM(T, L, N, kPreSwiGLU);   \
+        } else {                              \
+            TE_STREAM(T, L, N, kPreNone);     \
+        }                                     \
+    } while (0)
+#define TE_STREAM_NR(T, L)                                    \
+    do {                                                      \
+        if (nr == 4) {                                        \
+            TE_STREAM_PRE(T, L, (T == kGgmlQ4_0 ? 4 : 2));    \
+        } else if (nr == 2) {                                 \
+            TE_STREAM_PRE(T, L, 2);                           \
+        } else {                                              \
+            TE_STREAM_PRE(T, L, 1);                           \
+        }                                                     \
+    } while (0)
+#define TE_STREAM_LPR(T)          \
+    do {                          \
+        if (lpr == 64) {          \
+            TE_STREAM_NR(T, 64);  \
+        } else if (lpr == 32) {   \
+            TE_STREAM_NR(T, 32);  \
+        } else {                  \
+            TE_STREAM_NR(T, 16);  \
+        }                         \
+    } while (0)
+    if (ggml_type == kGgmlQ4_0) {
+        TE_STREAM_LPR(kGgmlQ4_0);
+    } else {
+        TE_STREAM_LPR(kGgmlQ8_0);
+    }
+#undef TE_STREAM_LPR
+#undef TE_STREAM_NR
+#undef TE_STREAM_PRE
+#undef TE_STREAM
+    *launched = true;
+    return launch_status();
+}
+
 te_status launch_matvec(const void *weights, uint32_t ggml_type, const float *input, size_t cols, size_t rows,
                         float *out, hipStream_t stream) {
     const size_t row_bytes = ggml_row_bytes(ggml_type, cols);
@@ -711,79 +930,16 @@ te_status launch_matvec(const void *weights, uint32_t ggml_type, const float *in
         const size_t groups = 64 / lpr;
         const size_t cus = (size_t)device_compute_units();
         const size_t want = cus * 8;
-        if (((size_t)weights & 15u) == 0 && rows * row_bytes % 16 == 0 && getenv("TE_HIP_GEMV_STRIDED") == nullptr) {
-            // streamed: row-group tiles of at most 12 KB (measured best of 4 / 8 / 12 KB at
-            // lm_head: more bytes in flight per wave), as many rows as keep every CU at 8
-            // waves; waves per workgroup as the LDS allows
-            int snr = 1;
-            size_t tile_cap = 12288;
-            if (const char *env = getenv("TE_HIP_GEMV_TILE")) {  // tuning override: bytes per row-group tile
-                tile_cap = (size_t)atoi(env) >= 1024 ? (size_t)atoi(env) : tile_cap;
-            }
-            for (int cand = 2; cand <= (ggml_type == kGgmlQ4_0 ? 4 : 2); cand *= 2) {
-                if (groups * cand * row_bytes + 15 <= tile_cap && rows >= cand * groups * want) {
-                    snr = cand;
-                }
-            }
-            const size_t tile_bytes = groups * snr * row_bytes;
-            const int ch = tile_bytes + 15 <= 4096 ? 4 : tile_bytes + 15 <= 8192 ? 8 : 12;
-            const size_t waves_fit = tile_bytes + 15 <= 12288 ? (kMaxPairLdsBytes - pair_lds_bytes) / (ch * 1024) : 0;
-            if (waves_fit >= 4) {
-                const int wpg = waves_fit < (size_t)kPairWaves ? (int)waves_fit : kPairWaves;
-                const size_t lds = pair_lds_bytes + (size_t)wpg * ch * 1024;
-                const size_t stiles = (rows + groups * snr - 1) / (groups * snr);
-                const dim3 sgrid((unsigned)(stiles < cus ? stiles : cus));
-                const size_t total_chunks = rows * row_bytes / 16;
-#define TE_STREAM(T, L, N, C)                                                                                     \
-    do {                                                                                                          \
-        if (lds > 65536 &&                                                                                        \
-            hipFuncSetAttribute(reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, C>),                \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {            \
-            return TE_STATUS_RUNTIME_ERROR;                                                                       \
-        }                                                                                                         \
-        matvec_stream_kernel<T, L, N, C><<<sgrid, dim3(64 * wpg), lds, stream>>>(                                 \
-            w, input, (int)cols, (int)rows, row_bytes, out, (int)stiles, total_chunks);                           \
-    } while (0)
-#define TE_STREAM_CH(T, L, N)       \
-    do {                            \
-        if (ch == 4) {              \
-            TE_STREAM(T, L, N, 4);  \
-        } else if (ch == 8) {       \
-            TE_STREAM(T, L, N, 8);  \
-        } else {                    \
-            TE_STREAM(T, L, N, 12); \
-        }                           \
-    } while (0)
-#define TE_STREAM_NR(T, L)                                       \
-    do {                                                         \
-        if (snr == 4) {                                          \
-            TE_STREAM_CH(T, L, (T == kGgmlQ4_0 ? 4 : 2));        \
-        } else if (snr == 2) {                                   \
-            TE_STREAM_CH(T, L, 2);                               \
-        } else {                                                 \
-            TE_STREAM_CH(T, L, 1);                               \
-        }                                                        \
-    } while (0)
-#define TE_STREAM_LPR(T)          \
-    do {                          \
-        if (lpr == 64) {          \
-            TE_STREAM_NR(T, 64);  \
-        } else if (lpr == 32) {   \
-            TE_STREAM_NR(T, 32);  \
-        } else {                  \
-            TE_STREAM_NR(T, 16);  \
-        }                         \
-    } while (0)
-                if (ggml_type == kGgmlQ4_0) {
-                    TE_STREAM_LPR(kGgmlQ4_0);
-                } else {
-                    TE_STREAM_LPR(kGgmlQ8_0);
-                }
-#undef TE_STREAM_LPR
-#undef TE_STREAM_NR
-#undef TE_STREAM_CH
-#undef TE_STREAM
-                return launch_status();
+        if (getenv("TE_HIP_GEMV_STRIDED") == nullptr) {
+            StreamArgs a = {};
+            a.seg[0] = StreamSeg{w, out, nullptr, 0, (int)rows, 0};
+            a.nseg = 1;
+            a.cols = (int)cols;
+            a.in = StageInput{input, nullptr, nullptr, 0.0f};
+            bool launched = false;
+            const te_status st = launch_stream(ggml_type, kPreNone, a, stream, &launched);
+            if (launched || st != TE_STATUS_OK) {
+                return st;
             }
         }
         int nr = rows >= 4 * groups * want && ggml_type == kGgmlQ4_0 ? 4 : rows >= 2 * groups * want ? 2 : 1;
@@ -860,6 +1016,47 @@ te_status launch_matvec(const void *weights, uint32_t ggml_type, const float *in
     }
 #undef TE_MATVEC_LAUNCH
     return launch_status();
+}
+
+te_status launch_gemv(uint32_t ggml_type, GemvPre pre, const GemvSeg *segs, int nseg, size_t cols, const float *x,
+                      const float *x2, const float *norm_w, float eps, float *xtmp, float *ytmp,
+                      hipStream_t stream) {
+    if (getenv("TE_HIP_GEMV_STRIDED") == nullptr && nseg >= 1 && nseg <= 3) {
+        StreamArgs a = {};
+        for (int s = 0; s < nseg; ++s) {
+            a.seg[s] = StreamSeg{static_cast<const unsigned char *>(segs[s].w), segs[s].out, segs[s].resid, 0,
+                                 (int)segs[s].rows, 0};
+        }
+        a.nseg = nseg;
+        a.cols = (int)cols;
+        a.in = StageInput{x, x2, norm_w, eps};
+        const int kpre = pre == kGemvRmsNorm ? kPreRmsNorm : pre == kGemvSwiGLU ? kPreSwiGLU : kPreNone;
+        bool launched = false;
+        const te_status st = launch_stream(ggml_type, kpre, a, stream, &launched);
+        if (launched || st != TE_STATUS_OK) {
+            return st;
+        }
+    }
+    const float *input = x;
+    te_status st = TE_STATUS_OK;
+    if (pre == kGemvRmsNorm) {
+        st = launch_rmsnorm(x, norm_w, 1, cols, eps, xtmp, stream);
+        input = xtmp;
+    } else if (pre == kGemvSwiGLU) {
+        st = launch_swiglu(x, x2, cols, xtmp, stream);
+        input = xtmp;
+    }
+    for (int s = 0; s < nseg && st == TE_STATUS_OK; ++s) {
+        if (segs[s].resid == nullptr) {
+            st = launch_matvec(segs[s].w, ggml_type, input, cols, segs[s].rows, segs[s].out, stream);
+        } else {
+            st = launch_matvec(segs[s].w, ggml_type, input, cols, segs[s].rows, ytmp, stream);
+            if (st == TE_STATUS_OK) {
+                st = launch_add(segs[s].resid, ytmp, segs[s].rows, segs[s].out, stream);
+            }
+        }
+    }
+    return st;
 }
 
 te_status launch_rmsnorm(const float *input, const float *weight, size_t rows, size_t len, float epsilon, float *out,
