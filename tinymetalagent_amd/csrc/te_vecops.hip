@@ -291,19 +291,21 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
             const int e = bad || m == 0.0f ? 0 : min(22 - ex, 126);
             const int f = i & 7;
             uint32_t planes[kDigitPlanes<TYPE>] = {};
+            // Balanced digits from plain ones: with B = sum_t 8 * 16^t (Q4_0) or
+            // sum_t 128 * 256^t (Q8_0), Y = X + B lies in [0, 2^24), and digit t of X is
+            // (digit t of Y) - 8 (or - 128), whose 4- (8-) bit two's complement is
+            // digit t of Y with its top bit flipped: one field extract per digit, the
+            // flips done on whole plane dwords.
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int xq = bad ? 0 : (int)rintf(ldexpf(xv[j], e));  // |xq| <= 2^22
+                const int xq = bad ? 0 : (int)rintf(ldexpf(xv[j], e));  // |xq| <= 2^22
+                const uint32_t y = (uint32_t)(xq + (TYPE == kGgmlQ4_0 ? 0x888888 : 0x808080));
 #pragma unroll
                 for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
                     if (TYPE == kGgmlQ4_0) {
-                        const int d = ((xq + 8) & 15) - 8;
-                        xq = (xq - d) >> 4;
-                        planes[t] |= (uint32_t)(d & 15) << (8 * j + ((f & 4) ? 4 : 0));
+                        planes[t] |= ((y >> (4 * t)) & 15u) << (8 * j + ((f & 4) ? 4 : 0));
                     } else {
-                        const int d = ((xq + 128) & 255) - 128;
-                        xq = (xq - d) >> 8;
-                        planes[t] |= (uint32_t)(d & 255) << (8 * j);
+                        planes[t] |= ((y >> (8 * t)) & 255u) << (8 * j);
                     }
                 }
             }
@@ -311,7 +313,12 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
                 // slices f and f + 4 fill the even and odd nibbles of dword f
 #pragma unroll
                 for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                    planes[t] |= __shfl_xor(planes[t], 4, 64);
+                    planes[t] = (planes[t] | __shfl_xor(planes[t], 4, 64)) ^ 0x88888888u;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
+                    planes[t] ^= 0x80808080u;
                 }
             }
             if (i < n4) {
@@ -763,12 +770,34 @@ __device__ __forceinline__ void argmax_take(float &bv, uint32_t &bi, float v, ui
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *values, uint32_t len, uint32_t *out_index) {
     float bv = -FLT_MAX;
     uint32_t bi = 0xffffffffu;
-    for (uint32_t i = threadIdx.x; i < len; i += 1024) {
-        const float v = values[i];
-        if (v > bv) {  // strictly greater: the first maximum of this thread's stride
+    // strictly greater: the first maximum of this thread's indices, which it
+    // visits in increasing order (float4 slices t, t + 1024, ..., then the tail)
+    auto take = [&](float v, uint32_t i) {
+        if (v > bv) {
             bv = v;
             bi = i;
         }
+    };
+    const uint32_t n4 = ((size_t)values & 15u) == 0 ? len / 4 : 0;
+    const float4 *v4 = reinterpret_cast<const float4 *>(values);
+    for (uint32_t base = 0; base < n4; base += 4 * 1024) {
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {  // all loads issued before the compares
+            const uint32_t j = base + u * 1024 + threadIdx.x;
+            q[u] = j < n4 ? v4[j] : make_float4(-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t i = 4 * (base + u * 1024 + threadIdx.x);
+            take(q[u].x, i);
+            take(q[u].y, i + 1);
+            take(q[u].z, i + 2);
+            take(q[u].w, i + 3);
+        }
+    }
+    for (uint32_t i = 4 * n4 + threadIdx.x; i < len; i += 1024) {
+        take(values[i], i);
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
