@@ -473,6 +473,108 @@ def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, rep
     return res
 
 
+def graph_time_us(torch, launches, reps: int) -> float:
+    """Mean microseconds per launch of `launches` (a list of callables taking a
+    stream), captured once into a HIP graph and replayed: no host launch cost."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    for f in launches:
+        f(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for f in launches:
+            f(s)
+    torch.cuda.synchronize()
+    settle(torch, g.replay, 0.25)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+
+
+def random_ggml(torch, ggml_type: int, nbytes: int):
+    """Random GGUF block bytes on the GPU with every block scale set to a small
+    finite fp16 (0x2000 = 2^-7), so no NaN / inf reaches the sums."""
+    w = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+    blocks = w[: nbytes // (18 if ggml_type == 2 else 34) * (18 if ggml_type == 2 else 34)]
+    blocks = blocks.view(-1, 18 if ggml_type == 2 else 34)
+    blocks[:, 0] = 0
+    blocks[:, 1] = 0x20
+    return w
+
+
+def gemv_case(torch, V, ggml_type: int, rows: int, cols: int, reps: int = 100) -> dict:
+    """te_hip_matvec_f32 on a [rows][cols] tensor: weight copies rotated so that
+    >= 1.2 GB is streamed per replay round (no MALL reuse), graph-replayed."""
+    nbytes = rows * V.row_bytes(ggml_type, cols)
+    copies = max(2, min(64, math.ceil(1.2e9 / nbytes)))
+    ws = [random_ggml(torch, ggml_type, nbytes) for _ in range(copies)]
+    x = torch.randn(cols, device="cuda")
+    out = torch.empty(rows, device="cuda")
+    us = graph_time_us(torch, [lambda s, w=w: V.matvec(w, ggml_type, x, rows, out=out, stream=s) for w in ws],
+                       max(1, reps // copies))
+    moved = nbytes + 4 * (cols + rows)
+    del ws
+    torch.cuda.empty_cache()
+    return {"us": r(us, 2), "gbs": round(moved / us / 1e3, 1), "frac": r(moved / us / 1e3 / HBM_PEAK_GBS),
+            "bytes_per_launch": moved}
+
+
+def decode_layers_case(torch, LY, V, ggml_type: int, *, layers=36, heads=16, kv_heads=2, d=128, ffn=11008,
+                       vocab=151936, ctx=8192, reps=30) -> dict:
+    """One decode token through every layer (te_hip_decode_all_layers_f16) at
+    Qwen2.5-3B shapes: position ctx-1, random weights of the given GGUF type (one
+    set: at 1.7 / 3.3 GB it exceeds the MALL by itself), greedy head + argmax."""
+    hidden, kv = heads * d, kv_heads * d
+    rb = lambda cols: V.row_bytes(ggml_type, cols)
+    shapes = [("q", hidden, hidden), ("k", kv, hidden), ("v", kv, hidden), ("output", hidden, hidden),
+              ("gate", ffn, hidden), ("up", ffn, hidden), ("down", hidden, ffn)]
+    offsets, cur, regions = {n: [] for n, _, _ in shapes}, 0, []
+    for _ in range(layers):
+        for n, rows, cols in shapes:
+            offsets[n].append(cur)
+            regions.append((cur, rows * rb(cols)))
+            cur += (rows * rb(cols) + 255) // 256 * 256
+    head_off = cur
+    regions.append((cur, vocab * rb(hidden)))
+    cur += (vocab * rb(hidden) + 255) // 256 * 256
+    mapping = torch.randint(0, 256, (cur,), dtype=torch.uint8, device="cuda")
+    bb = 18 if ggml_type == 2 else 34
+    for off, n in regions:
+        blk = mapping[off:off + n].view(-1, bb)
+        blk[:, 0] = 0
+        blk[:, 1] = 0x20
+    g = torch.Generator(device="cuda").manual_seed(42)
+    ones = lambda *shape: torch.ones(*shape, device="cuda")
+    an, fn, on = ones(layers, hidden), ones(layers, hidden), ones(hidden)
+    qb, kb, vb = (torch.randn(layers, n, generator=g, device="cuda") * 0.1 for n in (hidden, kv, kv))
+    from tinymetalagent_amd import attention as A
+    cos_t, sin_t = A.rope_table(ctx, d, THETA)
+    kc = torch.randn(layers, ctx, kv, generator=g, device="cuda").half()
+    vc = torch.randn(layers, ctx, kv, generator=g, device="cuda").half()
+    x = torch.randn(hidden, generator=g, device="cuda")
+    out, tok = torch.empty_like(x), torch.empty(1, dtype=torch.int32, device="cuda")
+    pos = ctx - 1
+    wsp = LY.workspace(pos, hidden, kv, heads, kv_heads, d, ffn, vocab)
+
+    def step(s):
+        LY.decode_all_layers(mapping, offsets, layers, ggml_type, x, an, fn, qb, kb, vb, cos_t, sin_t, kc, vc, pos,
+                             ctx, heads, kv_heads, d, ffn, 1e-6, out=out, head=(head_off, ggml_type), output_norm=on,
+                             vocab=vocab, token_out=tok, ws=wsp, stream=s)
+    us = graph_time_us(torch, [step], reps)
+    wbytes = sum(n for _, n in regions)
+    kvbytes = layers * (pos + 1) * kv * 2 * 2
+    del mapping, kc, vc
+    torch.cuda.empty_cache()
+    return {"us_per_token": r(us, 1), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wbytes,
+            "kv_bytes": kvbytes, "gbs": round((wbytes + kvbytes) / us / 1e3, 1),
+            "frac": r((wbytes + kvbytes) / us / 1e3 / HBM_PEAK_GBS), "launches_per_token": 6 * layers + 2}
+
+
 def split_fields(p) -> dict:
     """The key-split entry point's figures of a prefill_case(split=True) result."""
     return dict(attention_us=r(p["split_ms"] * 1e3, 2), tflops=round(p["split_tflops"], 1),
@@ -629,6 +731,21 @@ def main():
                                                          frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
                                                          split_entry=split_fields(p))
         line["configs"] = cfgs
+        # the decode-layer slot around attention: quantized projections and the
+        # whole token through every layer (one GPU, batch 1, greedy head)
+        from tinymetalagent_amd import layers as LY
+        from tinymetalagent_amd import vecops as V
+        line["decode_layers"] = {
+            "workload": "Qwen2.5-3B decode token: 36 x (RMSNorm + QKV GEMV, fused decode step, Wo + residual, "
+                        "RMSNorm + gate/up GEMV, SwiGLU + down GEMV + residual), then RMSNorm + lm_head + argmax; "
+                        "ctx 8K, random GGUF weights",
+            "gemv_lm_head_q4_0": gemv_case(torch, V, 2, 151936, 2048),
+            "gemv_lm_head_q8_0": gemv_case(torch, V, 8, 151936, 2048),
+            "gemv_gate_q4_0": gemv_case(torch, V, 2, 11008, 2048),
+            "gemv_down_q4_0": gemv_case(torch, V, 2, 2048, 11008),
+            "token_q4_0": decode_layers_case(torch, LY, V, 2),
+            "token_q8_0": decode_layers_case(torch, LY, V, 8),
+        }
     if not args.no_cpu_baseline:
         ql, kl, vl = dec["cpu_sample"]
         cpu = cpu_baseline(ql, kl, vl, H, KV, D, args.ctx, LAYERS, args.cpu_seconds)
