@@ -77,6 +77,10 @@ def parse_args():
     p.add_argument("--profile", action="store_true",
                    help="run a fixed kernel sequence for rocprofv3 (5x decode step at 3B/8K/36 layers, "
                         "5x prefill at L=4096, 3x a 512 MiB device copy for counter calibration) and exit")
+    p.add_argument("--profile-layers", action="store_true",
+                   help="run a fixed decode-layer sequence for rocprofv3 (10x lm_head GEMV Q4_0 and Q8_0 over "
+                        "rotated weight copies, 5x a 3B decode token through 36 layers, 3x a 512 MiB device copy) "
+                        "and exit")
     return p.parse_args()
 
 
@@ -139,6 +143,37 @@ def profile_sequence(torch, A) -> None:
     print("profile sequence done: decode step (0.25 s of steps, then 5 more; 3B, L=8192, 36 layers, "
           "4 rotated KV sets), "
           "prefill (0.25 s, then 5 more; L=4096), copy x3 (536870912 B read + written)")
+
+
+def profile_layers_sequence(torch) -> None:
+    """Fixed decode-layer launch sequence profiled by the commands recorded under
+    profiles/: the lm_head GEMV (151936 x 2048) in Q4_0 and Q8_0, each after
+    0.25 s of settling, 10 launches over weight copies rotated past the MALL;
+    then 5 decode tokens through 36 layers at 3B / ctx 8K (Q4_0); then the
+    512 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE."""
+    from tinymetalagent_amd import layers as LY
+    from tinymetalagent_amd import vecops as V
+    for t in (2, 8):
+        rows, cols = 151936, 2048
+        nbytes = rows * V.row_bytes(t, cols)
+        ws = [random_ggml(torch, t, nbytes) for _ in range(max(2, math.ceil(1.2e9 / nbytes)))]
+        x = torch.randn(cols, device="cuda")
+        out = torch.empty(rows, device="cuda")
+        count = iter(range(1 << 30))
+        settle(torch, lambda: V.matvec(ws[next(count) % len(ws)], t, x, rows, out=out))
+        for i in range(10):
+            V.matvec(ws[i % len(ws)], t, x, rows, out=out)
+        torch.cuda.synchronize()
+        del ws
+        torch.cuda.empty_cache()
+    decode_layers_case(torch, LY, V, 2, reps=5)
+    src = torch.ones(128 << 20, dtype=torch.float32, device="cuda")  # 512 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("profile sequence done: lm_head GEMV Q4_0 / Q8_0 (0.25 s, then 10 each; rotated copies), "
+          "3B decode token x5 (graph), copy x3 (536870912 B read + written)")
 
 
 def gpu_warmup(torch, A, seconds: float) -> None:
@@ -617,6 +652,10 @@ def main():
     if args.profile:
         gpu_warmup(torch, A, args.warmup_seconds)
         profile_sequence(torch, A)
+        return
+    if args.profile_layers:
+        gpu_warmup(torch, A, args.warmup_seconds)
+        profile_layers_sequence(torch)
         return
     timer = Timer(torch)
     H, KV, D, LAYERS = 16, 2, 128, 36
