@@ -73,8 +73,9 @@ def test_defaults_and_capabilities():
     assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), runtime.TE_OP_CAUSAL_ATTENTION) == 1
     for op in (0, 4, 7, 8, 9):  # matvec, RMSNorm, SwiGLU, residual add, argmax
         assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), op) == 1
-    for op in (1, 3, 10, 12):  # matmul, decode token, sampling, tokenize: not in this build
-        assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), op) == 0
+    for op in (3, 10, 12):  # decode token, sampling, tokenize
+        assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), op) == 1
+    assert lib.te_kernel_plan_supports_op(ctypes.byref(plan), 1) == 0  # matmul: not in this build
     for quant, want in ((1, 1), (2, 1), (4, 1), (8, 1), (5, 0), (11, 0)):  # F32 F16 Q4_0 Q8_0 | Q4_1 Q4_K
         assert lib.te_kernel_plan_supports_quant(ctypes.byref(plan), quant) == want
     assert plan.max_context_tokens == 8192
@@ -191,15 +192,18 @@ def test_workspace_query(lib):
     assert lib.te_hip_attention_decode_workspace_bytes(pos, 0, 3, 2, 28, 4, 128) > 0
 
 
-def test_out_of_scope_entry_points_report_unsupported():
+def test_model_and_generate_argument_statuses():
+    """Missing file -> IO_ERROR (tinyengine.c:278-280), the "unsupported"
+    text the agent layer matches, NULL handles -> INVALID_ARGUMENT."""
     from tinymetalagent_amd import runtime
 
     lib = runtime.load_library()
     model = ctypes.c_void_p()
     status = lib.te_model_load_gguf(b"/nonexistent.gguf", None, ctypes.byref(model))
-    assert status == runtime.TE_STATUS_UNSUPPORTED and model.value is None
+    assert status == runtime.TE_STATUS_IO_ERROR and model.value is None
     with pytest.raises(runtime.TinyEngineError, match="^unsupported$"):
-        runtime.check(status)
+        runtime.check(runtime.TE_STATUS_UNSUPPORTED)
     assert lib.te_context_create(None, None, ctypes.byref(model)) == 1
     cb = runtime._TOKEN_CALLBACK(lambda *a: None)
     assert lib.te_generate(None, b"hi", 4, cb, None) == 1
+    assert lib.te_generate_raw(None, b"hi", 4, cb, None) == 1

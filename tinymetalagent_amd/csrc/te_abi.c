@@ -1,20 +1,15 @@
 /*
- * ABI plumbing of libtinyengine.so (reference c/src/tinyengine.c:13-440):
+ * ABI plumbing of libtinyengine.so (reference c/src/tinyengine.c:13-268):
  * version and status strings, option defaults, capability and kernel-plan
- * reports, context handling and the generate entry points.
+ * reports.
  *
  * The status strings are part of the contract (reference tinyengine.c:17-34):
  * the agent layer matches the exact text "unsupported"
  * (python/tinyagent/engine.py:46, :62).
  *
- * Entry points outside this build (GGUF model loading, tokenizer, the
- * model-level matvec, full generation) keep the reference's argument checks
- * and then return TE_STATUS_UNSUPPORTED, the reference's "path not available
- * here" status (qwen.c:1162-1165).  The element-wise ops (te_rmsnorm_f32,
- * te_swiglu_f32, te_add_f32, te_argmax_f32) run on the GPU in
- * te_hip_runtime.hip.  They exist so that an
- * unchanged ctypes binding resolves all of its symbols
- * (python/tinyengine/runtime.py:271-378).
+ * GGUF models, the tokenizer, contexts and generation are in te_model.hip;
+ * the element-wise ops (te_rmsnorm_f32, te_swiglu_f32, te_add_f32,
+ * te_argmax_f32) run on the GPU in te_hip_runtime.hip.
  */
 #include "tinyengine.h"
 #include "te_hip_backend.h"
@@ -25,11 +20,6 @@
 #include <unistd.h>
 
 static const char *const TE_VERSION_STRING = "0.1.0-c-abi-hip-gfx950";
-
-struct te_context {
-    te_model *model;
-    te_runtime_options options;
-};
 
 const char *te_version(void) {
     return TE_VERSION_STRING;
@@ -85,13 +75,14 @@ te_runtime_options te_default_options(void) {
     return options;
 }
 
-/* The operations this build implements on the GPU: the attention step and the
- * decode-layer vector operations around it (matvec, RMSNorm, SwiGLU, residual
- * add, argmax). */
+/* The operations this build implements: the attention step, the decode-layer
+ * vector operations around it (matvec, RMSNorm, SwiGLU, residual add, argmax),
+ * whole decode tokens, top-k sampling and the tokenizer. */
 static uint64_t te_hip_op_mask(void) {
     return (1ull << TE_OP_ROPE) | (1ull << TE_OP_CAUSAL_ATTENTION) | (1ull << TE_OP_KV_CACHE) |
            (1ull << TE_OP_BATCHED_PREFILL) | (1ull << TE_OP_MATVEC) | (1ull << TE_OP_RMSNORM) |
-           (1ull << TE_OP_SWIGLU) | (1ull << TE_OP_RESIDUAL_ADD) | (1ull << TE_OP_ARGMAX);
+           (1ull << TE_OP_SWIGLU) | (1ull << TE_OP_RESIDUAL_ADD) | (1ull << TE_OP_ARGMAX) |
+           (1ull << TE_OP_DECODE_TOKEN) | (1ull << TE_OP_SAMPLING) | (1ull << TE_OP_TOKENIZE);
 }
 
 /* Weight / cache formats: fp32 and fp16 data, GGUF Q4_0 and Q8_0 matvec. */
@@ -190,159 +181,4 @@ int te_kernel_plan_supports_op(const te_kernel_plan *plan, te_vector_op op) {
         return 0;
     }
     return (int)((plan->vector_op_mask >> (unsigned)op) & 1u);
-}
-
-/* ---- outside the attention step: argument checks, then UNSUPPORTED ---- */
-
-te_status te_model_load_gguf(const char *path, const te_runtime_options *options, te_model **out_model) {
-    (void)options;
-    if (path == NULL || out_model == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_model = NULL;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_get_info(const te_model *model, te_model_info *out_info) {
-    return (model == NULL || out_info == NULL) ? TE_STATUS_INVALID_ARGUMENT : TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_get_tokenizer_info(const te_model *model, te_tokenizer_info *out_info) {
-    return (model == NULL || out_info == NULL) ? TE_STATUS_INVALID_ARGUMENT : TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_get_tensor_info(const te_model *model, const char *name, te_tensor_info *out_info) {
-    return (model == NULL || name == NULL || out_info == NULL) ? TE_STATUS_INVALID_ARGUMENT
-                                                                : TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_format_qwen_chat_prompt(const char *prompt, char *out, size_t out_capacity, size_t *out_written) {
-    (void)out;
-    (void)out_capacity;
-    if (prompt == NULL || out_written == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_written = 0;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_tokenize(const te_model *model, const char *text, int parse_special, uint32_t *out_tokens,
-                            size_t out_capacity, size_t *out_written) {
-    (void)parse_special;
-    (void)out_tokens;
-    (void)out_capacity;
-    if (model == NULL || text == NULL || out_written == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_written = 0;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_detokenize(const te_model *model, const uint32_t *tokens, size_t token_count,
-                              int skip_special, char *out, size_t out_capacity, size_t *out_written) {
-    (void)skip_special;
-    (void)out;
-    (void)out_capacity;
-    if (model == NULL || (tokens == NULL && token_count != 0u) || out_written == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_written = 0;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_read_f32_tensor(const te_model *model, const char *name, float *out, size_t out_capacity,
-                                   size_t *out_written) {
-    (void)out;
-    (void)out_capacity;
-    if (model == NULL || name == NULL || out_written == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_written = 0;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_dequantize_row_f32(const te_model *model, const char *name, uint64_t row_index, float *out,
-                                      size_t out_capacity, size_t *out_written) {
-    (void)row_index;
-    (void)out;
-    (void)out_capacity;
-    if (model == NULL || name == NULL || out_written == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_written = 0;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-te_status te_model_matvec_f32(const te_model *model, const char *name, const float *input, size_t input_len,
-                              float *out, size_t out_capacity, size_t *out_written) {
-    (void)input_len;
-    (void)out;
-    (void)out_capacity;
-    if (model == NULL || name == NULL || input == NULL || out_written == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    *out_written = 0;
-    return TE_STATUS_UNSUPPORTED;
-}
-
-void te_model_free(te_model *model) {
-    (void)model; /* no model can be created by this build */
-}
-
-/* ---- context and generation: reference tinyengine.c:374-440 ---- */
-
-te_status te_context_create(te_model *model, const te_runtime_options *options, te_context **out_context) {
-    if (model == NULL || out_context == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    te_context *context = (te_context *)calloc(1, sizeof(*context));
-    if (context == NULL) {
-        return TE_STATUS_OUT_OF_MEMORY;
-    }
-    context->model = model;
-    context->options = options != NULL ? *options : te_default_options();
-    *out_context = context;
-    return TE_STATUS_OK;
-}
-
-void te_context_free(te_context *context) {
-    free(context);
-}
-
-/* Stub generation mode kept from the reference (tinyengine.c:410-423): with
- * TINYENGINE_GENERATION=stub the fixed four-piece reply is streamed. */
-te_status te_generate(te_context *context, const char *prompt, uint32_t max_tokens, te_token_callback callback,
-                      void *userdata) {
-    if (context == NULL || prompt == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    if (max_tokens == 0u) {
-        return TE_STATUS_OK;
-    }
-    const char *mode = getenv("TINYENGINE_GENERATION");
-    if (mode == NULL || strcmp(mode, "stub") != 0) {
-        return TE_STATUS_UNSUPPORTED;
-    }
-    static const char *const pieces[] = {"Mi", " ch", "iamo", " Alex"};
-    static const uint32_t ids[] = {41887u, 521u, 34214u, 8515u};
-    const uint32_t count = max_tokens < 4u ? max_tokens : 4u;
-    for (uint32_t i = 0; i < count; ++i) {
-        if (callback != NULL) {
-            callback(pieces[i], ids[i], userdata);
-        }
-    }
-    return TE_STATUS_OK;
-}
-
-te_status te_generate_raw(te_context *context, const char *prompt, uint32_t max_tokens, te_token_callback callback,
-                          void *userdata) {
-    (void)callback;
-    (void)userdata;
-    if (context == NULL || prompt == NULL) {
-        return TE_STATUS_INVALID_ARGUMENT;
-    }
-    if (max_tokens == 0u) {
-        return TE_STATUS_OK;
-    }
-    return TE_STATUS_UNSUPPORTED;
 }

@@ -92,6 +92,10 @@ te_status launch_rmsnorm(const float *input, const float *weight, size_t rows, s
 te_status launch_swiglu(const float *gate, const float *up, size_t len, float *out, hipStream_t stream);
 te_status launch_add(const float *lhs, const float *rhs, size_t len, float *out, hipStream_t stream);
 te_status launch_argmax(const float *values, size_t len, uint32_t *out_index, hipStream_t stream);
+// Row `row` of a [rows][cols] F32 / Q4_0 / Q8_0 tensor as fp32 (Q4_0 / Q8_0: cols % 32 == 0);
+// the tensor may start at any byte address.
+te_status launch_dequant_row(const void *weights, uint32_t ggml_type, size_t cols, size_t row, float *out,
+                             hipStream_t stream);
 
 // One weight matrix of a fused GEMV launch: out[r] = W[r] . x' (+ resid[r] when
 // resid is set; resid may equal out), r < rows.

@@ -818,6 +818,33 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *values, uint3
     }
 }
 
+// Row `row` of a [rows][cols] GGUF tensor as fp32 (te_model_dequantize_row_f32,
+// ops.c:127-175; block formats ops.c:15-21): Q4_0 (code - 8) * d with low
+// nibbles first, Q8_0 code * d, F32 as stored.  One thread per value.
+__global__ __launch_bounds__(256) void dequant_row_kernel(const unsigned char *weights, uint32_t ggml_type,
+                                                          int cols, size_t row_bytes, size_t row, float *out) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) {
+        return;
+    }
+    const unsigned char *r = weights + row * row_bytes;
+    float v;
+    if (ggml_type == kGgmlF32) {
+        __builtin_memcpy(&v, r + (size_t)c * 4, 4);  // any byte alignment
+    } else if (ggml_type == kGgmlQ4_0) {
+        const unsigned char *b = r + (size_t)(c / 32) * 18;
+        const int j = c % 32;
+        const float d = f16_bits_to_f32((uint32_t)b[0] | (uint32_t)b[1] << 8);
+        const int q = j < 16 ? (b[2 + j] & 15) : (b[2 + j - 16] >> 4);
+        v = (float)(q - 8) * d;
+    } else {
+        const unsigned char *b = r + (size_t)(c / 32) * 34;
+        const float d = f16_bits_to_f32((uint32_t)b[0] | (uint32_t)b[1] << 8);
+        v = (float)(signed char)b[2 + c % 32] * d;
+    }
+    out[c] = v;
+}
+
 }  // namespace
 
 namespace te_hip {
@@ -1086,6 +1113,14 @@ te_status launch_gemv(uint32_t ggml_type, GemvPre pre, const GemvSeg *segs, int 
         }
     }
     return st;
+}
+
+te_status launch_dequant_row(const void *weights, uint32_t ggml_type, size_t cols, size_t row, float *out,
+                             hipStream_t stream) {
+    const size_t row_bytes = ggml_type == kGgmlF32 ? cols * 4 : ggml_row_bytes(ggml_type, cols);
+    dequant_row_kernel<<<dim3((unsigned)((cols + 255) / 256)), 256, 0, stream>>>(
+        static_cast<const unsigned char *>(weights), ggml_type, (int)cols, row_bytes, row, out);
+    return launch_status();
 }
 
 te_status launch_rmsnorm(const float *input, const float *weight, size_t rows, size_t len, float epsilon, float *out,

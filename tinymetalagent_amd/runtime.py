@@ -164,6 +164,17 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_generate", [_vp, ctypes.c_char_p, ctypes.c_uint32, _TOKEN_CALLBACK, _vp])
     _sig(lib, "te_generate_raw", [_vp, ctypes.c_char_p, ctypes.c_uint32, _TOKEN_CALLBACK, _vp])
     _sig(lib, "te_default_options", [], _RuntimeOptions)
+    _sig(lib, "te_model_get_info", [_vp, _vp])
+    _sig(lib, "te_model_get_tokenizer_info", [_vp, _vp])
+    _sig(lib, "te_model_get_tensor_info", [_vp, ctypes.c_char_p, _vp])
+    _sig(lib, "te_format_qwen_chat_prompt", [ctypes.c_char_p, ctypes.c_char_p, _sz, _szp])
+    _sig(lib, "te_model_tokenize", [_vp, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_uint32), _sz, _szp])
+    _sig(lib, "te_model_detokenize",
+         [_vp, ctypes.POINTER(ctypes.c_uint32), _sz, _int, ctypes.c_char_p, _sz, _szp])
+    _sig(lib, "te_model_read_f32_tensor", [_vp, ctypes.c_char_p, _f32p, _sz, _szp])
+    _sig(lib, "te_model_dequantize_row_f32", [_vp, ctypes.c_char_p, ctypes.c_uint64, _f32p, _sz, _szp])
+    _sig(lib, "te_model_matvec_f32", [_vp, ctypes.c_char_p, _f32p, _sz, _f32p, _sz, _szp])
+    _sig(lib, "te_model_free", [_vp], None)
     # Attention step, public (include/tinyengine.h).
     _sig(lib, "te_rope_f32", [_f32p, _sz, _sz, _sz, ctypes.c_float])
     _sig(lib, "te_attention_decode_f32", [_f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _f32p])
