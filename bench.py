@@ -81,6 +81,9 @@ def parse_args():
                    help="run a fixed decode-layer sequence for rocprofv3 (10x lm_head GEMV Q4_0 and Q8_0 over "
                         "rotated weight copies, 5x a 3B decode token through 36 layers, 3x a 512 MiB device copy) "
                         "and exit")
+    p.add_argument("--generate", action="store_true",
+                   help="only the end-to-end te_generate_raw case on a 3B-shaped GGUF (Q4_0 and Q8_0); print its "
+                        "JSON and exit")
     return p.parse_args()
 
 
@@ -610,6 +613,126 @@ def decode_layers_case(torch, LY, V, ggml_type: int, *, layers=36, heads=16, kv_
             "frac": r((wbytes + kvbytes) / us / 1e3 / HBM_PEAK_GBS), "launches_per_token": 6 * layers + 2}
 
 
+def write_3b_gguf(path: str, ggml_type: int, *, layers=36, heads=16, kv_heads=2, d=128, ffn=11008,
+                  vocab=151936) -> int:
+    """A Qwen2.5-3B-shaped GGUF with random weights (block scales 2^-7, random
+    codes), unit norms, small biases and a byte-level vocabulary of `vocab`
+    tokens (256 byte symbols, filler tokens, the chat specials), written in
+    streaming fashion.  Returns the file size."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import numpy as np
+    import _gguf as G
+    hidden, kv = heads * d, kv_heads * d
+    bb = {2: 18, 8: 34}[ggml_type]
+    syms = G.gpt2_byte_symbols()
+    tokens = syms + [f"tok{i}" for i in range(vocab - 256 - 3)] + G.SPECIALS
+    w = G.GGUFWriter(3, 32)
+    w.kv("general.architecture", G.STR, "qwen2").kv("general.name", G.STR, "synthetic-qwen2.5-3b")
+    for k, v in (("context_length", 32768), ("embedding_length", hidden), ("block_count", layers),
+                 ("feed_forward_length", ffn), ("attention.head_count", heads),
+                 ("attention.head_count_kv", kv_heads)):
+        w.kv(f"qwen2.{k}", G.U32, v)
+    w.kv("qwen2.attention.layer_norm_rms_epsilon", G.F32, 1e-6).kv("qwen2.rope.freq_base", G.F32, THETA)
+    w.kv("tokenizer.ggml.model", G.STR, "gpt2").kv("tokenizer.ggml.pre", G.STR, "qwen2")
+    w.kv("tokenizer.ggml.tokens", G.ARR, (G.STR, tokens))
+    w.kv("tokenizer.ggml.token_type", G.ARR, (G.I32, [1] * (vocab - 3) + [3] * 3))
+    w.kv("tokenizer.ggml.merges", G.ARR, (G.STR, []))
+    w.kv("tokenizer.ggml.eos_token_id", G.U32, vocab - 1).kv("tokenizer.ggml.padding_token_id", G.U32, vocab - 3)
+    plan = []  # (name, dims, type, kind, nbytes)
+    mats = [("attn_q", hidden, hidden), ("attn_k", kv, hidden), ("attn_v", kv, hidden), ("attn_output", hidden, hidden),
+            ("ffn_gate", ffn, hidden), ("ffn_up", ffn, hidden), ("ffn_down", hidden, ffn)]
+    for l in range(layers):
+        for n, rows, cols in mats:
+            plan.append((f"blk.{l}.{n}.weight", (cols, rows), ggml_type, "q", rows * cols // 32 * bb))
+        for n, size, kind in (("attn_norm.weight", hidden, "one"), ("ffn_norm.weight", hidden, "one"),
+                              ("attn_q.bias", hidden, "small"), ("attn_k.bias", kv, "small"),
+                              ("attn_v.bias", kv, "small")):
+            plan.append((f"blk.{l}.{n}", (size,), 0, kind, size * 4))
+    plan.append(("output_norm.weight", (hidden,), 0, "one", hidden * 4))
+    plan.append(("token_embd.weight", (hidden, vocab), ggml_type, "q", vocab * hidden // 32 * bb))
+    plan.append(("output.weight", (hidden, vocab), ggml_type, "q", vocab * hidden // 32 * bb))
+    off = 0
+    for name, dims, t, _, nb in plan:
+        w.tensor(name, dims, t, b"", offset=off)
+        off = (off + nb + 31) // 32 * 32
+    head = w.header()
+    rng = np.random.default_rng(7)
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * ((-len(head)) % 32))
+        for name, dims, t, kind, nb in plan:
+            if kind == "q":
+                blk = rng.integers(0, 256, size=(nb // bb, bb), dtype=np.uint8)
+                blk[:, 0], blk[:, 1] = 0, 0x20
+                data = blk.tobytes()
+            elif kind == "one":
+                data = np.ones(nb // 4, np.float32).tobytes()
+            else:
+                data = (rng.standard_normal(nb // 4) * 0.1).astype(np.float32).tobytes()
+            f.write(data + b"\0" * ((-nb) % 32))
+    return os.path.getsize(path)
+
+
+def generate_case(ggml_type: int, prompt_tokens: int = 512, new_tokens: int = 128, ctx: int = 1024) -> dict:
+    """End-to-end te_generate_raw on a 3B-shaped GGUF through the public C ABI
+    (the reference's own entry point, qwen.c:261-400): load, a prompt of
+    `prompt_tokens` byte tokens processed token by token, then greedy decode
+    with every token streamed to the callback.  Times: load (parse + upload of
+    the file to HBM on first use), prompt (to the first generated token) and
+    decode (tokens after the first, per second)."""
+    import ctypes
+    import tempfile
+    from tinymetalagent_amd import runtime as R
+    from tinymetalagent_amd.model import Model, RuntimeOptions
+    tmp = os.environ.get("TMPDIR", tempfile.gettempdir())
+    path = os.path.join(tmp, f"te_bench_3b_{ggml_type}.gguf")
+    t0 = time.perf_counter()
+    size = write_3b_gguf(path, ggml_type)
+    write_s = time.perf_counter() - t0
+    os.environ["TINYENGINE_TEMPERATURE"] = "0"
+    os.environ["TINYENGINE_IGNORE_EOS"] = "1"
+    out = {"file_bytes": size, "write_s": r(write_s, 2), "prompt_tokens": prompt_tokens, "new_tokens": new_tokens,
+           "context_tokens": ctx}
+    try:
+        m = Model(path, RuntimeOptions(context_tokens=ctx))
+        lib = R.load_library()
+        for rep in range(2):  # the first run also uploads the file and builds the context state
+            stamps = []
+            cb = R._TOKEN_CALLBACK(lambda s, i, u: stamps.append(time.perf_counter()))
+            hctx = ctypes.c_void_p()
+            opts = RuntimeOptions(context_tokens=ctx)._to_c()
+            R.check(lib.te_context_create(m.handle, ctypes.byref(opts), ctypes.byref(hctx)))
+            t0 = time.perf_counter()
+            R.check(lib.te_generate_raw(hctx, b"a" * prompt_tokens, new_tokens, cb, None))
+            lib.te_context_free(hctx)
+            assert len(stamps) == new_tokens
+            key = "first_run" if rep == 0 else "steady"
+            out[key] = {"to_first_token_ms": r((stamps[0] - t0) * 1e3, 2),
+                        "prompt_tokens_per_s": round(prompt_tokens / (stamps[0] - t0), 1),
+                        "decode_tokens_per_s": round((new_tokens - 1) / (stamps[-1] - stamps[0]), 1),
+                        "decode_ms_per_token": r((stamps[-1] - stamps[0]) * 1e3 / (new_tokens - 1), 3)}
+        # a second turn on the same context: the first turn's prompt plus 64
+        # new tokens, with the cache reused (default) and recomputed
+        for mode in ("1", "0"):
+            os.environ["TINYENGINE_KV_REUSE"] = mode
+            stamps = []
+            cb = R._TOKEN_CALLBACK(lambda s, i, u: stamps.append(time.perf_counter()))
+            hctx = ctypes.c_void_p()
+            opts = RuntimeOptions(context_tokens=ctx)._to_c()
+            R.check(lib.te_context_create(m.handle, ctypes.byref(opts), ctypes.byref(hctx)))
+            R.check(lib.te_generate_raw(hctx, b"a" * prompt_tokens, 8, cb, None))
+            stamps.clear()
+            t0 = time.perf_counter()
+            R.check(lib.te_generate_raw(hctx, b"a" * prompt_tokens + b"b" * 64, 8, cb, None))
+            lib.te_context_free(hctx)
+            key = "second_turn_kv_reuse" if mode == "1" else "second_turn_recomputed"
+            out[key] = {"prompt_tokens": prompt_tokens + 64, "to_first_token_ms": r((stamps[0] - t0) * 1e3, 2)}
+        os.environ.pop("TINYENGINE_KV_REUSE", None)
+        m.close()
+    finally:
+        os.remove(path)
+    return out
+
+
 def split_fields(p) -> dict:
     """The key-split entry point's figures of a prefill_case(split=True) result."""
     return dict(attention_us=r(p["split_ms"] * 1e3, 2), tflops=round(p["split_tflops"], 1),
@@ -656,6 +779,9 @@ def main():
     if args.profile_layers:
         gpu_warmup(torch, A, args.warmup_seconds)
         profile_layers_sequence(torch)
+        return
+    if args.generate:
+        print(json.dumps({"generate": {"q4_0": generate_case(2), "q8_0": generate_case(8)}}))
         return
     timer = Timer(torch)
     H, KV, D, LAYERS = 16, 2, 128, 36
@@ -784,6 +910,12 @@ def main():
             "gemv_down_q4_0": gemv_case(torch, V, 2, 2048, 11008),
             "token_q4_0": decode_layers_case(torch, LY, V, 2),
             "token_q8_0": decode_layers_case(torch, LY, V, 8),
+        }
+        # generation through the public C ABI on a 3B-shaped GGUF
+        line["generate"] = {
+            "workload": "te_generate_raw on a Qwen2.5-3B-shaped GGUF (random weights, 151936-token byte-level "
+                        "vocabulary): 512 prompt tokens token by token, then 128 greedy tokens; ctx 1024",
+            "q4_0": generate_case(2),
         }
     if not args.no_cpu_baseline:
         ql, kl, vl = dec["cpu_sample"]

@@ -217,3 +217,30 @@ def test_generate_stops_at_eos(q4_model, monkeypatch):
                                env={"TINYENGINE_TEMPERATURE": "1.5", "TINYENGINE_SEED": seed,
                                     "TINYENGINE_TOP_K": "400"})
         assert q["vocab"] - 1 not in got and q["vocab"] - 3 not in got
+
+
+def test_session_kv_reuse_matches_fresh_context(q4_model, monkeypatch):
+    """A second call on the same context reuses the K / V of the tokens it
+    shares with the first call's sequence; its tokens equal a fresh context's
+    and those of the same context with reuse off (TINYENGINE_KV_REUSE=0)."""
+    q = q4_model
+    monkeypatch.setenv("TINYENGINE_TEMPERATURE", "0")
+    monkeypatch.setenv("TINYENGINE_IGNORE_EOS", "1")
+    turn1 = "<|im_start|>user\nhello world<|im_end|>\n<|im_start|>assistant\n"
+    with Model(q["path"], RuntimeOptions(context_tokens=256)) as m:
+        runs = {}
+        for mode in ("reuse", "off"):
+            monkeypatch.setenv("TINYENGINE_KV_REUSE", "1" if mode == "reuse" else "0")
+            with m.session() as s:
+                ids1 = []
+                reply = s.generate_raw(turn1, 16, on_token=lambda t, i: ids1.append(i))
+                turn2 = turn1 + reply + "<|im_end|>\n<|im_start|>user\nthe engine<|im_end|>\n"
+                ids2 = []
+                s.generate_raw(turn2, 16, on_token=lambda t, i: ids2.append(i))
+                ids3 = []
+                s.generate_raw(turn1, 16, on_token=lambda t, i: ids3.append(i))  # a shorter prompt again
+            runs[mode] = (ids1, ids2, ids3)
+        fresh = []
+        m.generate_raw(turn2, 16, on_token=lambda t, i: fresh.append(i))
+    assert runs["reuse"] == runs["off"]
+    assert runs["reuse"][1] == fresh and runs["reuse"][2] == runs["reuse"][0]

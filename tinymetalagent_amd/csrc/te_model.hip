@@ -1140,6 +1140,8 @@ struct te_context {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     std::vector<void *> allocations;
+    // the tokens whose K / V fill cache positions 0 .. history.size() - 1
+    std::vector<uint32_t> history;
 };
 
 namespace {
@@ -1149,6 +1151,7 @@ void release_state(te_context *c) {
         (void)hipFree(p);
     }
     c->allocations.clear();
+    c->history.clear();
     c->ready = false;
 }
 
@@ -1492,13 +1495,30 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
     }
     Sampler sm;
     const bool greedy = sm.temperature <= 0.0f;
-    for (size_t i = 0; i < ids.size(); ++i) {
+    // Cache reuse across calls on one context: the positions whose tokens
+    // equal the previous call's (prompt and forwarded generated tokens) keep
+    // their K / V.  Their values are what recomputing them would write (the
+    // same tokens at the same positions through the same kernels), so the
+    // result is the same as a fresh context's.  The last prompt token is
+    // always run, for its logits.  TINYENGINE_KV_REUSE=0 turns reuse off.
+    size_t start = 0;
+    const char *reuse = getenv("TINYENGINE_KV_REUSE");
+    if (reuse == nullptr || strcmp(reuse, "0") != 0) {
+        while (start + 1 < ids.size() && start < c->history.size() && c->history[start] == ids[start]) {
+            ++start;
+        }
+    }
+    c->history.resize(start);
+    for (size_t i = start; i < ids.size(); ++i) {
         if ((s = forward(c, ids[i], i, greedy && i + 1 == ids.size())) != TE_STATUS_OK) {
+            c->history.clear();
             return s;
         }
+        c->history.push_back(ids[i]);
     }
     uint32_t next = 0;
     if ((s = next_token(c, sm, next)) != TE_STATUS_OK) {
+        c->history.clear();
         return s;
     }
     size_t position = ids.size();
@@ -1512,7 +1532,12 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         if (g + 1 == max_tokens) {
             break;
         }
-        if ((s = forward(c, next, position, greedy)) != TE_STATUS_OK || (s = next_token(c, sm, next)) != TE_STATUS_OK) {
+        if ((s = forward(c, next, position, greedy)) != TE_STATUS_OK) {
+            c->history.clear();
+            return s;
+        }
+        c->history.push_back(next);
+        if ((s = next_token(c, sm, next)) != TE_STATUS_OK) {
             return s;
         }
         ++position;

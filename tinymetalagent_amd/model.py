@@ -295,12 +295,62 @@ class Model:
             self._lib.te_context_free(context)
         return "".join(chunks)
 
+    def session(self) -> "Session":
+        """A context kept across calls: each call reuses the K / V of the
+        leading tokens it shares with the previous call's sequence."""
+        return Session(self)
+
     def close(self) -> None:
         if getattr(self, "_model", None):
             self._lib.te_model_free(self._model)
             self._model = None
 
     def __enter__(self) -> "Model":
+        return self
+
+    def __exit__(self, *_exc) -> None:
+        self.close()
+
+    def __del__(self) -> None:
+        self.close()
+
+
+class Session:
+    """One te_context over a Model, kept open between generate calls (this
+    build's addition: the reference binding makes a context per call)."""
+
+    def __init__(self, model: Model):
+        self._model = model
+        self._lib = model._lib
+        raw = model._options._to_c()
+        self._ctx = ctypes.c_void_p()
+        check(self._lib.te_context_create(model.handle, ctypes.byref(raw), ctypes.byref(self._ctx)))
+
+    def _run(self, fn, prompt: str, max_tokens: int, on_token) -> str:
+        chunks: list[str] = []
+
+        def callback(text: bytes, token_id: int, _userdata) -> None:
+            chunk = text.decode(errors="replace")
+            chunks.append(chunk)
+            if on_token is not None:
+                on_token(chunk, token_id)
+
+        c_callback = _TOKEN_CALLBACK(callback)
+        check(fn(self._ctx, prompt.encode(), max_tokens, c_callback, None))
+        return "".join(chunks)
+
+    def generate(self, prompt: str, max_tokens: int = 16, on_token=None) -> str:
+        return self._run(self._lib.te_generate, prompt, max_tokens, on_token)
+
+    def generate_raw(self, prompt: str, max_tokens: int = 256, on_token=None) -> str:
+        return self._run(self._lib.te_generate_raw, prompt, max_tokens, on_token)
+
+    def close(self) -> None:
+        if getattr(self, "_ctx", None):
+            self._lib.te_context_free(self._ctx)
+            self._ctx = None
+
+    def __enter__(self) -> "Session":
         return self
 
     def __exit__(self, *_exc) -> None:
