@@ -293,6 +293,29 @@ TE_API te_status te_hip_add_f32(const float *lhs, const float *rhs, size_t len, 
 TE_API te_status te_hip_argmax_f32(const float *values, size_t len, uint32_t *out_index, void *stream);
 
 /*
+ * Quantized GEMM of batched prompt prefill: out[m][n] = sum_k pre(x)[m][k] *
+ * W[n][k] (+ resid[m][n]) for `rows` activation rows at once -- the per-row
+ * meaning of te_model_matvec_f32 (ops.c:177-269) for the projections of
+ * te_qwen_prefill_prompt_batch (qwen.c:630-905), whose Metal matmuls it
+ * replaces.  pre: 0 none, 1 RMSNorm (norm_w, epsilon, as te_rmsnorm_f32),
+ * 2 SwiGLU (x is gate, x2 is up, as te_swiglu_f32).  W is a GGUF Q4_0 (2) or
+ * Q8_0 (8) tensor [n][k] in device memory at a 2-byte aligned address,
+ * k % 32 == 0.  The activations are rounded per 32-value block to 15 bits of
+ * the block's largest magnitude (error <= 2^-14 of it per value); products
+ * are exact int8 MFMA sums, accumulated per block in fp32.  `act` is device
+ * scratch of te_hip_gemm_act_bytes(rows, k) bytes.  `partials` (may be NULL)
+ * is device scratch of partial_bytes bytes: with it, an output grid too small
+ * to fill the GPU splits K into up to partial_bytes / (rows * n * 4) parts,
+ * summed afterwards in a fixed order.  Device pointers, asynchronous on
+ * `stream`; UNSUPPORTED for other types or shapes.
+ */
+TE_API size_t te_hip_gemm_act_bytes(size_t rows, size_t k);
+TE_API te_status te_hip_gemm_q_f32(const void *weights, uint32_t ggml_type, const float *x, const float *x2,
+                                   const float *norm_w, float epsilon, int pre, size_t rows, size_t n, size_t k,
+                                   float *out, const float *resid, void *act, float *partials,
+                                   size_t partial_bytes, void *stream);
+
+/*
  * One decode token through every layer (and, with out_token_id, the final
  * norm, lm_head and argmax): replaces te_metal_decode_all_layers_f32
  * (metal_backend.h:239-276, called by te_qwen_decode_all_layers_exact,

@@ -1,0 +1,353 @@
+// Quantized GEMM for batched prompt prefill: Y[m][n] = sum_k X[m][k] * W[n][k]
+// (+ R[m][n]) for M prompt rows at once against a GGUF Q4_0 / Q8_0 weight
+// matrix W [N][K] -- the projections of te_qwen_prefill_prompt_batch
+// (reference c/src/qwen.c:630-905), whose per-row meaning is te_model_matvec_f32
+// (ops.c:177-269) applied to every row.
+//
+// Activations (quant_act_kernel): each row, after an optional RMSNorm or
+// SwiGLU pre-op, is cut into 32-value blocks.  A block of largest magnitude
+// m = f * 2^E (f in [0.5, 1)) is scaled by 2^(14-E) and rounded to integers v,
+// |v| <= 2^14, stored as two balanced int8 digits v = 256*hi + lo
+// (lo in [-128, 127]) plus the block scale 2^(E-14).  Rounding moves each value
+// by at most 2^-14 of its block's largest magnitude.
+//
+// Products (gemm_q_kernel): one 32-value block of a row against one GGUF
+// block of a weight row is a K = 32 step of v_mfma_i32_32x32x32_i8 -- the
+// integer sum of hi * q, shifted by 8, then the lo * q sum accumulated onto it
+// by a second MFMA: exact, |C| <= 32 * 2^14 * 128 < 2^31.  Each block's integer
+// result is scaled by (activation scale * weight block scale) and accumulated
+// in fp32.  Weight codes enter the MFMA as int8: Q8_0 as stored, Q4_0 nibbles
+// n as n - 8 (the reference's (q - 8) * d, ops.c:15-21).
+//
+// Layout: the digit planes are stored in 32 x 32 tiles ([M/32][K/32][32 rows]
+// [32 k] int8), so one wave's operand for one block is 1 KiB contiguous.
+//
+// Tiles: a 256-thread workgroup computes a 64 x 64 block of Y as four 32 x 32
+// wave tiles; the K loop prefetches the next block's operands into registers
+// and stages the activation scales of the workgroup's 64 rows in LDS, 8
+// blocks at a time.  Where the output tiles alone would not fill the GPU,
+// the K range is split over grid.z and a second kernel adds the partial sums
+// in a fixed order (deterministic).
+#include "te_hip_common.h"
+
+#include <algorithm>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kQ4_0 = 2, kQ8_0 = 8;
+constexpr int kActThreads = 256;
+constexpr int kChunkBlocks = 8;
+
+__device__ __forceinline__ float half_bits(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+enum ActPre { kActPlain = 0, kActRmsNorm = 1, kActSwiGLU = 2 };
+
+// One workgroup per row: x' = pre(x), then digits and block scales.
+// planes: hi and lo, int8 in 32 x 32 tiles [M/32][K/32][32][32]; scales [M][K/32] fp32.
+template <int PRE>
+__global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__restrict__ x,
+                                                                const float *__restrict__ x2,
+                                                                const float *__restrict__ norm_w, float eps,
+                                                                int K, int8_t *__restrict__ hi,
+                                                                int8_t *__restrict__ lo,
+                                                                float *__restrict__ scales) {
+    const size_t row = blockIdx.x;
+    const float *xr = x + row * (size_t)K;
+    float rms = 1.0f;
+    if (PRE == kActRmsNorm) {
+        // te_rmsnorm_f32 (ops.c:272-293): fp64 sum of squares, 1 / sqrtf(mean + eps)
+        __shared__ double part[kActThreads / 64];
+        double ss = 0.0;
+        for (int i = threadIdx.x; i < K; i += kActThreads) {
+            const double v = (double)xr[i];
+            ss += v * v;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            ss += __shfl_xor(ss, off);
+        }
+        if ((threadIdx.x & 63) == 0) {
+            part[threadIdx.x >> 6] = ss;
+        }
+        __syncthreads();
+        double t = 0.0;
+        for (int w = 0; w < kActThreads / 64; ++w) {
+            t += part[w];
+        }
+        rms = 1.0f / sqrtf((float)(t / (double)K) + eps);
+    }
+    // one 32-value block per half wave: lane j of the half takes value j
+    const int lane = threadIdx.x & 31;
+    const int halves = kActThreads / 32;
+    for (int b = threadIdx.x >> 5; b < K / 32; b += halves) {
+        const int i = b * 32 + lane;
+        float v = xr[i];
+        if (PRE == kActRmsNorm) {
+            v = v * rms * norm_w[i];
+        } else if (PRE == kActSwiGLU) {
+            const float u = x2[row * (size_t)K + i];
+            v = v / (1.0f + expf(-v)) * u;  // te_swiglu_f32 (ops.c:397-405)
+        }
+        float m = fabsf(v);
+        for (int off = 16; off > 0; off >>= 1) {
+            m = fmaxf(m, __shfl_xor(m, off, 32));
+        }
+        int q = 0;
+        float s;
+        if (!(m <= 3.0e38f)) {  // inf or NaN in the block: its products are NaN
+            s = __builtin_nanf("");
+        } else if (m == 0.0f) {
+            s = 0.0f;
+        } else {
+            int E;
+            (void)frexpf(m, &E);
+            const int e = min(14 - E, 126);  // blocks below 2^-112 round towards 0
+            q = (int)rintf(ldexpf(v, e));
+            s = ldexpf(1.0f, -e);
+        }
+        const int l8 = ((q + 128) & 255) - 128;
+        const size_t t = (((row >> 5) * (size_t)(K >> 5) + b) << 10) + ((row & 31) << 5) + lane;
+        hi[t] = (int8_t)((q - l8) >> 8);
+        lo[t] = (int8_t)l8;
+        if (lane == 0) {
+            scales[row * (size_t)(K / 32) + b] = s;
+        }
+    }
+}
+
+// 16 weight codes of one GGUF block as int8: for Q4_0 the low (k < 16) or
+// high (k >= 16) nibbles of the 16 code bytes, n - 8; for Q8_0 the bytes
+// 16 * half .. +15.  `blk` is 2-byte aligned.
+template <uint32_t TYPE>
+__device__ __forceinline__ v4i weight_codes(const unsigned char *blk, int half, float &d) {
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(blk);
+    d = half_bits(h[0]);
+    uint32_t w[4];
+    const int base = TYPE == kQ4_0 ? 1 : 1 + 8 * half;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        w[k] = (uint32_t)h[base + 2 * k] | (uint32_t)h[base + 2 * k + 1] << 16;
+    }
+    v4i out;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (TYPE == kQ4_0) {
+            // n ^ 8 is n - 8 as a 4-bit two's complement value; sign-extend per byte
+            const uint32_t x = ((half ? w[k] >> 4 : w[k]) & 0x0f0f0f0fu) ^ 0x08080808u;
+            out[k] = (int)(x | ((x & 0x08080808u) * 0x1eu));
+        } else {
+            out[k] = (int)w[k];
+        }
+    }
+    return out;
+}
+
+// grid (N/64, M/64, splits): split z covers blocks [z * per, (z + 1) * per).
+// With one split the result (+ resid) goes to `out`; otherwise the split's
+// partial sums go to part[z][M][N].
+template <uint32_t TYPE, bool RESID>
+__global__ __launch_bounds__(256) void gemm_q_kernel(const unsigned char *__restrict__ w, size_t row_bytes,
+                                                     const int8_t *__restrict__ hi, const int8_t *__restrict__ lo,
+                                                     const float *__restrict__ scales, int M, int N, int K, int per,
+                                                     float *out, const float *resid, float *part) {
+    constexpr int kBlockBytes = TYPE == kQ4_0 ? 18 : 34;
+    __shared__ __align__(16) float s_lds[kChunkBlocks][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lr = lane & 31, kh = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m_wg = blockIdx.y * 64;
+    const int m0 = m_wg + wm * 32, n0 = blockIdx.x * 64 + wn * 32;
+    const int b_col = min(n0 + lr, N - 1);
+    const int nb = K / 32;
+    const int kb0 = blockIdx.z * per, kb1 = min(nb, kb0 + per);
+    // rows of a partial 32-row tile read padding; their results are not stored
+    const size_t a_tile = (size_t)(min(m0, (M - 1) & ~31) >> 5) * nb;
+    const int a_lane = lr * 32 + kh * 16;
+    const unsigned char *b_row = w + (size_t)b_col * row_bytes;
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc[r] = 0.0f;
+    }
+    auto load = [&](int b, v4i &ah, v4i &al, v4i &bq, float &d) {
+        const size_t o = ((a_tile + b) << 10) + a_lane;
+        ah = *reinterpret_cast<const v4i *>(hi + o);
+        al = *reinterpret_cast<const v4i *>(lo + o);
+        bq = weight_codes<TYPE>(b_row + (size_t)b * kBlockBytes, kh, d);
+    };
+    v4i ah, al, bq;
+    float d = 0.0f;
+    if (kb0 < kb1) {
+        load(kb0, ah, al, bq, d);
+    }
+    for (int b = kb0; b < kb1; ++b) {
+        const int bb = (b - kb0) & (kChunkBlocks - 1);
+        if (bb == 0) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < kChunkBlocks * 64; t += 256) {
+                const int rr = t & 63, cb = b + (t >> 6);
+                const int row = min(m_wg + rr, M - 1);
+                s_lds[t >> 6][rr] = cb < kb1 ? scales[(size_t)row * nb + cb] : 0.0f;
+            }
+            __syncthreads();
+        }
+        v4i ah_n = ah, al_n = al, bq_n = bq;
+        float d_n = d;
+        if (b + 1 < kb1) {
+            load(b + 1, ah_n, al_n, bq_n, d_n);
+        }
+        v16i c = {};
+        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bq, c, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            c[r] <<= 8;
+        }
+        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bq, c, 0, 0, 0);
+        // lane holds column lr of rows 8 * (r / 4) + 4 * kh + r % 4
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 s4 = *reinterpret_cast<const float4 *>(&s_lds[bb][wm * 32 + 8 * g + 4 * kh]);
+            acc[4 * g + 0] = fmaf((float)c[4 * g + 0], s4.x * d, acc[4 * g + 0]);
+            acc[4 * g + 1] = fmaf((float)c[4 * g + 1], s4.y * d, acc[4 * g + 1]);
+            acc[4 * g + 2] = fmaf((float)c[4 * g + 2], s4.z * d, acc[4 * g + 2]);
+            acc[4 * g + 3] = fmaf((float)c[4 * g + 3], s4.w * d, acc[4 * g + 3]);
+        }
+        ah = ah_n;
+        al = al_n;
+        bq = bq_n;
+        d = d_n;
+    }
+    const int col = n0 + lr;
+    if (col < N) {
+        float *dst = gridDim.z > 1 ? part + (size_t)blockIdx.z * M * N : out;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+            if (row < M) {
+                const size_t o = (size_t)row * N + col;
+                dst[o] = RESID && gridDim.z == 1 ? resid[o] + acc[r] : acc[r];
+            }
+        }
+    }
+}
+
+// out = (resid +) the splits' partial sums, added in split order.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int splits, size_t count,
+                                                          const float *resid, float *out) {
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
+        float a = part[i];
+        for (int z = 1; z < splits; ++z) {
+            a += part[(size_t)z * count + i];
+        }
+        out[i] = resid != nullptr ? resid[i] + a : a;
+    }
+}
+
+}  // namespace
+
+namespace te_hip {
+
+// digit planes padded to whole 32-row tiles
+static size_t plane_bytes(size_t rows, size_t cols) {
+    return (rows + 31) / 32 * 32 * cols;
+}
+
+size_t act_buffer_bytes(size_t rows, size_t cols) {
+    return 2 * plane_bytes(rows, cols) + rows * (cols / 32) * sizeof(float);
+}
+
+te_status launch_quant_act(int pre, const float *x, const float *x2, const float *norm_w, float eps, size_t rows,
+                           size_t cols, void *act, hipStream_t stream) {
+    if (rows == 0 || cols == 0 || cols % 32 != 0 || rows > 0x7fffffffu || cols > (1u << 24)) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    const size_t planes = plane_bytes(rows, cols);
+    int8_t *hi = static_cast<int8_t *>(act);
+    int8_t *lo = hi + planes;
+    float *scales = reinterpret_cast<float *>(lo + planes);
+    const dim3 grid((unsigned)rows);
+    if (pre == kActRmsNorm) {
+        quant_act_kernel<kActRmsNorm><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
+    } else if (pre == kActSwiGLU) {
+        quant_act_kernel<kActSwiGLU><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
+    } else {
+        quant_act_kernel<kActPlain><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
+    }
+    return launch_status();
+}
+
+te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n, size_t k,
+                        float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream) {
+    if ((ggml_type != kQ4_0 && ggml_type != kQ8_0) || k % 32 != 0 || rows == 0 || n == 0 ||
+        rows > 0x7fffffffu || n > 0x7fffffffu || k > (1u << 24) || ((size_t)weights & 1u) != 0) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    const size_t planes = plane_bytes(rows, k);
+    const int8_t *hi = static_cast<const int8_t *>(act);
+    const int8_t *lo = hi + planes;
+    const float *scales = reinterpret_cast<const float *>(lo + planes);
+    const size_t row_bytes = k / 32 * (ggml_type == kQ4_0 ? 18 : 34);
+    const size_t tiles = (n + 63) / 64 * ((rows + 63) / 64);
+    const size_t nb = k / 32;
+    // split K until the grid covers two workgroups per CU, keeping >= 8 blocks per split
+    size_t splits = 1;
+    const size_t want = 2 * (size_t)device_compute_units();
+    while (partials != nullptr && tiles * splits < want && nb / (splits * 2) >= 8 &&
+           splits * 2 * rows * n * sizeof(float) <= partial_bytes) {
+        splits *= 2;
+    }
+    const int per = (int)((nb + splits - 1) / splits);
+    const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)splits);
+    const unsigned char *w = static_cast<const unsigned char *>(weights);
+#define TE_GEMM(T, R)                                                                                             \
+    gemm_q_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n, (int)k, per, \
+                                                  out, resid, partials)
+    if (ggml_type == kQ4_0) {
+        if (resid != nullptr) {
+            TE_GEMM(kQ4_0, true);
+        } else {
+            TE_GEMM(kQ4_0, false);
+        }
+    } else {
+        if (resid != nullptr) {
+            TE_GEMM(kQ8_0, true);
+        } else {
+            TE_GEMM(kQ8_0, false);
+        }
+    }
+#undef TE_GEMM
+    if (splits > 1) {
+        const size_t count = rows * n;
+        const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
+        gemm_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, count, resid, out);
+    }
+    return launch_status();
+}
+
+}  // namespace te_hip
+
+// Test entry point: Y = pre(X) * W^T (+ R) through the two launches above, on
+// device pointers; `act` is scratch of te_hip_gemm_act_bytes(rows, k) bytes.
+extern "C" size_t te_hip_gemm_act_bytes(size_t rows, size_t k) {
+    return te_hip::act_buffer_bytes(rows, k);
+}
+
+extern "C" te_status te_hip_gemm_q_f32(const void *weights, uint32_t ggml_type, const float *x, const float *x2,
+                                       const float *norm_w, float epsilon, int pre, size_t rows, size_t n, size_t k,
+                                       float *out, const float *resid, void *act, float *partials,
+                                       size_t partial_bytes, void *stream) {
+    if (weights == nullptr || x == nullptr || out == nullptr || act == nullptr || pre < 0 || pre > 2 ||
+        (pre == kActRmsNorm && (norm_w == nullptr || !(epsilon > 0.0f))) || (pre == kActSwiGLU && x2 == nullptr)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = te_hip::as_stream(stream);
+    te_status st = te_hip::launch_quant_act(pre, x, x2, norm_w, epsilon, rows, k, act, s);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    return te_hip::launch_gemm_q(weights, ggml_type, act, rows, n, k, out, resid, partials, partial_bytes, s);
+}

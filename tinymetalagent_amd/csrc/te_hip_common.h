@@ -96,6 +96,22 @@ te_status launch_argmax(const float *values, size_t len, uint32_t *out_index, hi
 // the tensor may start at any byte address.
 te_status launch_dequant_row(const void *weights, uint32_t ggml_type, size_t cols, size_t row, float *out,
                              hipStream_t stream);
+// Rows rows[0 .. n) (a device array of valid row indices) into out [n][cols].
+te_status launch_dequant_rows(const void *weights, uint32_t ggml_type, size_t cols, const uint32_t *rows, size_t n,
+                              float *out, hipStream_t stream);
+
+// Batched-prefill GEMM (te_gemm.hip).  launch_quant_act turns rows x cols fp32
+// activations (after pre-op 0 none, 1 RMSNorm with norm_w / eps, 2 SwiGLU
+// with x2 as `up`) into the digit planes + block scales held in `act`
+// (act_buffer_bytes(rows, cols) bytes); launch_gemm_q then writes
+// out[m][n] = sum_k act[m][k] W[n][k] (+ resid[m][n]) for a Q4_0 / Q8_0
+// weight tensor W [n][k] at a 2-byte aligned address.
+size_t act_buffer_bytes(size_t rows, size_t cols);
+te_status launch_quant_act(int pre, const float *x, const float *x2, const float *norm_w, float eps, size_t rows,
+                           size_t cols, void *act, hipStream_t stream);
+// `partials` (partial_bytes, may be NULL) lets small output grids split K.
+te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n, size_t k,
+                        float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream);
 
 // One weight matrix of a fused GEMV launch: out[r] = W[r] . x' (+ resid[r] when
 // resid is set; resid may equal out), r < rows.

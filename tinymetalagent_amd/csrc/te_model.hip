@@ -1142,6 +1142,15 @@ struct te_context {
     std::vector<void *> allocations;
     // the tokens whose K / V fill cache positions 0 .. history.size() - 1
     std::vector<uint32_t> history;
+    // batched prompt prefill: chunk rows of hidden states, projections,
+    // attention output, gate / up, the GEMM's activation digits, token ids
+    bool batch_ok = false;
+    size_t chunk = 0;
+    float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *patt = nullptr, *pg = nullptr, *pu = nullptr;
+    void *pact = nullptr;
+    uint32_t *pids = nullptr;
+    float *ppart = nullptr;  // split-K partial sums
+    size_t ppart_bytes = 0;
 };
 
 namespace {
@@ -1305,8 +1314,100 @@ te_status init_state(te_context *c) {
         return s;
     }
     c->ws = ws;
+    // batched prefill needs 2-byte aligned layer weights (the GEMM's block reads)
+    c->batch_ok = true;
+    for (int w = 0; w < 7; ++w) {
+        for (size_t l = 0; l < c->layers; ++l) {
+            c->batch_ok = c->batch_ok && (c->offs[w][l] & 1u) == 0;
+        }
+    }
+    if (c->batch_ok) {
+        c->chunk = std::min<size_t>(256, c->ctx);
+        const size_t ch = c->chunk;
+        unsigned char *act = nullptr;
+        if ((s = dev_alloc(c, &c->px, ch * c->hidden)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->pq, ch * c->hidden)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->pk, ch * c->kv)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->pv, ch * c->kv)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->patt, ch * c->hidden)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->pg, ch * c->ffn)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->pu, ch * c->ffn)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->pids, ch)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->ppart, 8 * ch * c->hidden)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &act, te_hip::act_buffer_bytes(ch, std::max(c->hidden, c->ffn)))) != TE_STATUS_OK) {
+            return s;
+        }
+        c->pact = act;
+        c->ppart_bytes = 8 * ch * c->hidden * sizeof(float);
+    }
     c->ready = true;
     return TE_STATUS_OK;
+}
+
+// Prompt tokens ids[start .. end) at positions start .. end - 1, `chunk` rows
+// at a time through every layer (te_qwen_prefill_prompt_batch,
+// qwen.c:630-905): per layer RMSNorm + Q / K / V GEMMs, bias + RoPE + fp16
+// append + causal MFMA attention from the chunk's base position
+// (te_hip_attention_prefill_step_f16), Wo GEMM + residual, RMSNorm + gate / up
+// GEMMs, SwiGLU + down GEMM + residual.  The last row's hidden state is left
+// in hidden_buf.
+te_status prefill_batch(te_context *c, const uint32_t *ids, size_t start, size_t end) {
+    te_model *m = c->model;
+    const unsigned char *base = m->d_mapping;
+    const float eps = m->info.rms_norm_epsilon;
+    const size_t H = c->hidden, KV = c->kv, F = c->ffn;
+    te_status s = TE_STATUS_OK;
+    for (size_t p0 = start; p0 < end && s == TE_STATUS_OK; p0 += c->chunk) {
+        const size_t M = std::min(c->chunk, end - p0);
+        if (hipMemcpy(c->pids, ids + p0, M * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess) {
+            return TE_STATUS_RUNTIME_ERROR;
+        }
+        s = te_hip::launch_dequant_rows(base + c->embd_off, c->embd_type, H, c->pids, M, c->px, nullptr);
+        for (size_t l = 0; l < c->layers && s == TE_STATUS_OK; ++l) {
+            auto gemm = [&](int w, size_t n, size_t k, float *out, const float *resid) {
+                return te_hip::launch_gemm_q(base + c->offs[w][l], c->type, c->pact, M, n, k, out, resid, c->ppart,
+                                             c->ppart_bytes, nullptr);
+            };
+            const size_t kv_off = l * c->ctx * KV;
+            if ((s = te_hip::launch_quant_act(1, c->px, nullptr, c->attn_norm + l * H, eps, M, H, c->pact,
+                                              nullptr)) != TE_STATUS_OK ||
+                (s = gemm(0, H, H, c->pq, nullptr)) != TE_STATUS_OK ||
+                (s = gemm(1, KV, H, c->pk, nullptr)) != TE_STATUS_OK ||
+                (s = gemm(2, KV, H, c->pv, nullptr)) != TE_STATUS_OK ||
+                (s = te_hip_attention_prefill_step_f16(c->pq, c->pk, c->pv, c->qb + l * H, c->kb + l * KV,
+                                                       c->vb + l * KV, c->cos, c->sin, c->kc + kv_off,
+                                                       c->vc + kv_off, 1, 1, M, p0, c->ctx, c->heads, c->kv_heads,
+                                                       c->head_dim, c->patt, nullptr)) != TE_STATUS_OK ||
+                (s = te_hip::launch_quant_act(0, c->patt, nullptr, nullptr, 0.0f, M, H, c->pact, nullptr)) !=
+                    TE_STATUS_OK ||
+                (s = gemm(3, H, H, c->px, c->px)) != TE_STATUS_OK ||
+                (s = te_hip::launch_quant_act(1, c->px, nullptr, c->ffn_norm + l * H, eps, M, H, c->pact,
+                                              nullptr)) != TE_STATUS_OK ||
+                (s = gemm(4, F, H, c->pg, nullptr)) != TE_STATUS_OK ||
+                (s = gemm(5, F, H, c->pu, nullptr)) != TE_STATUS_OK ||
+                (s = te_hip::launch_quant_act(2, c->pg, c->pu, nullptr, 0.0f, M, F, c->pact, nullptr)) !=
+                    TE_STATUS_OK ||
+                (s = gemm(6, H, F, c->px, c->px)) != TE_STATUS_OK) {
+                break;
+            }
+        }
+        if (s == TE_STATUS_OK && p0 + M == end &&
+            hipMemcpy(c->hidden_buf, c->px + (M - 1) * H, H * sizeof(float), hipMemcpyDeviceToDevice) !=
+                hipSuccess) {
+            s = TE_STATUS_RUNTIME_ERROR;
+        }
+    }
+    return s;
+}
+
+// Greedy next token from hidden_buf: RMSNorm + lm_head GEMV, then argmax, into c->token.
+te_status project_greedy(te_context *c) {
+    const te_hip::GemvSeg h = {c->model->d_mapping + c->head_off, c->logits, nullptr, c->vocab};
+    float *xtmp = static_cast<float *>(c->ws);
+    te_status s = te_hip::launch_gemv(c->head_type, te_hip::kGemvRmsNorm, &h, 1, c->hidden, c->hidden_buf, nullptr,
+                                      c->out_norm, c->model->info.rms_norm_epsilon, xtmp,
+                                      xtmp + ((std::max(c->hidden, c->ffn) + 63) / 64 * 64), nullptr);
+    return s == TE_STATUS_OK ? te_hip::launch_argmax(c->logits, c->vocab, c->token, nullptr) : s;
 }
 
 // One token at `position` through every layer; with `token_out`, also the
@@ -1509,12 +1610,24 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         }
     }
     c->history.resize(start);
-    for (size_t i = start; i < ids.size(); ++i) {
-        if ((s = forward(c, ids[i], i, greedy && i + 1 == ids.size())) != TE_STATUS_OK) {
+    // several new prompt tokens go through the batched prefill unless
+    // TINYENGINE_BATCH_PREFILL=0 (the reference's switch, qwen.c:346-347)
+    const char *bp = getenv("TINYENGINE_BATCH_PREFILL");
+    if (c->batch_ok && ids.size() - start > 1 && (bp == nullptr || strcmp(bp, "0") != 0)) {
+        if ((s = prefill_batch(c, ids.data(), start, ids.size())) != TE_STATUS_OK ||
+            (greedy && (s = project_greedy(c)) != TE_STATUS_OK)) {
             c->history.clear();
             return s;
         }
-        c->history.push_back(ids[i]);
+        c->history.insert(c->history.end(), ids.begin() + start, ids.end());
+    } else {
+        for (size_t i = start; i < ids.size(); ++i) {
+            if ((s = forward(c, ids[i], i, greedy && i + 1 == ids.size())) != TE_STATUS_OK) {
+                c->history.clear();
+                return s;
+            }
+            c->history.push_back(ids[i]);
+        }
     }
     uint32_t next = 0;
     if ((s = next_token(c, sm, next)) != TE_STATUS_OK) {

@@ -821,13 +821,16 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *values, uint3
 // Row `row` of a [rows][cols] GGUF tensor as fp32 (te_model_dequantize_row_f32,
 // ops.c:127-175; block formats ops.c:15-21): Q4_0 (code - 8) * d with low
 // nibbles first, Q8_0 code * d, F32 as stored.  One thread per value.
+// Row rows[blockIdx.y] (or `row` without a list) into out + blockIdx.y * cols.
 __global__ __launch_bounds__(256) void dequant_row_kernel(const unsigned char *weights, uint32_t ggml_type,
-                                                          int cols, size_t row_bytes, size_t row, float *out) {
+                                                          int cols, size_t row_bytes, size_t row,
+                                                          const uint32_t *rows, float *out) {
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= cols) {
         return;
     }
-    const unsigned char *r = weights + row * row_bytes;
+    const unsigned char *r = weights + (rows != nullptr ? (size_t)rows[blockIdx.y] : row) * row_bytes;
+    out += (size_t)blockIdx.y * cols;
     float v;
     if (ggml_type == kGgmlF32) {
         __builtin_memcpy(&v, r + (size_t)c * 4, 4);  // any byte alignment
@@ -1119,7 +1122,15 @@ te_status launch_dequant_row(const void *weights, uint32_t ggml_type, size_t col
                              hipStream_t stream) {
     const size_t row_bytes = ggml_type == kGgmlF32 ? cols * 4 : ggml_row_bytes(ggml_type, cols);
     dequant_row_kernel<<<dim3((unsigned)((cols + 255) / 256)), 256, 0, stream>>>(
-        static_cast<const unsigned char *>(weights), ggml_type, (int)cols, row_bytes, row, out);
+        static_cast<const unsigned char *>(weights), ggml_type, (int)cols, row_bytes, row, nullptr, out);
+    return launch_status();
+}
+
+te_status launch_dequant_rows(const void *weights, uint32_t ggml_type, size_t cols, const uint32_t *rows, size_t n,
+                              float *out, hipStream_t stream) {
+    const size_t row_bytes = ggml_type == kGgmlF32 ? cols * 4 : ggml_row_bytes(ggml_type, cols);
+    dequant_row_kernel<<<dim3((unsigned)((cols + 255) / 256), (unsigned)n), 256, 0, stream>>>(
+        static_cast<const unsigned char *>(weights), ggml_type, (int)cols, row_bytes, 0, rows, out);
     return launch_status();
 }
 
