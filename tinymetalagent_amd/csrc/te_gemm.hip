@@ -23,9 +23,9 @@
 // [32 k] int8), so one wave's operand for one block is 1 KiB contiguous.
 //
 // Tiles: a 256-thread workgroup computes a 64 x 64 block of Y as four 32 x 32
-// wave tiles; the K loop prefetches the next block's operands into registers
-// and stages the activation scales of the workgroup's 64 rows in LDS, 8
-// blocks at a time.  Where the output tiles alone would not fill the GPU,
+// wave tiles; the K loop takes two blocks per step (two independent MFMA
+// chains) and stages the activation scales of the workgroup's 64 rows in
+// LDS, 8 blocks at a time.  Where the output tiles alone would not fill the GPU,
 // the K range is split over grid.z and a second kernel adds the partial sums
 // in a fixed order (deterministic).
 #include "te_hip_common.h"
@@ -80,10 +80,11 @@ __global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__r
         }
         rms = 1.0f / sqrtf((float)(t / (double)K) + eps);
     }
-    // one 32-value block per half wave: lane j of the half takes value j
+    // one 32-value block per half wave: lane j of the half takes value j;
+    // workgroup blockIdx.y of gridDim.y takes every gridDim.y-th group of blocks
     const int lane = threadIdx.x & 31;
-    const int halves = kActThreads / 32;
-    for (int b = threadIdx.x >> 5; b < K / 32; b += halves) {
+    const int halves = kActThreads / 32 * gridDim.y;
+    for (int b = (threadIdx.x >> 5) + blockIdx.y * (kActThreads / 32); b < K / 32; b += halves) {
         const int i = b * 32 + lane;
         float v = xr[i];
         if (PRE == kActRmsNorm) {
@@ -179,12 +180,29 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const unsigned char *__rest
         al = *reinterpret_cast<const v4i *>(lo + o);
         bq = weight_codes<TYPE>(b_row + (size_t)b * kBlockBytes, kh, d);
     };
-    v4i ah, al, bq;
-    float d = 0.0f;
-    if (kb0 < kb1) {
-        load(kb0, ah, al, bq, d);
-    }
-    for (int b = kb0; b < kb1; ++b) {
+    // two blocks per step: two independent MFMA chains in flight
+    auto step = [&](int bb, const v4i &ah, const v4i &al, const v4i &bq, float d, v16i &c) {
+        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bq, v16i{}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            c[r] <<= 8;
+        }
+        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bq, c, 0, 0, 0);
+        (void)bb;
+        (void)d;
+    };
+    auto scale_add = [&](int bb, const v16i &c, float d) {
+        // lane holds column lr of rows 8 * (r / 4) + 4 * kh + r % 4
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 s4 = *reinterpret_cast<const float4 *>(&s_lds[bb][wm * 32 + 8 * g + 4 * kh]);
+            acc[4 * g + 0] = fmaf((float)c[4 * g + 0], s4.x * d, acc[4 * g + 0]);
+            acc[4 * g + 1] = fmaf((float)c[4 * g + 1], s4.y * d, acc[4 * g + 1]);
+            acc[4 * g + 2] = fmaf((float)c[4 * g + 2], s4.z * d, acc[4 * g + 2]);
+            acc[4 * g + 3] = fmaf((float)c[4 * g + 3], s4.w * d, acc[4 * g + 3]);
+        }
+    };
+    for (int b = kb0; b < kb1; b += 2) {
         const int bb = (b - kb0) & (kChunkBlocks - 1);
         if (bb == 0) {
             __syncthreads();
@@ -195,31 +213,22 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const unsigned char *__rest
             }
             __syncthreads();
         }
-        v4i ah_n = ah, al_n = al, bq_n = bq;
-        float d_n = d;
-        if (b + 1 < kb1) {
-            load(b + 1, ah_n, al_n, bq_n, d_n);
+        v4i ah0, al0, bq0, ah1, al1, bq1;
+        float d0, d1;
+        load(b, ah0, al0, bq0, d0);
+        const bool two = b + 1 < kb1;
+        if (two) {
+            load(b + 1, ah1, al1, bq1, d1);
         }
-        v16i c = {};
-        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bq, c, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            c[r] <<= 8;
+        v16i c0, c1;
+        step(bb, ah0, al0, bq0, d0, c0);
+        if (two) {
+            step(bb + 1, ah1, al1, bq1, d1, c1);
         }
-        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bq, c, 0, 0, 0);
-        // lane holds column lr of rows 8 * (r / 4) + 4 * kh + r % 4
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4 s4 = *reinterpret_cast<const float4 *>(&s_lds[bb][wm * 32 + 8 * g + 4 * kh]);
-            acc[4 * g + 0] = fmaf((float)c[4 * g + 0], s4.x * d, acc[4 * g + 0]);
-            acc[4 * g + 1] = fmaf((float)c[4 * g + 1], s4.y * d, acc[4 * g + 1]);
-            acc[4 * g + 2] = fmaf((float)c[4 * g + 2], s4.z * d, acc[4 * g + 2]);
-            acc[4 * g + 3] = fmaf((float)c[4 * g + 3], s4.w * d, acc[4 * g + 3]);
+        scale_add(bb, c0, d0);
+        if (two) {
+            scale_add(bb + 1, c1, d1);
         }
-        ah = ah_n;
-        al = al_n;
-        bq = bq_n;
-        d = d_n;
     }
     const int col = n0 + lr;
     if (col < N) {
@@ -269,7 +278,8 @@ te_status launch_quant_act(int pre, const float *x, const float *x2, const float
     int8_t *hi = static_cast<int8_t *>(act);
     int8_t *lo = hi + planes;
     float *scales = reinterpret_cast<float *>(lo + planes);
-    const dim3 grid((unsigned)rows);
+    // without a row-wide norm, several workgroups share a long row
+    const dim3 grid((unsigned)rows, pre == kActRmsNorm ? 1u : (unsigned)std::max<size_t>(1, cols / 32 / 64));
     if (pre == kActRmsNorm) {
         quant_act_kernel<kActRmsNorm><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
     } else if (pre == kActSwiGLU) {
