@@ -271,3 +271,41 @@ def test_long_prompt_batched_and_token_by_token_vs_oracle(q4_model, monkeypatch,
     assert len(got) == 12
     exact = _check_greedy(q, pids, got, 512)
     print(f"300-token prompt, batch {batch}: {exact}/12 steps decided beyond the tolerance, all equal")
+
+
+def test_two_threads_two_contexts_one_model(q4_model, monkeypatch):
+    """Two threads generate at once on two contexts of one freshly loaded
+    model (the first GPU use, the file upload, races between them); each gets
+    the tokens a lone call gets."""
+    import threading
+    q = q4_model
+    monkeypatch.setenv("TINYENGINE_TEMPERATURE", "0")
+    monkeypatch.setenv("TINYENGINE_IGNORE_EOS", "1")
+    prompts = ["hello world, the engine", "json def return the cache"]
+    with Model(q["path"], RuntimeOptions(context_tokens=128)) as m:
+        alone = []
+        for p in prompts:
+            ids = []
+            m.generate_raw(p, 16, on_token=lambda t, i, ids=ids: ids.append(i))
+            alone.append(ids)
+    with Model(q["path"], RuntimeOptions(context_tokens=128)) as m:
+        got = [[], []]
+        errors = []
+
+        def run(k):
+            try:
+                for _ in range(3):
+                    ids = []
+                    m.generate_raw(prompts[k], 16, on_token=lambda t, i: ids.append(i))
+                    got[k].append(ids)
+            except Exception as e:  # pragma: no cover
+                errors.append(e)
+
+        threads = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=120)
+        assert not errors
+        for k in range(2):
+            assert got[k] == [alone[k]] * 3
