@@ -315,3 +315,51 @@ def test_sampler_restatement_pins():
         u.append(v)
     u = np.array(u)
     assert 0.0 <= u.min() and u.max() < 1.0 and abs(u.mean() - 0.5) < 0.01 and abs(u.var() - 1 / 12) < 0.003
+
+
+def test_loader_survives_corrupted_files(tmp_path, qwen_file):
+    """Truncations, byte flips and oversized counts / lengths anywhere in the
+    header and metadata: every load returns a status (OK or an error), never
+    crashes; a model that loads still tokenizes and reports info."""
+    import ctypes
+    lib = R.load_library()
+    good = open(G.kernel_ops_fixture(tmp_path / "k.gguf"), "rb").read()
+    big = open(qwen_file["path"], "rb").read()[:200000]
+    r = random.Random(9)
+    opts = RuntimeOptions()._to_c()
+    seen = set()
+    for trial in range(600):
+        src = good if trial % 2 == 0 else big
+        data = bytearray(src)
+        kind = trial % 4
+        if kind == 0:
+            data = data[:r.randint(0, len(data))]
+        elif kind == 1:
+            for _ in range(r.randint(1, 8)):
+                data[r.randrange(0, min(len(data), 4096))] = r.randrange(256)
+        elif kind == 2:  # a huge u64 (count / length / dimension / offset) somewhere in the header
+            at = r.randrange(8, min(len(data), 4096) - 8)
+            data[at:at + 8] = struct.pack("<Q", r.choice([2 ** 63, 2 ** 64 - 1, 2 ** 32, 2 ** 40 + 7]))
+        else:
+            at = r.randrange(8, min(len(data), 4096) - 4)
+            data[at:at + 4] = struct.pack("<I", r.choice([9, 12, 13, 255, 2 ** 31]))
+        p = tmp_path / "fuzz.gguf"
+        p.write_bytes(bytes(data))
+        h = ctypes.c_void_p()
+        st = lib.te_model_load_gguf(str(p).encode(), ctypes.byref(opts), ctypes.byref(h))
+        seen.add(st)
+        assert st in (0, 2, 3, 4, 5)
+        if st == 0:
+            m = Model.__new__(Model)
+            m._lib, m._model, m._options = lib, h, RuntimeOptions()
+            m.info()
+            m.tokenizer_info()
+            try:
+                m.tokenize("ab <|im_start|> x")
+                m.detokenize_bytes(list(range(min(3, m.tokenizer_info().token_count))))
+            except R.TinyEngineError:
+                pass
+            m.close()
+        else:
+            assert not h.value
+    assert 0 in seen and len(seen) >= 3

@@ -78,7 +78,7 @@ class _TokenizerInfo(ctypes.Structure):
 
 
 def _text(raw: bytes) -> str:
-    return raw.split(b"\0", 1)[0].decode()
+    return raw.split(b"\0", 1)[0].decode(errors="replace")
 
 
 @dataclass(frozen=True)
