@@ -710,6 +710,18 @@ def generate_case(ggml_type: int, prompt_tokens: int = 512, new_tokens: int = 12
                         "prompt_tokens_per_s": round(prompt_tokens / (stamps[0] - t0), 1),
                         "decode_tokens_per_s": round((new_tokens - 1) / (stamps[-1] - stamps[0]), 1),
                         "decode_ms_per_token": r((stamps[-1] - stamps[0]) * 1e3 / (new_tokens - 1), 3)}
+        # the reference's default sampling (T 0.3, top-k 40): logits come back per token
+        os.environ.pop("TINYENGINE_TEMPERATURE")
+        stamps = []
+        cb = R._TOKEN_CALLBACK(lambda s, i, u: stamps.append(time.perf_counter()))
+        hctx = ctypes.c_void_p()
+        opts = RuntimeOptions(context_tokens=ctx)._to_c()
+        R.check(lib.te_context_create(m.handle, ctypes.byref(opts), ctypes.byref(hctx)))
+        R.check(lib.te_generate_raw(hctx, b"a" * prompt_tokens, new_tokens, cb, None))
+        lib.te_context_free(hctx)
+        out["sampled_t0.3_top40"] = {"decode_tokens_per_s": round((len(stamps) - 1) / (stamps[-1] - stamps[0]), 1),
+                                     "decode_ms_per_token": r((stamps[-1] - stamps[0]) * 1e3 / (len(stamps) - 1), 3)}
+        os.environ["TINYENGINE_TEMPERATURE"] = "0"
         # a second turn on the same context: the first turn's prompt plus 64
         # new tokens, with the cache reused (default) and recomputed
         for mode in ("1", "0"):
