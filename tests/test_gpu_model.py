@@ -251,26 +251,26 @@ def test_session_kv_reuse_matches_fresh_context(q4_model, monkeypatch):
 
 @pytest.mark.parametrize("batch", ["1", "0"])
 def test_long_prompt_batched_and_token_by_token_vs_oracle(q4_model, monkeypatch, batch):
-    """A 300-token prompt: two 256-row chunks of batched prefill (the second
-    from base position 256), or one token at a time; greedy tokens against the
+    """A 600-token prompt: two chunks of batched prefill (512 rows, then 88 from
+    base position 512), or one token at a time; greedy tokens against the
     oracle's loop, teacher-forced."""
     q = q4_model
     import random
     rnd = random.Random(4)
     words = ["hello", " world", " the", " engine", " cache", "\n", " json", "{", "}", " qwen", " gpu"]
-    prompt = "".join(rnd.choice(words) for _ in range(400))
+    prompt = "".join(rnd.choice(words) for _ in range(800))
     pids = _prompt_ids(q, prompt)
-    assert len(pids) > 300
-    pids = pids[:300]
+    assert len(pids) > 600
+    pids = pids[:600]
     orc = OT.Tokenizer(q["tokens"], q["types"], q["merges"])
     prompt = orc.detokenize(pids, False).decode()
     assert _prompt_ids(q, prompt) == pids
-    got, _ = _gpu_generate(q["path"], prompt, 12, ctx=512, monkeypatch=monkeypatch,
+    got, _ = _gpu_generate(q["path"], prompt, 12, ctx=1024, monkeypatch=monkeypatch,
                            env={"TINYENGINE_TEMPERATURE": "0", "TINYENGINE_IGNORE_EOS": "1",
                                 "TINYENGINE_BATCH_PREFILL": batch})
     assert len(got) == 12
-    exact = _check_greedy(q, pids, got, 512)
-    print(f"300-token prompt, batch {batch}: {exact}/12 steps decided beyond the tolerance, all equal")
+    exact = _check_greedy(q, pids, got, 1024)
+    print(f"600-token prompt, batch {batch}: {exact}/12 steps decided beyond the tolerance, all equal")
 
 
 def test_two_threads_two_contexts_one_model(q4_model, monkeypatch):

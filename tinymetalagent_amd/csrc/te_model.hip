@@ -1322,7 +1322,7 @@ te_status init_state(te_context *c) {
         }
     }
     if (c->batch_ok) {
-        c->chunk = std::min<size_t>(256, c->ctx);
+        c->chunk = std::min<size_t>(512, c->ctx);
         const size_t ch = c->chunk;
         unsigned char *act = nullptr;
         if ((s = dev_alloc(c, &c->px, ch * c->hidden)) != TE_STATUS_OK ||
