@@ -37,6 +37,7 @@ constexpr size_t kMaxPairLdsBytes = 160 * 1024;     // staged digit planes (gfx9
 constexpr size_t kPairLdsBytes = 13 * 16;           // LDS per block pair: 12 uint4 of digit planes + scales
 constexpr int kStreamChunks = 10;                   // streamed kernel: 16-byte chunk loads per lane per tile
 constexpr size_t kStreamTileBytes = kStreamChunks * 1024;  // its LDS tile buffer per wave
+constexpr int kWideStreamChunks = 12;                // Q8_0 rows of 10-12 KB, one row per tile
 template <uint32_t TYPE>
 constexpr int kDigitPlanes = TYPE == kGgmlQ4_0 ? 6 : 3;  // balanced base-16 / base-256 digits of 22-bit X
 
@@ -905,14 +906,19 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
             nr = cand;
         }
     }
-    const size_t waves_fit = groups * row_bytes + 15 <= kStreamTileBytes && plane_bytes < kMaxPairLdsBytes
-                                 ? (kMaxPairLdsBytes - plane_bytes) / kStreamTileBytes
+    // Q8_0 rows of 10-12 KB (ffn_down at 11008 columns: 11696 bytes) take
+    // 12-chunk tiles, one row per tile
+    const bool wide = ggml_type == kGgmlQ8_0 && groups == 1 && row_bytes + 15 > kStreamTileBytes &&
+                      row_bytes + 15 <= (size_t)kWideStreamChunks * 1024;
+    const size_t tile_lds = wide ? (size_t)kWideStreamChunks * 1024 : kStreamTileBytes;
+    const size_t waves_fit = groups * row_bytes + 15 <= tile_lds && plane_bytes < kMaxPairLdsBytes
+                                 ? (kMaxPairLdsBytes - plane_bytes) / tile_lds
                                  : 0;
     if (waves_fit < 4) {
         return TE_STATUS_OK;
     }
     const int wpg = waves_fit < (size_t)kPairWaves ? (int)waves_fit : kPairWaves;
-    const size_t lds = plane_bytes + (size_t)wpg * kStreamTileBytes;
+    const size_t lds = plane_bytes + (size_t)wpg * tile_lds;
     a.row_bytes = row_bytes;
     a.tiles = 0;
     for (int s = 0; s < a.nseg; ++s) {
@@ -961,7 +967,26 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
             TE_STREAM_NR(T, 16);  \
         }                         \
     } while (0)
-    if (ggml_type == kGgmlQ4_0) {
+    if (wide) {
+#define TE_STREAM_WIDE(P)                                                                                           \
+    do {                                                                                                            \
+        if (lds > 65536 &&                                                                                          \
+            hipFuncSetAttribute(                                                                                    \
+                reinterpret_cast<const void *>(&matvec_stream_kernel<kGgmlQ8_0, 64, 1, kWideStreamChunks, P>),      \
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {                              \
+            return TE_STATUS_RUNTIME_ERROR;                                                                         \
+        }                                                                                                           \
+        matvec_stream_kernel<kGgmlQ8_0, 64, 1, kWideStreamChunks, P><<<grid, dim3(64 * wpg), lds, stream>>>(a);     \
+    } while (0)
+        if (pre == kPreRmsNorm) {
+            TE_STREAM_WIDE(kPreRmsNorm);
+        } else if (pre == kPreSwiGLU) {
+            TE_STREAM_WIDE(kPreSwiGLU);
+        } else {
+            TE_STREAM_WIDE(kPreNone);
+        }
+#undef TE_STREAM_WIDE
+    } else if (ggml_type == kGgmlQ4_0) {
         TE_STREAM_LPR(kGgmlQ4_0);
     } else {
         TE_STREAM_LPR(kGgmlQ8_0);
