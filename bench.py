@@ -45,6 +45,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "decode-attn µs/layer + HBM GB/s (% peak) at Qwen2.5-3B, ctx 8K; prefill TFLOP/s"
+INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 THETA = 1e6
@@ -613,6 +614,42 @@ def decode_layers_case(torch, LY, V, ggml_type: int, *, layers=36, heads=16, kv_
             "frac": r((wbytes + kvbytes) / us / 1e3 / HBM_PEAK_GBS), "launches_per_token": 6 * layers + 2}
 
 
+def gemm_case(torch, ggml_type: int, rows: int, n: int, k: int, pre: int = 0, reps: int = 20) -> dict:
+    """te_hip_gemm_q_f32 (the batched-prefill projection: activation digits +
+    int8-MFMA GEMM) at one prompt-chunk shape, graph-replayed over weight
+    copies rotated past the MALL.  Algorithmic work: rows * n * k multiply-adds,
+    priced against the dense int8 MFMA peak at two int8 products per
+    multiply-add (two activation digits) and, as `frac_algorithmic`, at one."""
+    from tinymetalagent_amd import runtime as R
+    lib = R.load_library()
+    rb = k // 32 * (18 if ggml_type == 2 else 34)
+    copies = max(1, int(math.ceil(1.2e9 / (n * rb))))
+    ws = [random_ggml(torch, ggml_type, n * rb) for _ in range(copies)]
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(rows, k, generator=g, device="cuda")
+    x2 = torch.randn(rows, k, generator=g, device="cuda")
+    nw = torch.ones(k, device="cuda")
+    out = torch.empty(rows, n, device="cuda")
+    act = torch.empty(lib.te_hip_gemm_act_bytes(rows, k), dtype=torch.uint8, device="cuda")
+    part = torch.empty(8 * rows * n, device="cuda")
+    state = {"i": 0}
+
+    def launch(s):
+        w = ws[state["i"] % copies]
+        state["i"] += 1
+        R.check(lib.te_hip_gemm_q_f32(w.data_ptr(), ggml_type, x.data_ptr(), x2.data_ptr(), nw.data_ptr(), 1e-6, pre,
+                                      rows, n, k, out.data_ptr(), None, act.data_ptr(), part.data_ptr(),
+                                      part.numel() * 4, s.cuda_stream))
+    us = graph_time_us(torch, [launch] * copies, reps)
+    macs = rows * n * k
+    tops = 2 * macs / us / 1e6
+    del ws
+    torch.cuda.empty_cache()
+    return {"rows": rows, "n": n, "k": k, "us": r(us, 2), "algorithmic_tops": round(tops, 1),
+            "int8_mfma_tops": round(2 * tops, 1), "frac": r(2 * tops / INT8_MFMA_PEAK_TOPS),
+            "frac_algorithmic": r(tops / INT8_MFMA_PEAK_TOPS)}
+
+
 def write_3b_gguf(path: str, ggml_type: int, *, layers=36, heads=16, kv_heads=2, d=128, ffn=11008,
                   vocab=151936) -> int:
     """A Qwen2.5-3B-shaped GGUF with random weights (block scales 2^-7, random
@@ -793,7 +830,9 @@ def main():
         profile_layers_sequence(torch)
         return
     if args.generate:
-        print(json.dumps({"generate": {"q4_0": generate_case(2), "q8_0": generate_case(8)}}))
+        print(json.dumps({"generate": {"q4_0": generate_case(2), "q8_0": generate_case(8),
+                                       "prefill_gemm_gate_q4_0": gemm_case(torch, 2, 512, 11008, 2048, pre=1),
+                                       "prefill_gemm_down_q4_0": gemm_case(torch, 2, 512, 2048, 11008, pre=2)}}))
         return
     timer = Timer(torch)
     H, KV, D, LAYERS = 16, 2, 128, 36
@@ -928,6 +967,8 @@ def main():
             "workload": "te_generate_raw on a Qwen2.5-3B-shaped GGUF (random weights, 151936-token byte-level "
                         "vocabulary): 512 prompt tokens token by token, then 128 greedy tokens; ctx 1024",
             "q4_0": generate_case(2),
+            "prefill_gemm_gate_q4_0": gemm_case(torch, 2, 512, 11008, 2048, pre=1),
+            "prefill_gemm_down_q4_0": gemm_case(torch, 2, 512, 2048, 11008, pre=2),
         }
     if not args.no_cpu_baseline:
         ql, kl, vl = dec["cpu_sample"]
