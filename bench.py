@@ -82,6 +82,8 @@ def parse_args():
                    help="run a fixed decode-layer sequence for rocprofv3 (10x lm_head GEMV Q4_0 and Q8_0 over "
                         "rotated weight copies, 5x a 3B decode token through 36 layers, 3x a 512 MiB device copy) "
                         "and exit")
+    p.add_argument("--prefill-gemm", action="store_true",
+                   help="only the prefill GEMM cases (3B gate and down, 512 rows, Q4_0); print their JSON and exit")
     p.add_argument("--generate", action="store_true",
                    help="only the end-to-end te_generate_raw case on a 3B-shaped GGUF (Q4_0 and Q8_0); print its "
                         "JSON and exit")
@@ -828,6 +830,10 @@ def main():
     if args.profile_layers:
         gpu_warmup(torch, A, args.warmup_seconds)
         profile_layers_sequence(torch)
+        return
+    if args.prefill_gemm:
+        print(json.dumps({"prefill_gemm_gate_q4_0": gemm_case(torch, 2, 512, 11008, 2048, pre=1, reps=5),
+                          "prefill_gemm_down_q4_0": gemm_case(torch, 2, 512, 2048, 11008, pre=2, reps=5)}))
         return
     if args.generate:
         print(json.dumps({"generate": {"q4_0": generate_case(2), "q8_0": generate_case(8),
