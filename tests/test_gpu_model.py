@@ -309,3 +309,42 @@ def test_two_threads_two_contexts_one_model(q4_model, monkeypatch):
         assert not errors
         for k in range(2):
             assert got[k] == [alone[k]] * 3
+
+
+def test_context_boundary(q4_model, monkeypatch):
+    """prompt + max_tokens == context_tokens runs (the last token lands on the
+    last slot); one more is UNSUPPORTED (qwen.c:446-450)."""
+    q = q4_model
+    monkeypatch.setenv("TINYENGINE_TEMPERATURE", "0")
+    monkeypatch.setenv("TINYENGINE_IGNORE_EOS", "1")
+    prompt = "hello world, the engine"
+    n = len(_prompt_ids(q, prompt))
+    with Model(q["path"], RuntimeOptions(context_tokens=n + 8)) as m:
+        ids = []
+        m.generate_raw(prompt, 8, on_token=lambda t, i: ids.append(i))
+        assert len(ids) == 8
+        with pytest.raises(R.TinyEngineError, match="unsupported"):
+            m.generate_raw(prompt, 9)
+
+
+def test_session_reuse_with_batched_prefill_vs_oracle(q4_model, monkeypatch):
+    """Second turn on one context with batched prefill: the cached prefix
+    (prompt from the batched path, the reply from the decode path) plus a
+    batched suffix from its base position; greedy tokens against the oracle's
+    loop over the whole second-turn prompt, teacher-forced."""
+    q = q4_model
+    monkeypatch.setenv("TINYENGINE_TEMPERATURE", "0")
+    monkeypatch.setenv("TINYENGINE_IGNORE_EOS", "1")
+    monkeypatch.delenv("TINYENGINE_BATCH_PREFILL", raising=False)
+    orc = OT.Tokenizer(q["tokens"], q["types"], q["merges"])
+    turn1 = "<|im_start|>user\nhello world<|im_end|>\n<|im_start|>assistant\n"
+    with Model(q["path"], RuntimeOptions(context_tokens=256)) as m, m.session() as s:
+        ids1 = []
+        s.generate_raw(turn1, 16, on_token=lambda t, i: ids1.append(i))
+        reply = orc.detokenize(ids1, False).decode(errors="replace")
+        turn2 = turn1 + reply + "<|im_end|>\n<|im_start|>user\nthe engine json<|im_end|>\n"
+        got = []
+        s.generate_raw(turn2, 12, on_token=lambda t, i: got.append(i))
+    assert len(got) == 12
+    exact = _check_greedy(q, _prompt_ids(q, turn2), got, 256)
+    print(f"second turn with reuse: {exact}/12 steps decided beyond the tolerance, all equal")
