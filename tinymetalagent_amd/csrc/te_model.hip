@@ -1598,10 +1598,12 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
     const bool greedy = sm.temperature <= 0.0f;
     // Cache reuse across calls on one context: the positions whose tokens
     // equal the previous call's (prompt and forwarded generated tokens) keep
-    // their K / V.  Their values are what recomputing them would write (the
-    // same tokens at the same positions through the same kernels), so the
-    // result is the same as a fresh context's.  The last prompt token is
-    // always run, for its logits.  TINYENGINE_KV_REUSE=0 turns reuse off.
+    // their K / V, as the previous call computed them.  With one numeric path
+    // (TINYENGINE_BATCH_PREFILL=0) that is exactly what a fresh context would
+    // compute; with the batched prefill, positions the decode path filled
+    // (generated tokens) differ from a fresh context's batched values by
+    // rounding only.  The last prompt token is always run, for its logits.
+    // TINYENGINE_KV_REUSE=0 turns reuse off.
     size_t start = 0;
     const char *reuse = getenv("TINYENGINE_KV_REUSE");
     if (reuse == nullptr || strcmp(reuse, "0") != 0) {
@@ -1613,14 +1615,24 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
     // several new prompt tokens go through the batched prefill unless
     // TINYENGINE_BATCH_PREFILL=0 (the reference's switch, qwen.c:346-347)
     const char *bp = getenv("TINYENGINE_BATCH_PREFILL");
+    bool batched = false;
     if (c->batch_ok && ids.size() - start > 1 && (bp == nullptr || strcmp(bp, "0") != 0)) {
-        if ((s = prefill_batch(c, ids.data(), start, ids.size())) != TE_STATUS_OK ||
-            (greedy && (s = project_greedy(c)) != TE_STATUS_OK)) {
+        s = prefill_batch(c, ids.data(), start, ids.size());
+        if (s == TE_STATUS_OK && greedy) {
+            s = project_greedy(c);
+        }
+        // UNSUPPORTED (a shape the batched kernels do not take): one token at
+        // a time instead, as the reference falls back (qwen.c:348-356)
+        if (s != TE_STATUS_OK && s != TE_STATUS_UNSUPPORTED) {
             c->history.clear();
             return s;
         }
-        c->history.insert(c->history.end(), ids.begin() + start, ids.end());
-    } else {
+        batched = s == TE_STATUS_OK;
+        if (batched) {
+            c->history.insert(c->history.end(), ids.begin() + start, ids.end());
+        }
+    }
+    if (!batched) {
         for (size_t i = start; i < ids.size(); ++i) {
             if ((s = forward(c, ids[i], i, greedy && i + 1 == ids.size())) != TE_STATUS_OK) {
                 c->history.clear();
