@@ -111,12 +111,29 @@ TE_API te_status te_hip_rope_kv_append_f16(
  * bytes for the same positions, or NULL to use a buffer the library owns (grown
  * on demand, guarded by the library mutex; calls using it must all go to one
  * stream).  Calls sharing one workspace must be stream-ordered.  The chunking
- * (and so the workspace size) depends on all positions, not only the longest:
- * the chunk length balances the total work over the GPU's wave slots.
+ * depends on all positions, not only the longest (the chunk length balances
+ * the total work over the GPU's wave slots); the workspace size depends only
+ * on the largest position and never decreases with it.
  */
 TE_API size_t te_hip_attention_decode_workspace_bytes(const size_t *positions, size_t position, size_t seqs,
                                                       size_t layers, size_t heads, size_t kv_heads,
                                                       size_t head_dim);
+
+/*
+ * The chunking behind the decode entry points: *chunk = cache positions per
+ * split-K workgroup, *chunks = chunks of the longest sequence.  fp32_cache != 0
+ * gives the chunking of te_attention_decode_f32 (seqs == layers == 1; a
+ * power-of-two multiple of 512 positions, at most 4096 chunks for any
+ * position).  A host computation from the sizes and the device's compute-unit
+ * count (256 assumed without a device).  The workspace query above sizes for
+ * an upper bound of `chunks` that never decreases with the position, so a
+ * workspace sized at the largest position a caller reaches serves every
+ * smaller one.  INVALID_ARGUMENT for null outputs, zero sizes or
+ * seqs > TE_HIP_MAX_SEQS.
+ */
+TE_API te_status te_hip_attention_decode_chunking(const size_t *positions, size_t position, size_t seqs,
+                                                  size_t layers, size_t kv_heads, int fp32_cache, size_t *chunk,
+                                                  size_t *chunks);
 
 TE_API te_status te_hip_attention_decode_f16(
     const float *query, const uint16_t *key_cache, const uint16_t *value_cache,

@@ -8,13 +8,16 @@
  * unchanged.  The Apple-only #error guard of the reference (tinyengine.h:4-6)
  * is dropped: this build targets Linux + ROCm.
  *
- * In this build the attention step (te_rope_f32, te_attention_decode_f32, and
- * the te_hip_* backend slot in te_hip_backend.h) executes on the GPU through
- * hand-written HIP kernels.  Entry points that belong to subsystems outside the
- * attention step (GGUF loading, tokenizer, quantized matvec, full generation)
- * are exported so the binding resolves every symbol, and return
- * TE_STATUS_UNSUPPORTED -- the status the reference itself uses for "this path
- * is not available here" (reference qwen.c:1162-1165).
+ * In this build every compute entry point runs on the GPU through
+ * hand-written HIP kernels: the attention step (te_rope_f32,
+ * te_attention_decode_f32 and the te_hip_* backend slot in te_hip_backend.h),
+ * the vector ops, the quantized matvec and generation.  GGUF loading, the
+ * tensor / tokenizer queries and the tokenizer itself are host work, as in the
+ * reference.  Without a usable gfx950 device the compute entry points return
+ * TE_STATUS_UNSUPPORTED -- the status the reference uses for "this path is not
+ * available here" (reference qwen.c:1162-1165) -- and never compute on the
+ * CPU.  Tensor types other than F32 / Q4_0 / Q8_0 (F16 for reads) are
+ * UNSUPPORTED where the reference would compute them.
  */
 #ifndef TINYENGINE_H
 #define TINYENGINE_H
@@ -242,9 +245,13 @@ TE_API int te_kernel_plan_supports_quant(const te_kernel_plan *plan, te_quant_ki
 TE_API int te_kernel_plan_optimizes_quant(const te_kernel_plan *plan, te_quant_kind quant);
 TE_API int te_kernel_plan_supports_op(const te_kernel_plan *plan, te_vector_op op);
 
-/* Model / tokenizer entry points: reference tinyengine.h:219-281.  Outside
- * the attention step; every one returns TE_STATUS_UNSUPPORTED here after the
- * reference's own argument checks. */
+/* Model / tokenizer entry points: reference tinyengine.h:219-281, with the
+ * reference's argument checks and statuses (gguf.c:147-1093,
+ * tokenizer.c:52-707, ops.c:88-269).  te_model_load_gguf parses GGUF v2 / v3
+ * from a memory mapping; the info, tensor-read, chat-template, tokenize and
+ * detokenize calls are host work.  te_model_dequantize_row_f32 and
+ * te_model_matvec_f32 run on the GPU for F32 / Q4_0 / Q8_0 tensors (other
+ * types, or no device: UNSUPPORTED). */
 TE_API te_status te_model_load_gguf(const char *path, const te_runtime_options *options, te_model **out_model);
 TE_API te_status te_model_get_info(const te_model *model, te_model_info *out_info);
 TE_API te_status te_model_get_tokenizer_info(const te_model *model, te_tokenizer_info *out_info);
@@ -262,8 +269,11 @@ TE_API te_status te_model_matvec_f32(const te_model *model, const char *name, co
                                      size_t input_len, float *out, size_t out_capacity, size_t *out_written);
 TE_API void te_model_free(te_model *model);
 
-/* Element-wise ops outside the attention step: reference tinyengine.h:283-289,
- * :307-309.  Exported for symbol parity; return TE_STATUS_UNSUPPORTED. */
+/* Element-wise ops of the decode layer: reference tinyengine.h:283-289,
+ * :307-309 (ops.c:272-293, :397-433), same argument checks.  They run on the
+ * GPU (host pointers in and out, synchronous, serialized by the process-wide
+ * mutex): RMSNorm sums squares in fp64 like the reference, add and argmax are
+ * exact, SwiGLU uses the device expf.  UNSUPPORTED without a device. */
 TE_API te_status te_rmsnorm_f32(const float *input, const float *weight, size_t len, float epsilon, float *out);
 TE_API te_status te_swiglu_f32(const float *gate, const float *up, size_t len, float *out);
 TE_API te_status te_add_f32(const float *lhs, const float *rhs, size_t len, float *out);
@@ -292,10 +302,15 @@ TE_API te_status te_attention_decode_f32(const float *query, const float *key_ca
                                          size_t position, size_t heads, size_t kv_heads, size_t head_dim,
                                          float *out);
 
-/* Context and generation: reference tinyengine.h:311-332 (tinyengine.c:374-440).
- * te_generate keeps the reference stub mode (TINYENGINE_GENERATION=stub); full
- * generation needs the GGUF/tokenizer/projection stack and returns
- * TE_STATUS_UNSUPPORTED. */
+/* Context and generation: reference tinyengine.h:311-332 (tinyengine.c:374-440,
+ * qwen.c:261-412).  te_generate / te_generate_raw tokenize, prefill the prompt
+ * and decode every token on the GPU with the KV cache in HBM, greedy or top-k
+ * temperature sampling with the reference's TINYENGINE_* variables, and call
+ * back once per emitted token.  A context keeps its cache between calls and
+ * reruns only the tokens after the longest shared prefix.  The reference stub
+ * mode (TINYENGINE_GENERATION=stub) is kept.  UNSUPPORTED without a device,
+ * for models this build does not run (non-Qwen2 shapes, other tensor types),
+ * and for contexts past the kernels' limits. */
 TE_API te_status te_context_create(te_model *model, const te_runtime_options *options, te_context **out_context);
 TE_API void te_context_free(te_context *context);
 TE_API te_status te_generate(te_context *context, const char *prompt, uint32_t max_tokens,

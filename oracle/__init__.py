@@ -54,7 +54,10 @@ def lib() -> ctypes.CDLL:
     global _oracle
     if _oracle is None:
         if not ORACLE_LIB.is_file():
-            build(with_reference=False)
+            # Never compiled on demand: a test process may already hold the
+            # GPU, and the GPU box only runs what was built beforehand.
+            raise RuntimeError(f"{ORACLE_LIB} is missing: build it first (__graft_entry__.build() or "
+                               f"`make -C {HERE}`)")
         l = ctypes.CDLL(str(ORACLE_LIB))
         l.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
         l.orc_f16_to_f32.restype = ctypes.c_float

@@ -192,6 +192,57 @@ def test_workspace_query(lib):
     assert lib.te_hip_attention_decode_workspace_bytes(pos, 0, 3, 2, 28, 4, 128) > 0
 
 
+def _chunking(lib, position, layers, kv_heads, fp32=0, positions=None):
+    chunk, chunks = ctypes.c_size_t(), ctypes.c_size_t()
+    seqs = 1 if positions is None else len(positions)
+    arr = None if positions is None else (ctypes.c_size_t * seqs)(*positions)
+    st = lib.te_hip_attention_decode_chunking(arr, ctypes.c_size_t(position), seqs, layers, kv_heads, fp32,
+                                              ctypes.byref(chunk), ctypes.byref(chunks))
+    assert st == 0
+    return chunk.value, chunks.value
+
+
+def test_decode_workspace_sized_at_the_last_position_serves_every_earlier_one(lib):
+    """A caller sizes the decode workspace once, at context_tokens - 1 (the
+    engine's context does), then decodes every position below it.  The launch
+    needs seqs*layers*heads*chunks(p)*(head_dim+2)*4 bytes, and the chunk
+    count is not monotone in p, so the size query must bound every p below."""
+    lib.te_hip_attention_decode_workspace_bytes.restype = ctypes.c_size_t
+    for layers, heads, kv, ctx in ((1, 16, 2, 131072), (1, 28, 4, 32768), (36, 16, 2, 32768),
+                                   (28, 12, 2, 131072), (1, 14, 2, 4096)):
+        have = lib.te_hip_attention_decode_workspace_bytes(None, ctypes.c_size_t(ctx - 1), 1, layers, heads, kv, 128)
+        step = 1 if ctx <= 32768 else 7
+        worst = 0
+        for p in range(0, ctx, step):
+            chunk, chunks = _chunking(lib, p, layers, kv)
+            assert chunk % 32 == 0 and chunks * chunk >= p + 1 and (chunks - 1) * chunk < p + 1
+            worst = max(worst, layers * heads * chunks * (128 + 2) * 4)
+        assert worst <= have, (layers, heads, kv, ctx, worst, have)
+    # the case that failed before: 1 layer, 2 KV heads, position 28608 against ctx 32768
+    _, c_small = _chunking(lib, 28608, 1, 2)
+    _, c_last = _chunking(lib, 32767, 1, 2)
+    assert c_small > c_last
+    have = lib.te_hip_attention_decode_workspace_bytes(None, ctypes.c_size_t(32767), 1, 1, 16, 2, 128)
+    assert 16 * c_small * 130 * 4 <= have
+    # ragged batches: sized at the largest position
+    positions = [3924, 1976, 11519, 12470, 1263, 4276, 3298, 9268]
+    _, chunks = _chunking(lib, 0, 28, 4, positions=positions)
+    arr = (ctypes.c_size_t * 8)(*positions)
+    assert 8 * 28 * 28 * chunks * 130 * 4 <= lib.te_hip_attention_decode_workspace_bytes(arr, 0, 8, 28, 28, 4, 128)
+
+
+def test_fp32_decode_chunking_fits_the_combine_at_any_position(lib):
+    """te_attention_decode_f32 accepts positions up to 2^30; its chunks must
+    stay within the 4096 per-chunk weights the combine kernel keeps in LDS."""
+    for p in [0, 1, 511, 512, 4096 * 512 - 1, 4096 * 512, 4096 * 512 + 1, 3_000_000, 2 ** 24 + 5,
+              2 ** 30 - 1, 2 ** 30]:
+        chunk, chunks = _chunking(lib, p, 1, 1, fp32=1)
+        assert chunk % 512 == 0 and (chunk // 512) & (chunk // 512 - 1) == 0
+        assert chunks <= 4096 and chunks * chunk >= p + 1 and (chunks - 1) * chunk < p + 1
+    assert _chunking(lib, 4096 * 512 - 1, 1, 1, fp32=1) == (512, 4096)
+    assert _chunking(lib, 4096 * 512, 1, 1, fp32=1) == (1024, 2049)
+
+
 def test_model_and_generate_argument_statuses():
     """Missing file -> IO_ERROR (tinyengine.c:278-280), the "unsupported"
     text the agent layer matches, NULL handles -> INVALID_ARGUMENT."""

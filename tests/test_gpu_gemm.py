@@ -27,10 +27,13 @@ def _dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
 
 
-def _run(oracle_mod, ggml_type, rows, n, k, pre=0, resid=False, seed=3, scale=1.0, split_bytes=0):
+def _run(oracle_mod, ggml_type, rows, n, k, pre=0, resid=False, seed=3, scale=1.0, split_bytes=0, clip=None):
     lib = R.load_library()
     w = S.ggml_tensor(seed, f"gw{ggml_type}{n}{k}", ggml_type, n, k, scale=0.05)
-    x = S.normal(seed, "gx", (rows, k)) * scale
+    x = S.normal(seed, "gx", (rows, k))
+    if clip is not None:
+        x = np.clip(x, -clip, clip)
+    x = (x.astype(np.float64) * scale).astype(np.float32)
     x2 = S.normal(seed, "gx2", (rows, k))
     nw = S.normal(seed, "gnw", (k,), 0.1) + 1.0
     r = S.normal(seed, "gr", (rows, n))
@@ -92,6 +95,9 @@ def test_gemm_input_ranges(oracle_mod):
     lib = R.load_library()
     for scale in (1e-30, 1e-3, 1e30):
         _run(oracle_mod, 2, 40, 64, 256, scale=scale)
+    # finite blocks whose largest magnitude is in (3e38, FLT_MAX]: finite scale 2^114
+    got = _run(oracle_mod, 2, 2, 40, 64, scale=3.3e38, clip=1.0)
+    assert np.isfinite(got).all()
 
 
 def test_gemm_argument_checks():

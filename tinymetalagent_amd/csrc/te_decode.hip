@@ -40,7 +40,10 @@
 #include "te_hip_common.h"
 
 #include <math.h>
+#include <stdint.h>
 #include <stdlib.h>
+
+#include <algorithm>
 
 namespace {
 
@@ -525,58 +528,72 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
 }
 
 // fp32-cache decode for te_attention_decode_f32 (host-pointer API, any head_dim):
-// one wave per (chunk of 64*8 positions, head); scores in LDS, two-pass softmax
-// within the chunk, partial written for decode_combine_kernel.
-constexpr int kF32Chunk = 512;
+// one wave per (chunk of positions, head).  The chunk is walked in blocks of
+// kF32Block positions whose scores sit in LDS; each block is a two-pass
+// softmax merged online into the partial (m, l, o), where o lives in the
+// partial itself (each lane owns dims lane, lane + 64, ...).  The partial is
+// then merged by decode_combine_kernel.
+constexpr int kF32Block = 512;
 
 __global__ __launch_bounds__(64) void decode_f32_chunk_kernel(const float *query, const float *key_cache,
                                                               const float *value_cache, int pos, int heads,
-                                                              int kv_heads, int head_dim, float qscale,
+                                                              int kv_heads, int head_dim, float qscale, int chunk,
                                                               int max_chunks, float *part_o, float *part_ml) {
     const int chunk_id = blockIdx.x;
     const int h = blockIdx.y;
     const int lane = threadIdx.x;
-    const int c0 = chunk_id * kF32Chunk;
-    const int c1 = min(c0 + kF32Chunk, pos + 1);
+    const int c0 = chunk_id * chunk;
+    const int c1 = min(c0 + chunk, pos + 1);
     const int kvh = h / (heads / kv_heads);
     const float *q = query + (size_t)h * head_dim;
-    __shared__ float sc[kF32Chunk];
-
-    float mx = -INFINITY;
-    for (int p = c0 + lane; p < c1; p += 64) {
-        const float *kr = key_cache + ((size_t)p * kv_heads + kvh) * head_dim;
-        float dot = 0.0f;
-        for (int i = 0; i < head_dim; ++i) {
-            dot = fmaf(q[i], kr[i], dot);
-        }
-        const float x = dot * qscale;
-        sc[p - c0] = x;
-        mx = fmaxf(mx, x);
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    }
-    float ls = 0.0f;
-    for (int p = c0 + lane; p < c1; p += 64) {
-        const float e = fast_exp2(sc[p - c0] - mx);
-        sc[p - c0] = e;
-        ls += e;
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        ls += __shfl_xor(ls, off, 64);
-    }
-    __syncthreads();
     const size_t pidx = (size_t)h * max_chunks + chunk_id;
-    for (int d = lane; d < head_dim; d += 64) {
-        float acc = 0.0f;
-        for (int p = c0; p < c1; ++p) {
-            acc = fmaf(sc[p - c0], value_cache[((size_t)p * kv_heads + kvh) * head_dim + d], acc);
+    float *po = part_o + pidx * head_dim;
+    __shared__ float sc[kF32Block];
+
+    float m = -INFINITY;
+    float l = 0.0f;
+    for (int b0 = c0; b0 < c1; b0 += kF32Block) {
+        const int b1 = min(b0 + kF32Block, c1);
+        float mx = -INFINITY;
+        for (int p = b0 + lane; p < b1; p += 64) {
+            const float *kr = key_cache + ((size_t)p * kv_heads + kvh) * head_dim;
+            float dot = 0.0f;
+            for (int i = 0; i < head_dim; ++i) {
+                dot = fmaf(q[i], kr[i], dot);
+            }
+            const float x = dot * qscale;
+            sc[p - b0] = x;
+            mx = fmaxf(mx, x);
         }
-        part_o[pidx * head_dim + d] = acc;
+        for (int off = 32; off > 0; off >>= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        }
+        const float mn = fmaxf(m, mx);
+        const float alpha = m == mn ? 1.0f : fast_exp2(m - mn);  // first block: o and l are still 0
+        float ls = 0.0f;
+        for (int p = b0 + lane; p < b1; p += 64) {
+            const float e = fast_exp2(sc[p - b0] - mn);
+            sc[p - b0] = e;
+            ls += e;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            ls += __shfl_xor(ls, off, 64);
+        }
+        l = l * alpha + ls;
+        m = mn;
+        __syncthreads();
+        for (int d = lane; d < head_dim; d += 64) {
+            float acc = b0 == c0 ? 0.0f : po[d] * alpha;
+            for (int p = b0; p < b1; ++p) {
+                acc = fmaf(sc[p - b0], value_cache[((size_t)p * kv_heads + kvh) * head_dim + d], acc);
+            }
+            po[d] = acc;
+        }
+        __syncthreads();  // the next block's scores overwrite sc
     }
     if (lane == 0) {
-        part_ml[pidx * 2] = mx;
-        part_ml[pidx * 2 + 1] = ls;
+        part_ml[pidx * 2] = m;
+        part_ml[pidx * 2 + 1] = l;
     }
 }
 
@@ -683,13 +700,47 @@ size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layer
     return parts * head_dim * sizeof(float) + parts * 2 * sizeof(float);
 }
 
+size_t decode_chunks_bound(size_t max_position, size_t layers, size_t kv_heads) {
+    // decode_geometry gives the longest stream n_longest = ceil(M / t0) chunks,
+    // M = its 32-position tiles, t0 = max(2, ceil(T / target)) and T >= layers *
+    // kv_heads * M the total tiles; the later steps only lengthen the chunk.  So
+    // n_longest <= ceil(M / 2) and n_longest <= ceil(target / (layers * kv_heads)),
+    // both non-decreasing in M.  With TE_HIP_DECODE_CHUNK the count is
+    // ceil(n / chunk) before the doubling that keeps it <= kMaxCombineChunks.
+    const size_t max_n = max_position + 1;
+    const size_t m_tiles = (max_n + kTile - 1) / kTile;
+    const char *env = getenv("TE_HIP_DECODE_CHUNK");
+    if (env != nullptr) {
+        const long v = strtol(env, nullptr, 10);
+        if (v >= kTile && v % kTile == 0 && v <= (1 << 24)) {
+            return std::min((max_n + (size_t)v - 1) / (size_t)v, (size_t)kMaxCombineChunks);
+        }
+    }
+    const size_t target = (size_t)device_compute_units() * kTargetWaves2PerCU / 2;
+    const size_t streams = layers * kv_heads;
+    const size_t b = std::min((m_tiles + 1) / 2, (target + streams - 1) / streams);
+    return std::min(std::max(b, (size_t)1), (size_t)kMaxCombineChunks);
+}
+
+int f32_decode_chunk(size_t position) {
+    // Positions per workgroup of te_attention_decode_f32: kF32Block, doubled
+    // until the chunks fit the combine kernel's weight cache.
+    const size_t n = position + 1;
+    size_t chunk = kF32Block;
+    while ((n + chunk - 1) / chunk > (size_t)kMaxCombineChunks) {
+        chunk *= 2;
+    }
+    return (int)chunk;
+}
+
 te_status launch_decode_f32(const float *query, const float *key_cache, const float *value_cache,
                             size_t position, size_t heads, size_t kv_heads, size_t head_dim, float *out,
                             float *part_o, float *part_ml, hipStream_t stream) {
-    const int max_chunks = (int)((position + 1 + kF32Chunk - 1) / kF32Chunk);
+    const int chunk = f32_decode_chunk(position);
+    const int max_chunks = (int)((position + (size_t)chunk) / (size_t)chunk);
     const float qscale = TE_LOG2E / sqrtf((float)head_dim);
     decode_f32_chunk_kernel<<<dim3(max_chunks, (unsigned)heads), 64, 0, stream>>>(
-        query, key_cache, value_cache, (int)position, (int)heads, (int)kv_heads, (int)head_dim, qscale,
+        query, key_cache, value_cache, (int)position, (int)heads, (int)kv_heads, (int)head_dim, qscale, chunk,
         max_chunks, part_o, part_ml);
     te_status st = launch_status();
     if (st != TE_STATUS_OK) {
@@ -702,7 +753,7 @@ te_status launch_decode_f32(const float *query, const float *key_cache, const fl
     c.layers = 1;
     c.heads = (int)heads;
     c.head_dim = (int)head_dim;
-    c.chunk = kF32Chunk;
+    c.chunk = chunk;
     c.max_chunks = max_chunks;
     c.positions[0] = (int)position;
     decode_combine_kernel<<<dim3((unsigned)heads, 1), 256, 0, stream>>>(c);
@@ -717,8 +768,41 @@ extern "C" size_t te_hip_attention_decode_workspace_bytes(const size_t *position
     if (seqs == 0 || seqs > TE_HIP_MAX_SEQS || layers == 0 || heads == 0 || kv_heads == 0 || head_dim == 0) {
         return 0;
     }
-    const te_hip::DecodeGeometry g = te_hip::decode_geometry(positions, position, seqs, layers, kv_heads);
+    // Sized by the chunk bound of the largest position, not by the chunking
+    // of these exact positions: the bound never decreases with the position,
+    // so a workspace sized for one position serves every smaller one.
+    size_t max_position = 0;
+    for (size_t s = 0; s < seqs; ++s) {
+        const size_t p = positions != nullptr ? positions[s] : position;
+        max_position = p > max_position ? p : max_position;
+    }
+    te_hip::DecodeGeometry g;
+    g.chunk = 0;
+    g.max_chunks = (int)te_hip::decode_chunks_bound(max_position, layers, kv_heads);
     return te_hip::decode_workspace_bytes(g, seqs, layers, heads, head_dim);
+}
+
+extern "C" te_status te_hip_attention_decode_chunking(const size_t *positions, size_t position, size_t seqs,
+                                                      size_t layers, size_t kv_heads, int fp32_cache,
+                                                      size_t *chunk, size_t *chunks) {
+    if (chunk == nullptr || chunks == nullptr || seqs == 0 || layers == 0 || kv_heads == 0) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (fp32_cache != 0) {
+        if (seqs != 1 || layers != 1 || position == SIZE_MAX) {
+            return TE_STATUS_INVALID_ARGUMENT;
+        }
+        *chunk = (size_t)te_hip::f32_decode_chunk(position);
+        *chunks = (position + *chunk) / *chunk;
+        return TE_STATUS_OK;
+    }
+    if (seqs > TE_HIP_MAX_SEQS) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    const te_hip::DecodeGeometry g = te_hip::decode_geometry(positions, position, seqs, layers, kv_heads);
+    *chunk = (size_t)g.chunk;
+    *chunks = (size_t)g.max_chunks;
+    return TE_STATUS_OK;
 }
 
 namespace {

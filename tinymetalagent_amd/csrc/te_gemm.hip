@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__r
         }
         int q = 0;
         float s;
-        if (!(m <= 3.0e38f)) {  // inf or NaN in the block: its products are NaN
+        if (!(m <= FLT_MAX)) {  // inf or NaN in the block: its products are NaN
             s = __builtin_nanf("");
         } else if (m == 0.0f) {
             s = 0.0f;

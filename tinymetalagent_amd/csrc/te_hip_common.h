@@ -136,6 +136,14 @@ DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t 
 
 size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layers, size_t heads, size_t head_dim);
 
+// Upper bound on decode_geometry(...).max_chunks over every set of positions
+// whose largest is <= max_position; non-decreasing in max_position.
+size_t decode_chunks_bound(size_t max_position, size_t layers, size_t kv_heads);
+
+// Chunk length of the fp32-cache decode (te_attention_decode_f32): a power-of-two
+// multiple of 512 positions giving at most 4096 chunks.
+int f32_decode_chunk(size_t position);
+
 // Internal launchers used by the host-pointer wrappers (te_hip_runtime.hip).
 te_status launch_decode_f32(const float *query, const float *key_cache, const float *value_cache,
                             size_t position, size_t heads, size_t kv_heads, size_t head_dim, float *out,

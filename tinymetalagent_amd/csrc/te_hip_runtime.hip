@@ -366,7 +366,8 @@ extern "C" te_status te_attention_decode_f32(const float *query, const float *ke
         heads > 65535 || head_dim > 65535) {
         return TE_STATUS_UNSUPPORTED;
     }
-    const size_t chunks = (n + 511) / 512;
+    const size_t chunk = (size_t)te_hip::f32_decode_chunk(position);
+    const size_t chunks = (n + chunk - 1) / chunk;
     std::lock_guard<std::mutex> lock(g_mutex);
     if (!probe_locked()) {
         return TE_STATUS_UNSUPPORTED;

@@ -1,8 +1,12 @@
-"""GGUF models, the tokenizer and generation over libtinyengine.so: the
-`Model` class and `format_qwen_chat_prompt` of the reference binding
-(python/tinyengine/runtime.py:133-243 for the info types, :438-693 for the
-calls), with the same struct layouts (tinyengine.h:100-198), retry-on-short-
-buffer behaviour and errors (TinyEngineError(te_strerror(status))).
+"""GGUF models, the tokenizer and generation over libtinyengine.so.
+
+The public surface is the reference binding's (python/tinyengine/runtime.py:
+133-243 for the info types, :438-693 for the calls): the same class and
+method names and signatures, the same struct layouts (tinyengine.h:100-198),
+and errors raised as TinyEngineError(te_strerror(status)).  Every call that
+fills a caller buffer goes through one grow-and-retry helper (_sized_call),
+and generation runs through a context object that owns the te_context and the
+callback (_Context).
 
 Loading, tensor info and the tokenizer are host code; dequantize_row, matvec
 and generate run on the GPU and raise where none is present.
@@ -10,6 +14,7 @@ and generate run on the GPU and raise where none is present.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import os
 from dataclasses import dataclass
 from typing import Callable, Optional
@@ -151,210 +156,226 @@ class TokenizerInfo:
     add_bos_token: bool
 
 
+class _Handle:
+    """Owner of one library handle: close() releases it once; usable as a
+    context manager, and released at garbage collection."""
+
+    _handle_attr = "_handle"
+
+    def _release(self, handle) -> None:  # pragma: no cover - overridden
+        raise NotImplementedError
+
+    def close(self) -> None:
+        handle = self.__dict__.get(self._handle_attr)
+        if handle:
+            self.__dict__[self._handle_attr] = None
+            self._release(handle)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *_exc) -> None:
+        self.close()
+
+    def __del__(self) -> None:
+        self.close()
+
+
+def _sized_call(call, alloc, capacity: int, slack: int):
+    """Run call(buffer, capacity, written) into alloc(capacity).  The library
+    reports a short buffer as INVALID_ARGUMENT with `written` set to the
+    length the result needs; `slack` extra elements hold a terminator.  The
+    buffer then grows to fit and the call runs again.  Returns (buffer,
+    written)."""
+    written = ctypes.c_size_t()
+    while True:
+        buffer = alloc(capacity)
+        status = call(buffer, capacity, ctypes.byref(written))
+        needed = written.value + slack
+        if status == TE_STATUS_INVALID_ARGUMENT and needed > capacity:
+            capacity = needed
+            continue
+        check(status)
+        return buffer, written.value
+
+
 def format_qwen_chat_prompt(prompt: str) -> str:
     lib = load_library()
     data = prompt.encode()
-    capacity = len(data) + 64
-    while True:
-        out = ctypes.create_string_buffer(capacity)
-        written = ctypes.c_size_t()
-        status = lib.te_format_qwen_chat_prompt(data, out, capacity, ctypes.byref(written))
-        if status == 0:
-            return out.value.decode()
-        if status == TE_STATUS_INVALID_ARGUMENT and written.value + 1 > capacity:
-            capacity = written.value + 1
-            continue
-        check(status)
+    buffer, n = _sized_call(lambda buf, cap, w: lib.te_format_qwen_chat_prompt(data, buf, cap, w),
+                            ctypes.create_string_buffer, len(data) + 128, 1)
+    return buffer.raw[:n].decode()
 
 
-class Model:
+class _TextSink:
+    """Collects the text te_generate* hands to its callback and forwards each
+    piece to an optional Python callable; owns the ctypes callback object for
+    the duration of one call."""
+
+    def __init__(self, on_token: Optional[Callable[[str, int], None]]):
+        self.pieces: list[str] = []
+        self._on_token = on_token
+        self.c_callback = _TOKEN_CALLBACK(self._receive)
+
+    def _receive(self, text: bytes, token_id: int, _userdata) -> None:
+        piece = (text or b"").decode("utf-8", "replace")
+        self.pieces.append(piece)
+        if self._on_token is not None:
+            self._on_token(piece, token_id)
+
+    def text(self) -> str:
+        return "".join(self.pieces)
+
+
+class _Context(_Handle):
+    """One te_context: generation state (the KV cache in HBM) of a model."""
+
+    def __init__(self, model: "Model"):
+        self._lib = model._lib
+        handle = ctypes.c_void_p()
+        options = model._options._to_c()
+        check(self._lib.te_context_create(model.handle, ctypes.byref(options), ctypes.byref(handle)))
+        self._handle = handle
+
+    def _release(self, handle) -> None:
+        self._lib.te_context_free(handle)
+
+    def run(self, raw: bool, prompt: str, max_tokens: int, on_token) -> str:
+        fn = self._lib.te_generate_raw if raw else self._lib.te_generate
+        sink = _TextSink(on_token)
+        check(fn(self._handle, prompt.encode(), max_tokens, sink.c_callback, None))
+        return sink.text()
+
+
+class Model(_Handle):
     """A loaded GGUF file (te_model_load_gguf)."""
+
+    _handle_attr = "_model"
 
     def __init__(self, gguf_path, options: RuntimeOptions = RuntimeOptions()):
         self._lib = load_library()
         self._options = options
+        self._model = None
+        handle = ctypes.c_void_p()
         raw = options._to_c()
-        self._model = ctypes.c_void_p()
-        check(self._lib.te_model_load_gguf(os.fsencode(gguf_path), ctypes.byref(raw), ctypes.byref(self._model)))
+        check(self._lib.te_model_load_gguf(os.fsencode(gguf_path), ctypes.byref(raw), ctypes.byref(handle)))
+        self._model = handle
+
+    def _release(self, handle) -> None:
+        self._lib.te_model_free(handle)
 
     @property
     def handle(self) -> ctypes.c_void_p:
         return self._model
 
+    def _query(self, fn, struct_type, *args):
+        out = struct_type()
+        check(fn(self._model, *args, ctypes.byref(out)))
+        return out
+
     def info(self) -> ModelInfo:
-        r = _ModelInfo()
-        check(self._lib.te_model_get_info(self._model, ctypes.byref(r)))
-        return ModelInfo(r.gguf_version, r.metadata_kv_count, r.tensor_count, r.tensor_data_offset,
-                         r.tensor_data_bytes, r.parameter_count, r.file_size_bytes, _text(r.name),
-                         _text(r.architecture), r.context_length, r.embedding_length, r.block_count,
-                         r.feed_forward_length, r.attention_head_count, r.attention_head_count_kv, r.head_dim,
-                         r.vocab_size, float(r.rms_norm_epsilon), float(r.rope_freq_base),
-                         tuple(r.quant_tensor_counts))
+        r = self._query(self._lib.te_model_get_info, _ModelInfo)
+        fields = {f.name: getattr(r, f.name) for f in dataclasses.fields(ModelInfo)}
+        fields.update(name=_text(r.name), architecture=_text(r.architecture),
+                      rms_norm_epsilon=float(r.rms_norm_epsilon), rope_freq_base=float(r.rope_freq_base),
+                      quant_tensor_counts=tuple(r.quant_tensor_counts))
+        return ModelInfo(**fields)
 
     def tensor_info(self, name: str) -> TensorInfo:
-        r = _TensorInfo()
-        check(self._lib.te_model_get_tensor_info(self._model, name.encode(), ctypes.byref(r)))
-        return TensorInfo(_text(r.name), r.quant, r.ggml_type, tuple(r.dims[:r.n_dims]), r.elements, r.bytes,
-                          r.relative_offset, r.absolute_offset)
+        r = self._query(self._lib.te_model_get_tensor_info, _TensorInfo, name.encode())
+        fields = {f.name: getattr(r, f.name) for f in dataclasses.fields(TensorInfo) if f.name not in ("name", "dims")}
+        return TensorInfo(name=_text(r.name), dims=tuple(r.dims[:r.n_dims]), **fields)
 
     def tokenizer_info(self) -> TokenizerInfo:
-        r = _TokenizerInfo()
-        check(self._lib.te_model_get_tokenizer_info(self._model, ctypes.byref(r)))
-        return TokenizerInfo(_text(r.model), _text(r.pre), r.token_count, r.token_type_count, r.merge_count,
-                             r.bos_token_id, r.eos_token_id, r.padding_token_id, bool(r.add_bos_token))
+        r = self._query(self._lib.te_model_get_tokenizer_info, _TokenizerInfo)
+        fields = {f.name: getattr(r, f.name) for f in dataclasses.fields(TokenizerInfo)}
+        fields.update(model=_text(r.model), pre=_text(r.pre), add_bos_token=bool(r.add_bos_token))
+        return TokenizerInfo(**fields)
 
     def tokenize(self, text, parse_special: bool = True) -> list[int]:
         data = text.encode() if isinstance(text, str) else bytes(text)
-        capacity = max(len(data) + 16, 16)
-        while True:
-            out = (ctypes.c_uint32 * capacity)()
-            written = ctypes.c_size_t()
-            status = self._lib.te_model_tokenize(self._model, data, int(parse_special), out, capacity,
-                                                 ctypes.byref(written))
-            if status == 0:
-                return list(out[:written.value])
-            if status == TE_STATUS_INVALID_ARGUMENT and written.value > capacity:
-                capacity = written.value
-                continue
-            check(status)
+        # byte-level BPE: at most one token per byte, plus a BOS token
+        buffer, n = _sized_call(
+            lambda buf, cap, w: self._lib.te_model_tokenize(self._model, data, int(parse_special), buf, cap, w),
+            lambda cap: (ctypes.c_uint32 * cap)(), len(data) + 2, 0)
+        return list(buffer[:n])
 
     def detokenize_bytes(self, tokens, skip_special: bool = True) -> bytes:
-        ids = (ctypes.c_uint32 * max(len(tokens), 1))(*tokens)
-        capacity = max(len(tokens) * 16 + 16, 16)
-        while True:
-            out = ctypes.create_string_buffer(capacity)
-            written = ctypes.c_size_t()
-            status = self._lib.te_model_detokenize(self._model, ids, len(tokens), int(skip_special), out, capacity,
-                                                   ctypes.byref(written))
-            if status == 0:
-                return out.raw[:written.value]
-            if status == TE_STATUS_INVALID_ARGUMENT and written.value + 1 > capacity:
-                capacity = written.value + 1
-                continue
-            check(status)
+        ids = list(tokens)
+        arr = (ctypes.c_uint32 * max(len(ids), 1))(*ids)
+        buffer, n = _sized_call(
+            lambda buf, cap, w: self._lib.te_model_detokenize(self._model, arr, len(ids), int(skip_special), buf,
+                                                              cap, w),
+            ctypes.create_string_buffer, 8 * len(ids) + 64, 1)
+        return buffer.raw[:n]
 
     def detokenize(self, tokens, skip_special: bool = True) -> str:
         return self.detokenize_bytes(tokens, skip_special).decode()
 
     def read_f32_tensor(self, name: str) -> list[float]:
-        info = self.tensor_info(name)
-        values = (ctypes.c_float * max(info.elements, 1))()
-        written = ctypes.c_size_t()
-        check(self._lib.te_model_read_f32_tensor(self._model, name.encode(), values, info.elements,
-                                                 ctypes.byref(written)))
-        return list(values[:written.value])
+        count = self.tensor_info(name).elements
+        buffer, n = _sized_call(
+            lambda buf, cap, w: self._lib.te_model_read_f32_tensor(self._model, name.encode(), buf, cap, w),
+            lambda cap: (ctypes.c_float * max(cap, 1))(), count, 0)
+        return list(buffer[:n])
+
+    def _matrix_dims(self, name: str) -> tuple[int, int]:
+        dims = self.tensor_info(name).dims
+        if len(dims) != 2:
+            raise TinyEngineError(f"tensor {name!r} has {len(dims)} dimensions; this call takes a matrix")
+        return dims[0], dims[1]
 
     def dequantize_row(self, name: str, row_index: int) -> list[float]:
-        info = self.tensor_info(name)
-        if len(info.dims) != 2:
-            raise TinyEngineError(f"{name} is not rank-2")
-        cols = info.dims[0]
-        values = (ctypes.c_float * cols)()
-        written = ctypes.c_size_t()
-        check(self._lib.te_model_dequantize_row_f32(self._model, name.encode(), row_index, values, cols,
-                                                    ctypes.byref(written)))
-        return list(values[:written.value])
+        cols, _rows = self._matrix_dims(name)
+        buffer, n = _sized_call(
+            lambda buf, cap, w: self._lib.te_model_dequantize_row_f32(self._model, name.encode(), row_index, buf,
+                                                                      cap, w),
+            lambda cap: (ctypes.c_float * max(cap, 1))(), cols, 0)
+        return list(buffer[:n])
 
     def matvec(self, name: str, input_values) -> list[float]:
-        info = self.tensor_info(name)
-        if len(info.dims) != 2:
-            raise TinyEngineError(f"{name} is not rank-2")
-        x = (ctypes.c_float * max(len(input_values), 1))(*input_values)
-        rows = info.dims[1]
-        out = (ctypes.c_float * rows)()
-        written = ctypes.c_size_t()
-        check(self._lib.te_model_matvec_f32(self._model, name.encode(), x, len(input_values), out, rows,
-                                            ctypes.byref(written)))
-        return list(out[:written.value])
+        _cols, rows = self._matrix_dims(name)
+        values = list(input_values)
+        x = (ctypes.c_float * max(len(values), 1))(*values)
+        buffer, n = _sized_call(
+            lambda buf, cap, w: self._lib.te_model_matvec_f32(self._model, name.encode(), x, len(values), buf,
+                                                              cap, w),
+            lambda cap: (ctypes.c_float * max(cap, 1))(), rows, 0)
+        return list(buffer[:n])
 
     def generate(self, prompt: str, max_tokens: int = 16,
                  on_token: Optional[Callable[[str, int], None]] = None) -> str:
-        return self._run_generate(self._lib.te_generate, prompt, max_tokens, on_token)
+        """Chat-templated generation in a fresh context."""
+        with _Context(self) as ctx:
+            return ctx.run(False, prompt, max_tokens, on_token)
 
     def generate_raw(self, prompt: str, max_tokens: int = 256,
                      on_token: Optional[Callable[[str, int], None]] = None) -> str:
         """The prompt verbatim (special tokens parsed), no chat template."""
-        return self._run_generate(self._lib.te_generate_raw, prompt, max_tokens, on_token)
-
-    def _run_generate(self, fn, prompt: str, max_tokens: int, on_token) -> str:
-        raw = self._options._to_c()
-        context = ctypes.c_void_p()
-        check(self._lib.te_context_create(self._model, ctypes.byref(raw), ctypes.byref(context)))
-        chunks: list[str] = []
-
-        def callback(text: bytes, token_id: int, _userdata) -> None:
-            chunk = text.decode(errors="replace")
-            chunks.append(chunk)
-            if on_token is not None:
-                on_token(chunk, token_id)
-
-        c_callback = _TOKEN_CALLBACK(callback)
-        try:
-            check(fn(context, prompt.encode(), max_tokens, c_callback, None))
-        finally:
-            self._lib.te_context_free(context)
-        return "".join(chunks)
+        with _Context(self) as ctx:
+            return ctx.run(True, prompt, max_tokens, on_token)
 
     def session(self) -> "Session":
         """A context kept across calls: each call reuses the K / V of the
         leading tokens it shares with the previous call's sequence."""
         return Session(self)
 
-    def close(self) -> None:
-        if getattr(self, "_model", None):
-            self._lib.te_model_free(self._model)
-            self._model = None
 
-    def __enter__(self) -> "Model":
-        return self
-
-    def __exit__(self, *_exc) -> None:
-        self.close()
-
-    def __del__(self) -> None:
-        self.close()
-
-
-class Session:
+class Session(_Handle):
     """One te_context over a Model, kept open between generate calls (this
     build's addition: the reference binding makes a context per call)."""
 
+    _handle_attr = "_context"
+
     def __init__(self, model: Model):
         self._model = model
-        self._lib = model._lib
-        raw = model._options._to_c()
-        self._ctx = ctypes.c_void_p()
-        check(self._lib.te_context_create(model.handle, ctypes.byref(raw), ctypes.byref(self._ctx)))
+        self._context = _Context(model)
 
-    def _run(self, fn, prompt: str, max_tokens: int, on_token) -> str:
-        chunks: list[str] = []
-
-        def callback(text: bytes, token_id: int, _userdata) -> None:
-            chunk = text.decode(errors="replace")
-            chunks.append(chunk)
-            if on_token is not None:
-                on_token(chunk, token_id)
-
-        c_callback = _TOKEN_CALLBACK(callback)
-        check(fn(self._ctx, prompt.encode(), max_tokens, c_callback, None))
-        return "".join(chunks)
+    def _release(self, context: _Context) -> None:
+        context.close()
 
     def generate(self, prompt: str, max_tokens: int = 16, on_token=None) -> str:
-        return self._run(self._lib.te_generate, prompt, max_tokens, on_token)
+        return self._context.run(False, prompt, max_tokens, on_token)
 
     def generate_raw(self, prompt: str, max_tokens: int = 256, on_token=None) -> str:
-        return self._run(self._lib.te_generate_raw, prompt, max_tokens, on_token)
-
-    def close(self) -> None:
-        if getattr(self, "_ctx", None):
-            self._lib.te_context_free(self._ctx)
-            self._ctx = None
-
-    def __enter__(self) -> "Session":
-        return self
-
-    def __exit__(self, *_exc) -> None:
-        self.close()
-
-    def __del__(self) -> None:
-        self.close()
+        return self._context.run(True, prompt, max_tokens, on_token)
