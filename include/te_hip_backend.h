@@ -194,6 +194,31 @@ TE_API te_status te_hip_attention_decode_step_splitk_f16(
     void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * No counterpart in the reference: the fused decode step for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc).  Same arguments and results as
+ * te_hip_attention_decode_step_f16 without the workspace: the split-K partials
+ * go to a device array inside the library, TE_HIP_DECODE_NOALLOC_SCRATCH_BYTES
+ * (16 MiB) per GPU, held from first use until the process ends.  The call
+ * allocates nothing.  A call whose partials
+ * (seqs*layers*heads*chunks*(head_dim+2)*4 bytes, chunks as reported by
+ * te_hip_attention_decode_chunking) exceed the array returns
+ * TE_STATUS_UNSUPPORTED before any work is queued.  Every call on one GPU
+ * shares the array: calls that overlap in time on one GPU (different streams,
+ * different threads) race and must be ordered by the caller.
+ */
+#define TE_HIP_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
+TE_API te_status te_hip_attention_decode_step_noalloc_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *stream);
+
+/*
  * Batched-prefill causal attention over the fp16 cache.  Replaces the CPU
  * per-token loop (qwen.c:810-824: row t = decode at position t) and the MMA
  * prefill kernel te_attention_flash_mma_t_f32_kernel

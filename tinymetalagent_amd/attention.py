@@ -163,6 +163,27 @@ def decode_step(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_cache,
     return out
 
 
+def decode_step_noalloc(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_cache, *, position: int = 0,
+                        positions: Sequence[int] | None = None, q_bias=None, k_bias=None, v_bias=None,
+                        out: torch.Tensor, stream=None) -> torch.Tensor:
+    """decode_step through te_hip_attention_decode_step_noalloc_f16: the split-K
+    partials live in the library's per-GPU device array, so the call allocates
+    nothing (`out` is required).  Calls that overlap on one GPU race."""
+    q = query if query.dim() == 4 else query.reshape(query.shape[0], query.shape[1], query.shape[-2],
+                                                     query.shape[-1])
+    seqs, layers, heads, head_dim = q.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    for t, dt, n in ((q, torch.float32, "query"), (k_new, torch.float32, "k_new"), (v_new, torch.float32, "v_new"),
+                     (key_cache, torch.float16, "key_cache"), (value_cache, torch.float16, "value_cache"),
+                     (out, torch.float32, "out")):
+        _dtype(t, dt, n)
+    check(load_library().te_hip_attention_decode_step_noalloc_f16(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(rope_cos), _ptr(rope_sin),
+        _ptr(key_cache), _ptr(value_cache), _positions(positions), position, seqs, layers, ctx, heads, kv_heads,
+        head_dim, _ptr(out), _stream(stream)))
+    return out
+
+
 def attention_prefill(q_half, key_cache, value_cache, *, base_position: int = 0, out: torch.Tensor | None = None,
                       stream=None) -> torch.Tensor:
     """Causal prefill: q_half fp16 [seqs, layers, tokens, heads, d] -> out fp32, same shape."""

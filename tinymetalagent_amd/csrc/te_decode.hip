@@ -44,6 +44,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 namespace {
 
@@ -966,4 +967,84 @@ extern "C" te_status te_hip_attention_decode_combine(
         decode_merge_kernel<64><<<grid, 256, 0, te_hip::as_stream(stream)>>>(c);
     }
     return te_hip::launch_status();
+}
+
+// ---- te_hip_attention_decode_step_noalloc_f16 -------------------------------
+//
+// The fused decode step for callers that cannot allocate (code under graph
+// capture, serving loops that forbid hipMalloc): its split-K partials go to a
+// file-scope device array instead of a caller workspace.  Every GPU the library
+// runs on holds its own copy of `scratch` until the process ends; host code
+// reaches it only through the address hipGetSymbolAddress returns for the
+// current device (the array's name is a host-side stand-in, not a device
+// address).  All calls on one GPU share the array, so calls that overlap on
+// one GPU race; stream-ordered calls are safe (each call's merge reads only
+// partials its own split-K launch wrote, so nothing needs clearing).
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[TE_HIP_DECODE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Address of `scratch` on the current device, looked up once per device.
+te_status scratch_address(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return TE_STATUS_RUNTIME_ERROR;
+    }
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            return TE_STATUS_RUNTIME_ERROR;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TE_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" te_status te_hip_attention_decode_step_noalloc_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache,
+    const size_t *positions, size_t position,
+    size_t seqs, size_t layers, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *stream) {
+    if (query == nullptr || k_new == nullptr || v_new == nullptr || rope_cos == nullptr || rope_sin == nullptr ||
+        key_cache == nullptr || value_cache == nullptr || out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    size_t max_position = 0;
+    te_status st = check_decode_args(positions, position, seqs, layers, context_tokens, heads, kv_heads, head_dim,
+                                     &max_position);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    // The partials this exact call writes (not the position-monotone bound
+    // the workspace query reports) must fit the array.
+    const te_hip::DecodeGeometry geo = te_hip::decode_geometry(positions, position, seqs, layers, kv_heads);
+    const size_t need = te_hip::decode_workspace_bytes(geo, seqs, layers, heads, head_dim);
+    if (need > (size_t)TE_HIP_DECODE_NOALLOC_SCRATCH_BYTES) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    void *ws = nullptr;
+    if ((st = scratch_address(&ws)) != TE_STATUS_OK) {
+        return st;
+    }
+    return te_hip_attention_decode_step_f16(query, k_new, v_new, q_bias, k_bias, v_bias, rope_cos, rope_sin,
+                                            key_cache, value_cache, positions, position, seqs, layers,
+                                            context_tokens, heads, kv_heads, head_dim, out, ws,
+                                            (size_t)TE_HIP_DECODE_NOALLOC_SCRATCH_BYTES, stream);
 }

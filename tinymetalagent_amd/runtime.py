@@ -199,6 +199,9 @@ def _configure_library(lib: ctypes.CDLL) -> None:
           _vp])
     _sig(lib, "te_hip_attention_decode_step_splitk_f16",
          [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _szp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _sz, _vp])
+    _sig(lib, "te_hip_attention_decode_step_noalloc_f16",
+         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _szp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp])
+    _sig(lib, "te_hip_attention_decode_chunking", [_szp, _sz, _sz, _sz, _sz, _int, _szp, _szp])
     _sig(lib, "te_hip_attention_prefill_f16", [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp])
     _sig(lib, "te_hip_attention_prefill_workspace_bytes", [_sz] * 8, _sz)
     _sig(lib, "te_hip_attention_prefill_split_f16",
