@@ -30,6 +30,8 @@
 // in a fixed order (deterministic).
 #include "te_hip_common.h"
 
+#include <float.h>
+
 #include <algorithm>
 #include <cstdlib>
 
