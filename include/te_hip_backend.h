@@ -227,10 +227,84 @@ TE_API te_status te_hip_attention_decode_step_noalloc_f16(
  * attends cache positions 0..base_position+t inclusive; the cache must already
  * hold those positions (te_hip_rope_kv_append_f16 writes them).
  *
+ * The kernel reads the K cache and a transposed copy of the V cache, V^T:
+ *   value_t fp16 [seqs][layers][kv_heads][head_dim][ctx_pad],
+ *   ctx_pad = context_tokens rounded up to a multiple of 64,
+ * element (s, l, h, i, p) = value_cache (s, l, p, h, i) -- one row of positions
+ * per (kv head, dim), the layout the PV product reads with 16-byte loads
+ * (as the reference's Metal path keeps transposed copies,
+ * te_qkv_bias_rope_cache_batch_t_f32, metal_kernels.metal.inc:2254-2342).
+ * The *_vt entry points take V^T from the caller (te_hip_value_transpose_f16 or
+ * te_hip_attention_prefill_step_vt_f16 keep it current); the others build it
+ * for positions 0 .. base_position+tokens on every call.  V^T positions from
+ * base_position+tokens up to the next multiple of 8 must be finite (the V^T
+ * writers set them to 0): the kernel loads 8 positions at a time and weights
+ * the ones past a row's position by exactly 0.
+ *
  * q_half: fp16 rotated queries [seqs][layers][tokens][heads][head_dim];
  * out: fp32, same layout.  QK^T and PV run on fp16 MFMA with fp32 accumulation;
  * softmax is fp32.  head_dim in {64, 128}; heads % kv_heads == 0;
  * base_position + tokens <= context_tokens.
+ */
+
+/* Bytes of a V^T buffer (0 for zero sizes). */
+TE_API size_t te_hip_value_t_bytes(size_t seqs, size_t layers, size_t context_tokens, size_t kv_heads,
+                                   size_t head_dim);
+
+/* V^T of positions [first_position, first_position + count) of every
+ * (seq, layer, kv head), and 0 at the positions after them up to the next
+ * multiple of 8.  Other positions are not written.  Bit-exact copy. */
+TE_API te_status te_hip_value_transpose_f16(const uint16_t *value_cache, uint16_t *value_cache_t, size_t seqs,
+                                            size_t layers, size_t first_position, size_t count,
+                                            size_t context_tokens, size_t kv_heads, size_t head_dim,
+                                            void *stream);
+
+/*
+ * Prefill attention over the K cache and V^T.  With a workspace of at least
+ * te_hip_attention_prefill_vt_workspace_bytes bytes (the same shape), a launch
+ * whose tile pairs alone would leave compute units idle (short prompts, few
+ * heads, a chunk after a long cache) splits each (tile pair, head) over S key
+ * ranges: every split writes unnormalised partial rows to the workspace, and a
+ * second launch merges them into `out`.  S comes from the shape and the
+ * device's compute-unit count; the query returns S*seqs*layers*tokens*heads*
+ * (head_dim+2)*4 bytes, or 0 when S == 1.  workspace NULL runs one split.
+ * INVALID_ARGUMENT when a given workspace is too small.
+ */
+TE_API size_t te_hip_attention_prefill_vt_workspace_bytes(size_t seqs, size_t layers, size_t tokens,
+                                                          size_t base_position, size_t context_tokens, size_t heads,
+                                                          size_t kv_heads, size_t head_dim);
+TE_API te_status te_hip_attention_prefill_vt_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache_t,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Fused prefill step keeping V^T: bias + RoPE + fp16 append of the chunk's
+ * k / v into key_cache and value_cache (te_hip_rope_kv_append_f16's slots and
+ * bits), the chunk's V^T positions into value_cache_t, then the causal
+ * attention, whose prologue applies bias + RoPE to each query row in registers
+ * and rounds it to the fp16 operand (the bits te_hip_rope_kv_append_f16 writes
+ * to q_half).  `query`, `k_new` and `v_new` are inputs only.  Layouts: query
+ * [seqs][layers][tokens][heads][head_dim], k_new / v_new
+ * [seqs][layers][tokens][kv_heads][head_dim], out like query.  Every sequence
+ * starts at base_position; value_cache_t must hold V^T of positions
+ * 0 .. base_position-1.  workspace as te_hip_attention_prefill_vt_f16.  Four
+ * launches: append, V^T, attention, and the merge when the launch splits.
+ */
+TE_API te_status te_hip_attention_prefill_step_vt_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *value_cache_t,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Prefill over the plain caches: V^T of positions 0 .. base_position+tokens-1
+ * goes to a buffer the library owns (grown on demand under the library mutex;
+ * calls must share one stream), then the attention runs as one split.
  */
 TE_API te_status te_hip_attention_prefill_f16(
     const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
@@ -239,17 +313,11 @@ TE_API te_status te_hip_attention_prefill_f16(
     float *out, void *stream);
 
 /*
- * Key-split prefill: te_hip_attention_prefill_f16 for launches whose tile
- * pairs alone would leave compute units idle (short prompts, few heads, or a
- * chunk after a long cache).  Each (tile pair, head) is split over S key
- * ranges; every split writes unnormalised partial rows to `workspace`, and a
- * second launch merges them into `out`.  S is chosen from the shape and the
- * device's compute-unit count; S == 1 is the plain kernel and then the
- * workspace is not touched (it may be NULL).
- * te_hip_attention_prefill_workspace_bytes returns the bytes needed (0 when
- * S == 1 or the arguments are invalid): S*seqs*layers*tokens*heads*(head_dim+2)
- * floats.  Arguments otherwise as te_hip_attention_prefill_f16.
- * INVALID_ARGUMENT when the workspace is missing or too small.
+ * Key-split prefill over the plain caches: the workspace holds the key-split
+ * partials (when the launch splits, as te_hip_attention_prefill_vt_f16) followed
+ * by V^T of the cache; te_hip_attention_prefill_workspace_bytes returns both
+ * (0 only for invalid arguments).  INVALID_ARGUMENT when the workspace is
+ * missing or too small.
  */
 TE_API size_t te_hip_attention_prefill_workspace_bytes(size_t seqs, size_t layers, size_t tokens,
                                                        size_t base_position, size_t context_tokens, size_t heads,
@@ -261,16 +329,9 @@ TE_API te_status te_hip_attention_prefill_split_f16(
     float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
- * Fused prefill step: te_hip_rope_kv_append_f16 (tokens tokens at base_position)
- * followed by te_hip_attention_prefill_f16, as two launches: bias + RoPE + fp16
- * append of the chunk's k/v, then the causal attention, whose prologue applies
- * bias + RoPE to each query row in registers and rounds it to the fp16 operand
- * (the same bits te_hip_rope_kv_append_f16 writes to q_half).  `query`, `k_new`
- * and `v_new` are inputs only: nothing is rotated in place and no fp16 copy of
- * the queries is stored.  Layouts: query [seqs][layers][tokens][heads][head_dim],
- * k_new / v_new [seqs][layers][tokens][kv_heads][head_dim], out like query.
- * Every sequence starts at base_position.  Arguments and limits otherwise as
- * te_hip_rope_kv_append_f16 and te_hip_attention_prefill_f16.
+ * Fused prefill step over the plain caches: te_hip_attention_prefill_step_vt_f16
+ * with V^T of positions 0 .. base_position+tokens-1 built in the library-owned
+ * buffer (as te_hip_attention_prefill_f16) and one split.
  */
 TE_API te_status te_hip_attention_prefill_step_f16(
     const float *query, const float *k_new, const float *v_new,

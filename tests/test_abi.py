@@ -156,13 +156,32 @@ def test_backend_guard_conventions(lib):
     assert lib.te_hip_attention_prefill_workspace_bytes(1, 1, 4, 6, 8, 2, 1, 128) == 0  # chunk past the cache
     assert lib.te_hip_attention_prefill_workspace_bytes(1, 1, 4, 0, 8, 2, 1, 80) == 0  # head_dim 80
     need = lib.te_hip_attention_prefill_workspace_bytes(1, 1, 300, 0, 300, 16, 2, 128)
-    assert need % (300 * 16 * 130 * 4) == 0  # splits x rows x heads x (head_dim + 2) floats
+    vt = lib.te_hip_value_t_bytes(1, 1, 300, 2, 128)
+    assert vt == 2 * 128 * 320 * 2  # [kv][head_dim][ctx rounded up to 64] fp16
+    part = lib.te_hip_attention_prefill_vt_workspace_bytes(1, 1, 300, 0, 300, 16, 2, 128)
+    assert need == part + vt
+    assert part % (300 * 16 * 130 * 4) == 0  # splits x rows x heads x (head_dim + 2) floats
     split = lib.te_hip_attention_prefill_split_f16
     assert split(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None, 0, None) in ok
     assert split(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None, 0, None) == 3  # head_dim 80
-    if need:
-        assert split(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, None, 0, None) == 1  # workspace missing
-        assert split(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, ws, need - 1, None) == 1  # too small
+    assert split(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, None, 0, None) == 1  # workspace missing
+    assert split(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, ws, need - 1, None) == 1  # too small
+    vt_attn = lib.te_hip_attention_prefill_vt_f16
+    assert vt_attn(None, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128, buf, None, 0, None) in ok
+    assert vt_attn(buf, buf, buf, 1, 1, 4, 6, 8, 2, 1, 128, buf, None, 0, None) == 1  # chunk past the cache
+    assert vt_attn(buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80, buf, None, 0, None) == 3  # head_dim 80
+    if part:
+        assert vt_attn(buf, buf, buf, 1, 1, 300, 0, 300, 16, 2, 128, buf, ws, part - 1, None) == 1  # too small
+    tr = lib.te_hip_value_transpose_f16
+    assert tr(None, buf, 1, 1, 0, 4, 8, 2, 128, None) == 1
+    assert tr(buf, buf, 1, 1, 6, 4, 8, 2, 128, None) == 1  # range past the cache
+    assert tr(buf, buf, 1, 1, 0, 4, 8, 2, 96, None) == 3  # head_dim 96
+    assert tr(buf, buf, 1, 1, 3, 0, 8, 2, 128, None) == 0  # nothing to do
+    step_vt = lib.te_hip_attention_prefill_step_vt_f16
+    assert step_vt(buf, buf, buf, None, None, None, buf, buf, buf, buf, None, 1, 1, 4, 0, 8, 2, 1, 128,
+                   buf, None, 0, None) == 1  # no V^T buffer
+    assert step_vt(buf, buf, buf, None, None, None, buf, buf, buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 80,
+                   buf, None, 0, None) == 3  # head_dim 80
     step = lib.te_hip_attention_prefill_step_f16
     assert step(buf, None, buf, None, None, None, buf, buf, buf, buf, 1, 1, 4, 0, 8, 2, 1, 128,
                 buf, None) == 1  # no k_new

@@ -438,8 +438,9 @@ def test_prefill_split_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens, bas
     q16 = S.to_f16_bits(S.normal(41, tag + "q", (seqs, layers, tokens, h, d)))
     lib = R.load_library()
     nbytes = lib.te_hip_attention_prefill_workspace_bytes(seqs, layers, tokens, base, ctx, h, kv, d)
-    splits = nbytes // (seqs * layers * tokens * h * (d + 2) * 4) if nbytes else 1
-    assert nbytes == 0 or nbytes == splits * seqs * layers * tokens * h * (d + 2) * 4
+    part = nbytes - lib.te_hip_value_t_bytes(seqs, layers, ctx, kv, d)
+    splits = part // (seqs * layers * tokens * h * (d + 2) * 4) if part else 1
+    assert part == 0 or part == splits * seqs * layers * tokens * h * (d + 2) * 4
     qd, kd, vd = f16_dev(q16), f16_dev(kc), f16_dev(vc)
     got = A.attention_prefill_split(qd, kd, vd, base_position=base).cpu().numpy()
     plain = A.attention_prefill(qd, kd, vd, base_position=base).cpu().numpy()
@@ -454,10 +455,9 @@ def test_prefill_split_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens, bas
           f"max abs err {worst:.3e}, vs plain kernel {drift:.3e}")
     assert worst <= TOL
     assert drift <= TOL
-    if nbytes:
-        with pytest.raises(R.TinyEngineError):
-            A.attention_prefill_split(qd, kd, vd, base_position=base,
-                                      workspace=torch.empty(nbytes - 4, dtype=torch.uint8, device=DEV))
+    with pytest.raises(R.TinyEngineError):
+        A.attention_prefill_split(qd, kd, vd, base_position=base,
+                                  workspace=torch.empty(nbytes - 4, dtype=torch.uint8, device=DEV))
 
 
 def test_prefill_several_sequences_and_layers(oracle_mod):
@@ -668,3 +668,115 @@ def test_calibration_kernel_runs():
     R.check(lib.te_hip_calibrate_mfma_f16(blocks, iters, out.data_ptr(), torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
+
+
+# ----------------------------------------------------- V^T prefill paths ---
+
+@pytest.mark.parametrize("seqs,layers,ctx,kv,d,first,count", [
+    (1, 1, 300, 2, 128, 0, 300),     # whole cache, ctx not a multiple of 8 or 64
+    (2, 3, 130, 4, 64, 5, 100),      # unaligned range, zero tail 105..111
+    (1, 2, 1000, 2, 128, 937, 61),   # tail range ending at the cache end
+    (1, 1, 64, 2, 128, 10, 0),       # nothing to do
+])
+def test_value_transpose_bits(seqs, layers, ctx, kv, d, first, count):
+    """te_hip_value_transpose_f16: V^T[.., i, p] = V[.., p, .., i] bit for bit over
+    [first, first + count), 0 from there to the next multiple of 8, every
+    other position untouched."""
+    g = torch.Generator(device=DEV).manual_seed(ctx + first)
+    vc = torch.randn((seqs, layers, ctx, kv, d), generator=g, device=DEV).half()
+    vt = A.value_t_buffer(seqs, layers, ctx, kv, d)
+    pad = vt.shape[-1]
+    assert pad % 64 == 0 and pad >= ctx
+    vt.fill_(7.0)
+    A.value_transpose(vc, vt, first_position=first, count=count)
+    torch.cuda.synchronize()
+    want = torch.full_like(vt, 7.0)
+    end = first + count
+    want[..., first:end] = vc.permute(0, 1, 3, 4, 2)[..., first:end]
+    if count:
+        want[..., end:min((end + 7) // 8 * 8, pad)] = 0.0
+    assert torch.equal(vt.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("seqs,layers,h,kv,d,tokens,base", [
+    (1, 1, 16, 2, 128, 300, 0),      # 3 tiles: the lone middle tile and a pair
+    (1, 1, 16, 2, 128, 130, 200),    # chunk after a cached prefix
+    (1, 1, 16, 2, 128, 1, 0),        # one row
+    (1, 1, 14, 2, 64, 200, 37),      # head_dim 64, unaligned base
+    (2, 3, 12, 2, 128, 129, 1000),   # several (seq, layer) units, long prefix
+    (1, 1, 28, 4, 128, 257, 3),      # 7B grouping
+])
+def test_prefill_vt_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens, base):
+    """te_hip_attention_prefill_vt_f16 over V^T from te_hip_value_transpose_f16,
+    with one split and with the library's key split, against the oracle for
+    every row; one split is bit-identical to the plain-cache entry point."""
+    ctx = base + tokens + 5
+    tag = f"pvt{seqs}{layers}{h}{d}{tokens}{base}"
+    kc = S.to_f16_bits(S.normal(43, tag + "k", (seqs, layers, ctx, kv, d)))
+    vc = S.to_f16_bits(S.normal(43, tag + "v", (seqs, layers, ctx, kv, d)))
+    q16 = S.to_f16_bits(S.normal(43, tag + "q", (seqs, layers, tokens, h, d)))
+    qd, kd, vd = f16_dev(q16), f16_dev(kc), f16_dev(vc)
+    vt = A.value_t_buffer(seqs, layers, ctx, kv, d)
+    A.value_transpose(vd, vt, first_position=0, count=base + tokens)
+    ws = A.prefill_vt_workspace(seqs, layers, tokens, h, kv, d, base_position=base, context_tokens=ctx)
+    one = A.attention_prefill_vt(qd, kd, vt, base_position=base).cpu().numpy()
+    split = A.attention_prefill_vt(qd, kd, vt, base_position=base, workspace=ws).cpu().numpy()
+    plain = A.attention_prefill(qd, kd, vd, base_position=base).cpu().numpy()
+    assert np.array_equal(one, plain)
+    worst = 0.0
+    for s_ in range(seqs):
+        for l_ in range(layers):
+            want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q16[s_, l_]).reshape(tokens, h, d),
+                                                kc[s_, l_].copy(), vc[s_, l_].copy(), tokens, base, ctx, h, kv, d)
+            want = want.reshape(tokens, h, d)
+            worst = max(worst, maxabs(one[s_, l_], want), maxabs(split[s_, l_], want))
+    nsplit = 1 if ws is None else ws.numel() // (seqs * layers * tokens * h * (d + 2) * 4)
+    print(f"prefill V^T {seqs}x{layers} H{h} KV{kv} d{d} L{tokens} base{base} ({nsplit} splits): "
+          f"max abs err {worst:.3e}")
+    assert worst <= TOL
+
+
+@pytest.mark.parametrize("seqs,layers,h,kv,d,tokens,base,bias", [
+    (1, 1, 16, 2, 128, 300, 0, True),
+    (2, 2, 14, 2, 64, 130, 37, True),
+    (1, 2, 12, 2, 128, 200, 500, False),
+])
+def test_prefill_step_vt_matches_plain_step(seqs, layers, h, kv, d, tokens, base, bias):
+    """te_hip_attention_prefill_step_vt_f16 (caller V^T, key split) against
+    te_hip_attention_prefill_step_f16 (library V^T, one split): the same cache
+    bits, V^T equal to the transposed value cache over positions
+    0 .. base + tokens - 1, and the same output (bit for bit without a split,
+    within the bar with one)."""
+    ctx = base + tokens + 3
+    g = torch.Generator(device=DEV).manual_seed(tokens + base)
+    q = torch.randn((seqs, layers, tokens, h, d), generator=g, device=DEV) / math.sqrt(d)
+    k = torch.randn((seqs, layers, tokens, kv, d), generator=g, device=DEV)
+    v = torch.randn((seqs, layers, tokens, kv, d), generator=g, device=DEV)
+    qb = torch.randn((layers, h * d), generator=g, device=DEV) * 0.1 if bias else None
+    kb = torch.randn((layers, kv * d), generator=g, device=DEV) * 0.1 if bias else None
+    vb = torch.randn((layers, kv * d), generator=g, device=DEV) * 0.1 if bias else None
+    kc0 = torch.randn((seqs, layers, ctx, kv, d), generator=g, device=DEV).half()
+    vc0 = torch.randn((seqs, layers, ctx, kv, d), generator=g, device=DEV).half()
+    cos, sin = A.rope_table(ctx, d, 1e6)
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    ref = A.prefill_step(q, k, v, cos, sin, kc1, vc1, base_position=base, q_bias=qb, k_bias=kb, v_bias=vb)
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    vt = A.value_t_buffer(seqs, layers, ctx, kv, d)
+    A.value_transpose(vc2, vt, first_position=0, count=base)  # the cached prefix
+    one = A.prefill_step_vt(q, k, v, cos, sin, kc2, vc2, vt, base_position=base, q_bias=qb, k_bias=kb, v_bias=vb)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    n = base + tokens
+    assert torch.equal(vt[..., :n].view(torch.int16), vc2.permute(0, 1, 3, 4, 2)[..., :n].view(torch.int16))
+    assert torch.equal(one, ref)
+    ws = A.prefill_vt_workspace(seqs, layers, tokens, h, kv, d, base_position=base, context_tokens=ctx)
+    kc3, vc3 = kc0.clone(), vc0.clone()
+    vt3 = A.value_t_buffer(seqs, layers, ctx, kv, d)
+    A.value_transpose(vc3, vt3, first_position=0, count=base)
+    split = A.prefill_step_vt(q, k, v, cos, sin, kc3, vc3, vt3, base_position=base, q_bias=qb, k_bias=kb,
+                              v_bias=vb, workspace=ws)
+    torch.cuda.synchronize()
+    err = float((split - ref).abs().max())
+    print(f"fused step V^T H{h} d{d} L{tokens} base{base}: split vs one split {err:.3e}")
+    assert err <= TOL

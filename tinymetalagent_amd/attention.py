@@ -200,6 +200,80 @@ def attention_prefill(q_half, key_cache, value_cache, *, base_position: int = 0,
     return out
 
 
+def value_t_buffer(seqs: int, layers: int, context_tokens: int, kv_heads: int, head_dim: int,
+                   device="cuda") -> torch.Tensor:
+    """A zeroed V^T buffer [seqs, layers, kv_heads, head_dim, ctx_pad] (fp16) for
+    the *_vt prefill entry points; ctx_pad = context_tokens rounded up to 64."""
+    n = load_library().te_hip_value_t_bytes(seqs, layers, context_tokens, kv_heads, head_dim)
+    if n == 0:
+        raise TinyEngineError("invalid argument")
+    pad = n // (2 * seqs * layers * kv_heads * head_dim)
+    return torch.zeros((seqs, layers, kv_heads, head_dim, pad), dtype=torch.float16, device=device)
+
+
+def value_transpose(value_cache, value_t, *, first_position: int = 0, count: int | None = None,
+                    stream=None) -> torch.Tensor:
+    """te_hip_value_transpose_f16: V^T of positions [first, first + count) of
+    every (seq, layer, kv head) into value_t (zeros up to the next multiple of 8)."""
+    seqs, layers, ctx, kv_heads, head_dim = value_cache.shape
+    _dtype(value_cache, torch.float16, "value_cache")
+    _dtype(value_t, torch.float16, "value_t")
+    if count is None:
+        count = ctx - first_position
+    check(load_library().te_hip_value_transpose_f16(_ptr(value_cache), _ptr(value_t), seqs, layers, first_position,
+                                                    count, ctx, kv_heads, head_dim, _stream(stream)))
+    return value_t
+
+
+def prefill_vt_workspace(seqs: int, layers: int, tokens: int, heads: int, kv_heads: int, head_dim: int, *,
+                         base_position: int = 0, context_tokens: int, device="cuda") -> torch.Tensor | None:
+    """Key-split partials for the *_vt prefill entry points (None: no split)."""
+    n = load_library().te_hip_attention_prefill_vt_workspace_bytes(seqs, layers, tokens, base_position,
+                                                                   context_tokens, heads, kv_heads, head_dim)
+    return None if n == 0 else torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def attention_prefill_vt(q_half, key_cache, value_t, *, base_position: int = 0, out: torch.Tensor | None = None,
+                         workspace: torch.Tensor | None = None, context_tokens: int | None = None,
+                         stream=None) -> torch.Tensor:
+    """Causal prefill over the K cache and V^T; `workspace` (prefill_vt_workspace)
+    lets the launch split keys, None runs one split."""
+    seqs, layers, tokens, heads, head_dim = q_half.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    _dtype(q_half, torch.float16, "q_half")
+    _dtype(key_cache, torch.float16, "key_cache")
+    _dtype(value_t, torch.float16, "value_t")
+    if out is None:
+        out = torch.empty(q_half.shape, dtype=torch.float32, device=q_half.device)
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load_library().te_hip_attention_prefill_vt_f16(
+        _ptr(q_half), _ptr(key_cache), _ptr(value_t), seqs, layers, tokens, base_position, ctx, heads, kv_heads,
+        head_dim, _ptr(out), _ptr(workspace), nbytes, _stream(stream)))
+    return out
+
+
+def prefill_step_vt(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_cache, value_t, *,
+                    base_position: int = 0, q_bias=None, k_bias=None, v_bias=None, out: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Fused prefill step keeping V^T: bias + RoPE + fp16 append of the chunk's
+    k / v (into key_cache, value_cache and value_t), then the causal attention
+    over the K cache and V^T.  query / k_new / v_new are read only."""
+    seqs, layers, tokens, heads, head_dim = query.shape
+    ctx, kv_heads = key_cache.shape[2], key_cache.shape[3]
+    for t, dt, n in ((query, torch.float32, "query"), (k_new, torch.float32, "k_new"),
+                     (v_new, torch.float32, "v_new"), (key_cache, torch.float16, "key_cache"),
+                     (value_cache, torch.float16, "value_cache"), (value_t, torch.float16, "value_t")):
+        _dtype(t, dt, n)
+    if out is None:
+        out = torch.empty(query.shape, dtype=torch.float32, device=query.device)
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load_library().te_hip_attention_prefill_step_vt_f16(
+        _ptr(query), _ptr(k_new), _ptr(v_new), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(rope_cos),
+        _ptr(rope_sin), _ptr(key_cache), _ptr(value_cache), _ptr(value_t), seqs, layers, tokens, base_position, ctx,
+        heads, kv_heads, head_dim, _ptr(out), _ptr(workspace), nbytes, _stream(stream)))
+    return out
+
+
 def prefill_workspace(seqs: int, layers: int, tokens: int, heads: int, kv_heads: int, head_dim: int, *,
                       base_position: int = 0, context_tokens: int, device="cuda") -> torch.Tensor | None:
     """Workspace for attention_prefill_split (None when the launch does not split)."""

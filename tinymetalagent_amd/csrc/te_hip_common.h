@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "te_hip_backend.h"
 
 typedef _Float16 f16;
@@ -82,6 +84,19 @@ struct DecodeGeometry {
 
 // Compute units of the current device (256 when the query fails).
 int device_compute_units();
+
+// The library's process-wide mutex: held by the host-pointer entry points, and
+// by device entry points called without a workspace while they enqueue work
+// that uses a library-owned buffer.
+std::mutex &library_mutex();
+
+// Library-owned device buffers for entry points called without a workspace,
+// one per purpose, grown on demand (a growth frees the old buffer, which
+// waits for the device) and kept.  The caller holds library_mutex() from the
+// request until its last use of the buffer is enqueued; calls sharing a
+// buffer must go to one stream.
+enum LibraryBuffer { kLibBufDecode = 0, kLibBufPrefillVt = 1, kLibBufCount = 2 };
+te_status library_buffer(LibraryBuffer which, size_t bytes, void **ptr);
 
 // Decode-layer vector operations (te_vecops.hip); arguments already checked.
 size_t ggml_row_bytes(uint32_t ggml_type, size_t cols);  // 0 = type / cols not supported

@@ -58,6 +58,7 @@ struct Runtime {
 };
 
 Runtime g_rt;
+DeviceBuffer g_library_buffers[te_hip::kLibBufCount];
 
 // Caller holds g_mutex.
 int probe_locked() {
@@ -150,6 +151,19 @@ te_status mma_twin(int mode, const float *query, const float *key_t, const float
 }
 
 }  // namespace
+
+namespace te_hip {
+
+std::mutex &library_mutex() { return g_mutex; }
+
+te_status library_buffer(LibraryBuffer which, size_t bytes, void **ptr) {
+    DeviceBuffer &b = g_library_buffers[which];
+    const te_status st = b.ensure(bytes);
+    *ptr = st == TE_STATUS_OK ? b.ptr : nullptr;
+    return st;
+}
+
+}  // namespace te_hip
 
 extern "C" int te_hip_available(void) {
     std::lock_guard<std::mutex> lock(g_mutex);
@@ -414,19 +428,18 @@ extern "C" te_status te_hip_attention_decode_f16(
         }
         // The library-owned workspace is shared: serialize whole calls on it.
         std::lock_guard<std::mutex> lock(g_mutex);
-        static DeviceBuffer ws;
-        te_status st = ws.ensure(need);
+        void *ws = nullptr;
+        te_status st = te_hip::library_buffer(te_hip::kLibBufDecode, need, &ws);
         if (st != TE_STATUS_OK) {
             return st;
         }
         st = te_hip_attention_decode_splitk_f16(query, key_cache, value_cache, positions, position, seqs, layers,
-                                                context_tokens, heads, kv_heads, head_dim, ws.ptr, ws.bytes,
-                                                stream);
+                                                context_tokens, heads, kv_heads, head_dim, ws, need, stream);
         if (st != TE_STATUS_OK) {
             return st;
         }
         return te_hip_attention_decode_combine(positions, position, seqs, layers, heads, kv_heads, head_dim, out,
-                                               ws.ptr, ws.bytes, stream);
+                                               ws, need, stream);
     }
     te_status st = te_hip_attention_decode_splitk_f16(query, key_cache, value_cache, positions, position, seqs,
                                                       layers, context_tokens, heads, kv_heads, head_dim,

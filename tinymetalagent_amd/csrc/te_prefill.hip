@@ -5,6 +5,12 @@
 // `key <= base + row` of te_attention_flash_mma_t_f32_kernel
 // (metal_kernels.metal.inc:2767-2775), which also defines chunked prefill.
 //
+// Inputs: the fp16 K cache in the slot layout [sl][ctx][kv][D], and a
+// transposed copy of the V cache, V^T [sl][kv][D][ctx_pad] (ctx_pad =
+// context_tokens rounded up to 64): one row of keys per (kv head, dim), the
+// layout the PV product reads (the reference Metal path keeps transposed
+// copies the same way, te_qkv_bias_rope_cache_batch_t_f32).
+//
 // Work decomposition.  Query rows are cut into tiles of BM (128) rows.  One
 // workgroup = 8 waves (two per SIMD) = the PAIR of tiles (n-1-i, i) of one
 // head, processed one after the other, so every workgroup does the same causal
@@ -12,19 +18,30 @@
 // (32*(w&3), two 16-row MFMA column blocks) and key half w>>2: a step of 128
 // keys is two BN (64) key blocks, block 2*step + half for each wave, and the
 // two halves' softmax states merge through LDS at the end of the tile.  The
-// K/V of each step reach LDS by global_load_lds DMA, double-buffered: the
-// DMA of step s+1 is in flight while step s is consumed, one barrier per step.
-// A key split (te_hip_attention_prefill_split_f16) gives each workgroup a
-// range of the steps and writes unnormalised partial rows instead.
+// K and V^T of each step reach LDS by global_load_lds DMA, double-buffered:
+// the DMA of step s+1 is in flight while step s is consumed, one barrier per
+// step.  A key split (te_hip_attention_prefill_vt_f16 with a workspace) gives
+// each workgroup a range of the steps and writes unnormalised partial rows.
 //
 //   S^T[64 keys x 32 rows] = K[64 x D] . Q^T[D x 32]            fp16 MFMA 16x16x32
 //   O^T[D x 32 rows]      += V^T[D x 64] . P^T[64 x 32]         fp16 MFMA 16x16x32
 //
-// The S^T result layout (lane = row c, keys 4g+r) is the P^T B-operand layout
-// of the PV MFMA (keys kmap(g,j) = 16(j/4)+4g+(j%4) per 32-key step), so P stays
-// in registers.  V^T's A operand comes from row-major LDS through the gfx950
-// transposing read ds_read_b64_tr_b16 (two per 16-dim output tile), so O^T
-// comes out with each lane holding dims 16t + 4g + {0..3} of one row.
+// Key order.  The A operand of QK^T tile i (16 rows) takes, for row m, key
+// sigma(i, m) = 32(i/2) + 8(m/4) + 4(i%2) + m%4 of the block.  The S^T result
+// of lane (c, g) (query row c, result rows 4g + r) then holds keys
+// 32(i/2) + 8g + 4(i%2) + r, so for the PV k-step ks (tiles 2ks, 2ks+1) each
+// lane holds the eight consecutive keys 32ks + 8g .. +7: its P^T B operand,
+// kept in registers, and its V^T A operand is one 16-byte LDS read (dim
+// 16t + c, keys 32ks + 8g ..).
+//
+// LDS layouts (every operand read is a conflict-free ds_read_b128; the rates
+// were measured on MI355X against a linear read):
+//   K half block:  64 rows of 2D bytes; row 16i + c holds key sigma(i, c);
+//                  16-byte chunk q of a row sits at slot q ^ (c & (D/8 - 1)).
+//   V^T half block: D rows (dims) of 128 bytes (64 keys); chunk q (keys
+//                  8q .. 8q+7) at slot q ^ (dim & 7).
+// The DMA writes 1 KB per wave instruction with lane l at +16 l; each lane's
+// global source is the chunk its slot holds.
 //
 // Softmax: fp32, base 2.  The row maximum is taken on raw scores; p =
 // exp2(s*qscale - m_ref) with one FMA.  m_ref is only raised (and O, l
@@ -41,7 +58,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
-
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -52,6 +69,10 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr float kLazyLog2 = 8.0f;
 constexpr int kMaxPrefillSplits = 32;
+constexpr int kVtAlign = 64;  // V^T rows are padded to a multiple of this many positions
+constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dispatched to them round-robin
+constexpr int kQkAhead = 2;   // K operand read-ahead, in batches of two reads (four MFMAs)
+constexpr int kPvAhead = 4;   // V^T operand read-ahead, in reads (two MFMAs each)
 
 struct PrefillArgs {
     const f16 *q;            // fp16 rotated queries, or null when q32 is given
@@ -60,12 +81,13 @@ struct PrefillArgs {
     const float *rope_cos;   // fused step: [ctx][D/2]
     const float *rope_sin;
     const f16 *key_cache;
-    const f16 *value_cache;
+    const f16 *value_t;      // V^T [sl][kv][D][ctx_pad]
     float *out;
     int layers;
     int tokens;
     int base;
     int ctx;
+    int ctx_pad;
     int heads;
     int kv_heads;
     int group;
@@ -151,46 +173,37 @@ __device__ __forceinline__ float xor_sum_16_32(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// LDS layout of a 64-key half block (one key half of a step), built for
-// global_load_lds_dwordx4: one wave instruction writes 1 KB contiguous, lane l
-// at +16 l.  The 64 keys form NB groups of R = 1024 / (2 D) keys; group b
-// holds keys b, b + NB, b + 2 NB, ... as R unpadded rows at
-//   b * kGroupPitch + 16 * rho(b) + (key / NB) * 2D   bytes,
-// rho(b) = 2 (b & 3) + ((b >> 2) & 1).  The group offsets 16 rho(b) mod 128
-// make both operand reads conflict-free with plain immediate offsets:
-//   K (ds_read_b128): 8 lanes read keys c..c+7 (groups c & (NB-1)), 16 B each,
-//     at 8 distinct 16-byte bank slots;
-//   V (ds_read_b64_tr_b16): 16 lanes read 4 keys x 32 B, groups 4(g&1) + j,
-//     at 4 distinct 32-byte bank slots.
-constexpr int kGroupPitch = 1024 + 128;
-
-__device__ __forceinline__ int rho(int b) { return 2 * (b & 3) + ((b >> 2) & 1); }
+// Key of row m of QK^T tile i within a 64-key block (see "Key order").
+__device__ __forceinline__ int sigma(int i, int m) { return 32 * (i >> 1) + 8 * (m >> 2) + 4 * (i & 1) + (m & 3); }
 
 template <int D>
-struct HalfLayout {
-    static constexpr int R = 1024 / (2 * D);   // keys per group (one 1 KB load)
-    static constexpr int NB = BN / R;          // groups per 64 keys
-    static constexpr int BYTES = NB * kGroupPitch;
-    // byte offset of (key, 16-byte chunk q) inside the half block
-    static __device__ __forceinline__ int offset(int key, int q) {
-        const int b = key % NB;
-        return b * kGroupPitch + 16 * rho(b) + (key / NB) * (2 * D) + 16 * q;
-    }
+struct KHalf {
+    static constexpr int ROWB = 2 * D;              // bytes per key row
+    static constexpr int CPR = D / 8;               // 16-byte chunks per row
+    static constexpr int BYTES = BN * ROWB;         // 16 KB (D = 128)
+    static constexpr int LOADS = BYTES / 1024;      // DMA instructions per half block
+};
+
+template <int D>
+struct VtHalf {
+    static constexpr int ROWB = 2 * BN;             // 64 keys per dim row
+    static constexpr int BYTES = D * ROWB;          // 16 KB (D = 128)
+    static constexpr int LOADS = BYTES / 1024;
 };
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
-    typedef HalfLayout<D> HL;
+    typedef KHalf<D> KH;
+    typedef VtHalf<D> VH;
     constexpr int KK = D / 32;                      // QK^T K-steps
     constexpr int NT = D / 16;                      // O^T output tiles
-    constexpr int CPR = D / 8;                      // 16-byte chunks per cache row
-    constexpr int HB = HL::BYTES;                   // one 64-key half block (K or V)
-    constexpr int STAGE = 4 * HB;                   // K halves 0,1 then V halves 0,1
-    constexpr int GROUPS = 2 * 2 * HL::NB;          // 1 KB loads per step (K and V, both halves)
-    constexpr int LOADS = GROUPS / kWaves;          // per wave per step
+    constexpr int KB = KH::BYTES;
+    constexpr int VB = VH::BYTES;
     constexpr int XFER = (4 * NT + 2) * 64;         // floats per wave in the merge exchange
+    constexpr int STAGE = std::max(2 * KB + 2 * VB, kWaves * XFER * 4);
+    constexpr int GROUPS = 2 * KH::LOADS + 2 * VH::LOADS;  // 1 KB loads per step
+    constexpr int LOADS = GROUPS / kWaves;          // per wave per step
     static_assert(LOADS * kWaves == GROUPS, "staging loads must tile the step");
-    static_assert(kWaves * XFER * 4 <= STAGE, "merge exchange must fit in one staging buffer");
 
     // Two staging buffers as separate LDS variables: the compiler can then
     // tell the DMA into one from the operand reads of the other and does not
@@ -198,11 +211,24 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     __shared__ __attribute__((aligned(1024))) unsigned char st0[STAGE];
     __shared__ __attribute__((aligned(1024))) unsigned char st1[STAGE];
 
-    const int pair = blockIdx.x;
-    const int h = blockIdx.y;
-    const int sl = blockIdx.z / a.splits;
-    const int split = blockIdx.z % a.splits;
-    const int kvh = h / a.group;
+    // Work unit of this workgroup.  Units are ordered pair-fastest, then the
+    // heads of one KV group, then KV head, then (seq*layer, split); the
+    // hardware hands workgroup ids to the 8 XCDs round-robin, so XCD x gets
+    // units [x W/8, (x+1) W/8): the heads sharing one KV group's K/V run on
+    // one XCD and its L2 holds that group's keys and values only.
+    int unit = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+    const int n_units = (int)(gridDim.x * gridDim.y * gridDim.z);
+    if (n_units % kXcds == 0) {
+        unit = (unit % kXcds) * (n_units / kXcds) + unit / kXcds;
+    }
+    const int pair = unit % (int)gridDim.x;
+    const int hg = unit / (int)gridDim.x;           // (z, kv head, head in group)
+    const int h_in = hg % a.group;
+    const int kvh = (hg / a.group) % a.kv_heads;
+    const int zz = hg / (a.group * a.kv_heads);
+    const int h = kvh * a.group + h_in;
+    const int sl = zz / a.splits;
+    const int split = zz % a.splits;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -213,37 +239,106 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     const int n_tiles_wg = pair == long_tile ? 1 : 2;  // odd tile count: the middle tile has no partner
 
     const size_t row_stride = (size_t)a.kv_heads * D;
-    const size_t cache_base = (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
-    const f16 *kbase = a.key_cache + cache_base;
-    const f16 *vbase = a.value_cache + cache_base;
+    const f16 *kbase = a.key_cache + (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
+    const f16 *vtbase = a.value_t + ((size_t)sl * a.kv_heads + kvh) * D * (size_t)a.ctx_pad;
     const float qs = a.qscale;
 
     auto tile_kmax = [&](int qt) { return a.base + min(qt * BM + BM, a.tokens) - 1; };  // last key of a tile
 
-    // Direct global -> LDS staging of step `step` (keys step*128 ..) into buffer
-    // `buf`: wave w issues groups w, w + 8, ...; group u = (kv, half, b) lands
-    // at its 1 KB slot, lane l carrying row l / CPR, chunk l % CPR of the group.
-    const int ld_pos = lane / CPR;
-    const int ld_q = lane % CPR;
+    // Direct global -> LDS staging of step `step` (keys step*128 ..) into
+    // buffer `stage`: wave w issues loads w, w + 8, ...; loads 0 .. 2 KL-1 are
+    // the K half blocks, the rest the V^T half blocks (a wave-uniform choice).
+    // The loads are buffer loads: a descriptor per operand (base = this unit's
+    // K slice / V^T rows, bounded by their extent, so any address past them
+    // reads 0 instead of faulting), a per-lane byte offset fixed for the
+    // kernel (ld_off) and a scalar per-step offset, so a step's loads cost no
+    // vector address arithmetic.  On a step that reaches past kmax (the last
+    // step of a partial tile), K keys past kmax are clamped to it and a V^T
+    // chunk past kmax becomes the chunk holding kmax (its extra keys are
+    // masked, and finite: the V^T writers zero the positions up to the next
+    // multiple of 8 after a sequence).
+    const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16 *>(kbase), (short)0, (int)(((size_t)a.ctx * row_stride - (size_t)kvh * D) * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16 *>(vtbase), (short)0, (int)((size_t)D * a.ctx_pad * 2), 0x00020000);
+    // Load i of a wave is a K load for i < KH::LOADS / 4 (the first half of
+    // the wave's loads), else a V^T load; its half block and 1 KB slot follow
+    // from i at compile time plus the wave index.
+    static_assert(KH::LOADS == VH::LOADS && KH::LOADS % kWaves == 0, "load split");
+    constexpr int NKL = KH::LOADS / 4;  // K loads per wave per step
+    const int wave_slot = __builtin_amdgcn_readfirstlane(wave) * 1024;
+    auto stage_dst = [&](unsigned char *stage, int i) __attribute__((always_inline)) {
+        const int w = i < NKL ? i : i - NKL;          // index among this wave's K (or V^T) loads
+        const int hh = (kWaves * w) / KH::LOADS;      // half block
+        const int slot = (kWaves * w) % KH::LOADS;    // + wave: 1 KB slot in the half block
+        return stage + (i < NKL ? hh * KB : 2 * KB + hh * VB) + 1024 * slot + wave_slot;
+    };
+    unsigned ld_off[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int w = i < NKL ? i : i - NKL;
+        const int hh = (kWaves * w) / KH::LOADS;
+        const int j = (kWaves * w) % KH::LOADS + wave;
+        if (i < NKL) {
+            const int byte = 1024 * j + 16 * lane;
+            const int row = byte / KH::ROWB;
+            const int q = ((byte % KH::ROWB) >> 4) ^ (row & 15 & (KH::CPR - 1));
+            ld_off[i] = (unsigned)(((hh * BN + sigma(row >> 4, row & 15)) * (int)row_stride + 8 * q) * 2);
+        } else {
+            const int dim = 8 * j + (lane >> 3);
+            const int q = (lane & 7) ^ (dim & 7);
+            ld_off[i] = (unsigned)((dim * a.ctx_pad + hh * BN + 8 * q) * 2);
+        }
+    }
     auto stage_load = [&](int step, int kmax, unsigned char *stage) {
+        const int key0 = step * 2 * BN;
+        if (key0 + 2 * BN - 1 <= kmax) {
+            const int k_soff = key0 * (int)row_stride * 2;
+            const int v_soff = key0 * 2;
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    i < NKL ? krsrc : vrsrc, (__attribute__((address_space(3))) void *)stage_dst(stage, i), 16,
+                    (int)ld_off[i], i < NKL ? k_soff : v_soff, 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int u = wave + kWaves * i;
-            const int is_v = u / (2 * HL::NB);
-            const int hh = (u / HL::NB) & 1;
-            const int b = u % HL::NB;
-            const int key = min(step * 2 * BN + hh * BN + b + HL::NB * ld_pos, kmax);
-            const f16 *src = (is_v ? vbase : kbase) + (size_t)key * row_stride + 8 * ld_q;
-            unsigned char *dst = stage + (2 * is_v + hh) * HB + b * kGroupPitch + 16 * rho(b);
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            const int w = i < NKL ? i : i - NKL;
+            const int hh = (kWaves * w) / KH::LOADS;
+            const int j = (kWaves * w) % KH::LOADS + wave;
+            int off;
+            if (i < NKL) {
+                const int byte = 1024 * j + 16 * lane;
+                const int row = byte / KH::ROWB;
+                const int q = ((byte % KH::ROWB) >> 4) ^ (row & 15 & (KH::CPR - 1));
+                const int key = min(key0 + hh * BN + sigma(row >> 4, row & 15), kmax);
+                off = (key * (int)row_stride + 8 * q) * 2;
+            } else {
+                const int dim = 8 * j + (lane >> 3);
+                const int q = (lane & 7) ^ (dim & 7);
+                const int kc = min(key0 + hh * BN + 8 * q, kmax & ~7);
+                off = (dim * a.ctx_pad + kc) * 2;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < NKL ? krsrc : vrsrc,
+                                                     (__attribute__((address_space(3))) void *)stage_dst(stage, i),
+                                                     16, off, 0, 0, 0);
         }
     };
     auto stage_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0): this wave's loads are in LDS
 
-    // Lane-dependent parts of the operand addresses (the rest are immediates).
-    const int k_off = HL::offset(c, g);                          // K[c][chunk g]; + 16i rows, + 4kk chunks
-    const int v_key = 4 * g + (c >> 2);
-    const int v_off = HL::offset(v_key, 0) + 8 * (c & 3);        // + 16 rows (hi), 32 rows (ks), 32 B per t
+    // Lane-dependent parts of the operand addresses (tiles add immediates).
+    int k_off[KK];  // K row c of tile 0, chunk 4kk + g
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        k_off[kk] = c * KH::ROWB + 16 * ((4 * kk + g) ^ (c & (KH::CPR - 1)));
+    }
+    int v_off[2];   // V^T row c (dim c of tile 0), keys 32 ks + 8 g ..
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        v_off[ks] = c * VH::ROWB + 16 * ((4 * ks + g) ^ (c & 7));
+    }
 
     // Key split `split` of a tile takes its steps [lo, lo + cnt) (of 128 keys);
     // with one split that is every step.  A tile's first step is staged in st0.
@@ -281,15 +376,23 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                     qop[nb][kk] = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
                 }
             }
-            if (!ok) {
+            // The softmax scale log2(e)/sqrt(D) rides in the operand: q' =
+            // fp16(q * qscale), so S^T comes out in log2 units and p =
+            // exp2(s - m_ref) needs no multiply.
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    qop[nb][kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    qop[nb][kk][j] = ok ? (f16)((float)qop[nb][kk][j] * qs) : (f16)0.0f;
                 }
             }
         }
 
         float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
+        // QK^T accumulators start at -m_ref (0 while m_ref is -inf), so the
+        // MFMA results are already s - m_ref: one tile per row block, the
+        // lane's row in all four elements.
+        f32x4 negm[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
         float l[2] = {0.0f, 0.0f};               // per-lane partial row sums
         f32x4 o[2][NT];
 #pragma unroll
@@ -304,47 +407,68 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         const int wave_max_pos = a.base + wave_last_row;
         const int wave_min_pos = a.base + wr0;
 
-        // One 64-key block (keys kb0 .. kb0+63) staged at lk / lv (byte pointers).
+        // One 64-key block (keys kb0 .. kb0+63) staged at lk (K) / lv (V^T).
         // MASK: a diagonal block (some key beyond some row's position); the
         // interior variant carries no mask code, so nothing splits the QK^T
         // MFMAs from the softmax into separate scheduling regions.
         auto compute = [&](auto mask_tag, int kb0, const unsigned char *lk, const unsigned char *lv)
                            __attribute__((always_inline)) {
             constexpr bool MASK = decltype(mask_tag)::value;
-            // ---- S^T = K Q^T, keys 0-31 then 32-63 (kk inner): the row
-            // maximum of the first half is taken while the second half's MFMAs run ----
+            // ---- S^T = K Q^T, tiles 0-1 (keys 0-31) then 2-3 (keys 32-63):
+            // batch b = (key half b / KK, k-step b % KK) is two K operand reads
+            // (tiles 2hk, 2hk+1) and four MFMAs; the reads run kQkAhead batches
+            // ahead of their MFMAs so LDS latency hides under the MFMAs, and
+            // the row maximum of the first half is taken while the second
+            // half's MFMAs run ----
+            constexpr int QB = 2 * KK;
             f32x4 s[4][2];
             float mxh[2][2];  // [key half][row block]
+            f16x8 kbuf[QB][2];
+            auto kread = [&](int b) __attribute__((always_inline)) {
 #pragma unroll
-            for (int hk = 0; hk < 2; ++hk) {
+                for (int i = 0; i < 2; ++i) {
+                    kbuf[b][i] = *reinterpret_cast<const f16x8 *>(lk + k_off[b % KK] +
+                                                                  (2 * (b / KK) + i) * 16 * KH::ROWB);
+                }
+            };
 #pragma unroll
-                for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
-                    s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int b = 0; b < kQkAhead; ++b) {
+                kread(b);
+            }
+#pragma unroll
+            for (int b = 0; b < QB; ++b) {
+                const int hk = b / KK;
+                const int kk = b % KK;
+                if (b + kQkAhead < QB) {
+                    kread(b + kQkAhead);
+                }
+                if (kk == 0) {
+#pragma unroll
+                    for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
+                        s[i][0] = negm[0];
+                        s[i][1] = negm[1];
+                    }
                 }
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    f16x8 ka[2];
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        ka[i] = *reinterpret_cast<const f16x8 *>(lk + k_off + HL::offset(16 * (2 * hk + i), 4 * kk) -
-                                                                 HL::offset(0, 0));
-                    }
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        s[2 * hk + i][0] = mfma16x16x32(ka[i], qop[0][kk], s[2 * hk + i][0]);
-                        s[2 * hk + i][1] = mfma16x16x32(ka[i], qop[1][kk], s[2 * hk + i][1]);
-                    }
+                for (int i = 0; i < 2; ++i) {
+                    s[2 * hk + i][0] = mfma16x16x32(kbuf[b][i], qop[0][kk], s[2 * hk + i][0]);
+                    s[2 * hk + i][1] = mfma16x16x32(kbuf[b][i], qop[1][kk], s[2 * hk + i][1]);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // this batch's reads ahead ...
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // ... of its MFMAs
+                if (kk != KK - 1) {
+                    continue;
                 }
                 if (MASK) {
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb) {
-                        const int lim = a.base + wr0 + 16 * nb + c - kb0 - 4 * g;  // mask key offsets > lim
+                        // key of s[i][nb][r] is kb0 + 32(i/2) + 8g + 4(i%2) + r; masked past the row's position
+                        const int lim = a.base + wr0 + 16 * nb + c - kb0 - 8 * g;
 #pragma unroll
                         for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
 #pragma unroll
                             for (int r = 0; r < 4; ++r) {
-                                if (16 * i + r > lim) {
+                                if (32 * (i >> 1) + 4 * (i & 1) + r > lim) {
                                     s[i][nb][r] = -INFINITY;
                                 }
                             }
@@ -364,27 +488,47 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                     mxh[hk][nb] = m;
                 }
             }
+            f16x8 vbuf[2 * NT];
+            auto vread = [&](int b) __attribute__((always_inline)) {
+                vbuf[b] = *reinterpret_cast<const f16x8 *>(lv + v_off[b / NT] + (b % NT) * 16 * VH::ROWB);
+            };
+#pragma unroll
+            for (int b = 0; b < kPvAhead; ++b) {
+                vread(b);
+            }
             // ---- lazy online softmax per row ----
-            f16x8 pb[2][2];  // [k-step][row block]
+            f16x8 pb[2][2];  // [k-step][row block]: keys 32 ks + 8 g + j
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-                float mx = xor_max_16_32(fmaxf(mxh[0][nb], mxh[1][nb])) * qs;
-                if (__any(mx > mref[nb] + kLazyLog2)) {
-                    // A row that has seen no unmasked key keeps m_ref = -inf (its
-                    // l and O are still zero): a key half can meet such rows.
-                    const float nref = fmaxf(mref[nb], mx);
-                    const float alpha = mref[nb] == -INFINITY ? 0.0f : fast_exp2(mref[nb] - nref);
-                    mref[nb] = nref;
+                // row maximum of s - m_ref (of s itself while m_ref is -inf)
+                const float mx = xor_max_16_32(fmaxf(mxh[0][nb], mxh[1][nb]));
+                const bool first = mref[nb] == -INFINITY;
+                if (__any(mx > kLazyLog2 || (first && mx > -INFINITY))) {
+                    // A new reference: m_ref + mx (mx for a row's first
+                    // unmasked key).  A row that has seen no unmasked key keeps
+                    // m_ref = -inf (its l and O are still zero): a key half can
+                    // meet such rows.
+                    const bool move = first ? mx > -INFINITY : mx > kLazyLog2;
+                    const float shift = move ? mx : 0.0f;
+                    const float alpha = first ? 0.0f : fast_exp2(-shift);
+                    mref[nb] = first ? mx : mref[nb] + shift;
+                    negm[nb] = f32x4{-mref[nb], -mref[nb], -mref[nb], -mref[nb]};
+                    if (mref[nb] == -INFINITY) {
+                        negm[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
                     l[nb] *= alpha;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         o[nb][t] = o[nb][t] * alpha;
                     }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        s[i][nb] = s[i][nb] - shift;
+                    }
                 }
-                const float nm = mref[nb] == -INFINITY ? 0.0f : -mref[nb];  // all-masked row: p = exp2(-inf) = 0
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    pb[e >> 3][nb][e & 7] = (f16)fast_exp2(fmaf(s[e >> 2][nb][e & 3], qs, nm));
+                    pb[e >> 3][nb][e & 7] = (f16)fast_exp2(s[e >> 2][nb][e & 3]);
                 }
                 // row sum of the fp16 weights the PV product uses (v_dot2_f32_f16)
                 float psum = l[nb];
@@ -398,23 +542,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                 }
                 l[nb] = psum;
             }
-            // ---- O^T += V^T P^T ----
-            // V^T A operand of tile t (dims 16t + m) with the transposing read:
-            // source lane k of each 16-lane group reads 4 dims (16t + 4(k%4) ..)
-            // of key kmap(g, k/4) (+16 keys for the second half), and lane c
-            // receives dim 16t + c of all 8 keys.
+            // ---- O^T += V^T P^T: tile t (dims 16t .. 16t+15), k-step ks: lane
+            // (c, g) reads dim 16t + c, keys 32 ks + 8g .. +7; the first
+            // kPvAhead reads are issued before the softmax above and each
+            // later one kPvAhead MFMA pairs ahead ----
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const unsigned char *p0 = lv + v_off + HL::offset(32 * ks, 2 * t) - HL::offset(0, 0);
-                    const unsigned char *p1 = lv + v_off + HL::offset(32 * ks + 16, 2 * t) - HL::offset(0, 0);
-                    const f16x4 lo = lds_read_tr16(reinterpret_cast<const f16 *>(p0));
-                    const f16x4 hi = lds_read_tr16(reinterpret_cast<const f16 *>(p1));
-                    const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[0][t] = mfma16x16x32(va, pb[ks][0], o[0][t]);
-                    o[1][t] = mfma16x16x32(va, pb[ks][1], o[1][t]);
+            for (int b = 0; b < 2 * NT; ++b) {
+                if (b + kPvAhead < 2 * NT) {
+                    vread(b + kPvAhead);
                 }
+                o[0][b % NT] = mfma16x16x32(vbuf[b], pb[b / NT][0], o[0][b % NT]);
+                o[1][b % NT] = mfma16x16x32(vbuf[b], pb[b / NT][1], o[1][b % NT]);
             }
         };
 
@@ -435,9 +573,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             const int kb0 = (2 * (lo + j) + half) * BN;
             if (j < cnt && wave_active && kb0 <= wave_max_pos) {
                 if (kb0 + BN - 1 > wave_min_pos) {
-                    compute(std::true_type(), kb0, cur + half * HB, cur + (2 + half) * HB);  // diagonal block
+                    compute(std::true_type(), kb0, cur + half * KB, cur + 2 * KB + half * VB);  // diagonal block
                 } else {
-                    compute(std::false_type(), kb0, cur + half * HB, cur + (2 + half) * HB);
+                    compute(std::false_type(), kb0, cur + half * KB, cur + 2 * KB + half * VB);
                 }
             }
             stage_wait();
@@ -481,7 +619,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             const int row = wr0 + 16 * nb + c;
             if (row < a.tokens && a.part_o != nullptr) {
                 // key split: O relative to the row maximum mn, unnormalised, with (mn, l)
-                const size_t pi = ((size_t)blockIdx.z * a.tokens + row) * a.heads + h;
+                const size_t pi = ((size_t)zz * a.tokens + row) * a.heads + h;
                 float *prow = a.part_o + pi * D;
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
@@ -563,16 +701,98 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float *part_o,
         make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
+// V^T of positions [first, end) of every (seq*layer, kv head):
+//   vt[((sl*kv + h)*D + i)*ctx_pad + p] = v[((sl*ctx + p)*kv + h)*D + i],
+// and zeros at [end, end8) (end8 = end rounded up to 8, at most ctx_pad), so
+// the 8-key chunks the attention kernel reads past a sequence's end are
+// finite.  One workgroup per 64 aligned positions, kv head and seq*layer:
+// the rows come in as whole 16-byte chunks into LDS, the dim rows go out as
+// 16-byte chunks of 8 positions (single halves at the range's edges).
+template <int D>
+__global__ __launch_bounds__(256) void value_transpose_kernel(const f16 *v, f16 *vt, int first, int end, int end8,
+                                                              int ctx, int ctx_pad, int kv_heads) {
+    constexpr int P = 64;
+    constexpr int CPR = D / 8;
+    __shared__ __attribute__((aligned(16))) f16 tile[P][D + 8];
+    const int p0 = (first & ~(P - 1)) + P * (int)blockIdx.x;
+    const int h = blockIdx.y;
+    const size_t sl = blockIdx.z;
+    const f16 *src = v + sl * (size_t)ctx * kv_heads * D + (size_t)h * D;
+    for (int idx = threadIdx.x; idx < P * CPR; idx += 256) {
+        const int r = idx / CPR;
+        const int cq = idx % CPR;
+        const int p = p0 + r;
+        f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (p >= first && p < end) {
+            val = *reinterpret_cast<const f16x8 *>(src + (size_t)p * kv_heads * D + 8 * cq);
+        }
+        *reinterpret_cast<f16x8 *>(&tile[r][8 * cq]) = val;
+    }
+    __syncthreads();
+    f16 *dst = vt + (sl * kv_heads + h) * (size_t)D * ctx_pad;
+    for (int idx = threadIdx.x; idx < D * (P / 8); idx += 256) {
+        const int i = idx / (P / 8);
+        const int pc = idx % (P / 8);
+        const int pa = p0 + 8 * pc;
+        if (pa >= end8 || pa + 8 <= first) {
+            continue;
+        }
+        f16x8 val;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            val[j] = tile[8 * pc + j][i];
+        }
+        f16 *row = dst + (size_t)i * ctx_pad + pa;
+        if (pa >= first && pa + 8 <= end8) {
+            *reinterpret_cast<f16x8 *>(row) = val;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (pa + j >= first && pa + j < end8) {
+                    row[j] = val[j];
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
 namespace {
 
+size_t vt_pitch(size_t context_tokens) { return (context_tokens + kVtAlign - 1) / kVtAlign * kVtAlign; }
+
+size_t vt_bytes(size_t seqs, size_t layers, size_t context_tokens, size_t kv_heads, size_t head_dim) {
+    return seqs * layers * kv_heads * head_dim * vt_pitch(context_tokens) * sizeof(uint16_t);
+}
+
+te_status launch_value_transpose(const f16 *v, f16 *vt, size_t sl_count, size_t first, size_t count,
+                                 size_t context_tokens, size_t kv_heads, size_t head_dim, hipStream_t stream) {
+    const size_t pad = vt_pitch(context_tokens);
+    const size_t end = first + count;
+    const size_t end8 = std::min((end + 7) / 8 * 8, pad);
+    if (end8 <= first) {
+        return TE_STATUS_OK;
+    }
+    const size_t tiles = (end8 - (first & ~(size_t)63) + 63) / 64;
+    const dim3 grid((unsigned)tiles, (unsigned)kv_heads, (unsigned)sl_count);
+    if (head_dim == 128) {
+        value_transpose_kernel<128><<<grid, 256, 0, stream>>>(v, vt, (int)first, (int)end, (int)end8,
+                                                             (int)context_tokens, (int)pad, (int)kv_heads);
+    } else {
+        value_transpose_kernel<64><<<grid, 256, 0, stream>>>(v, vt, (int)first, (int)end, (int)end8,
+                                                            (int)context_tokens, (int)pad, (int)kv_heads);
+    }
+    return te_hip::launch_status();
+}
+
 te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t tokens, size_t base_position,
-                         size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim, void *stream) {
+                         size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim, hipStream_t strm) {
     a.layers = (int)layers;
     a.tokens = (int)tokens;
     a.base = (int)base_position;
     a.ctx = (int)context_tokens;
+    a.ctx_pad = (int)vt_pitch(context_tokens);
     a.heads = (int)heads;
     a.kv_heads = (int)kv_heads;
     a.group = (int)(heads / kv_heads);
@@ -583,7 +803,6 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
     }
     const int n_pairs = (a.n_qtiles + 1) / 2;
     const dim3 grid((unsigned)n_pairs, (unsigned)heads, (unsigned)(seqs * layers * a.splits));
-    hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
         prefill_causal_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
     } else {
@@ -656,7 +875,162 @@ te_status check_prefill_args(size_t seqs, size_t layers, size_t tokens, size_t b
     return TE_STATUS_OK;
 }
 
+// The attention over V^T with `splits` key splits (workspace = the partials),
+// then the merge launch when splits > 1.
+te_status run_prefill(PrefillArgs a, int splits, void *partials, size_t seqs, size_t layers, size_t tokens,
+                      size_t base_position, size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim,
+                      float *out, hipStream_t strm) {
+    a.out = out;
+    a.splits = splits;
+    if (splits > 1) {
+        const size_t parts = (size_t)splits * seqs * layers * tokens * heads;
+        a.part_o = static_cast<float *>(partials);
+        a.part_ml = a.part_o + parts * head_dim;
+    }
+    te_status st = launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim,
+                                  strm);
+    if (st != TE_STATUS_OK || splits == 1) {
+        return st;
+    }
+    const int items = (int)(tokens * heads);
+    const int per_block = 256 / (int)(head_dim / 4);
+    const dim3 grid((unsigned)((items + per_block - 1) / per_block), (unsigned)(seqs * layers));
+    if (head_dim == 128) {
+        prefill_merge_kernel<128><<<grid, 256, 0, strm>>>(a.part_o, a.part_ml, splits, items, out);
+    } else {
+        prefill_merge_kernel<64><<<grid, 256, 0, strm>>>(a.part_o, a.part_ml, splits, items, out);
+    }
+    return te_hip::launch_status();
+}
+
+// The split count a call with this workspace runs with: the cost model's
+// choice when the workspace holds its partials, else one split.
+int splits_for(void *workspace, size_t workspace_bytes, size_t seqs, size_t layers, size_t tokens,
+               size_t base_position, size_t heads, size_t head_dim, te_status *st) {
+    *st = TE_STATUS_OK;
+    if (workspace == nullptr) {
+        return 1;
+    }
+    const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
+    if (workspace_bytes < prefill_workspace(splits, seqs, layers, tokens, heads, head_dim)) {
+        *st = TE_STATUS_INVALID_ARGUMENT;
+    }
+    return splits;
+}
+
 }  // namespace
+
+extern "C" size_t te_hip_value_t_bytes(size_t seqs, size_t layers, size_t context_tokens, size_t kv_heads,
+                                       size_t head_dim) {
+    if (seqs == 0 || layers == 0 || context_tokens == 0 || kv_heads == 0 || head_dim == 0) {
+        return 0;
+    }
+    return vt_bytes(seqs, layers, context_tokens, kv_heads, head_dim);
+}
+
+extern "C" te_status te_hip_value_transpose_f16(const uint16_t *value_cache, uint16_t *value_cache_t, size_t seqs,
+                                                size_t layers, size_t first_position, size_t count,
+                                                size_t context_tokens, size_t kv_heads, size_t head_dim,
+                                                void *stream) {
+    if (value_cache == nullptr || value_cache_t == nullptr || seqs == 0 || layers == 0 || context_tokens == 0 ||
+        kv_heads == 0 || head_dim == 0 || first_position > context_tokens ||
+        count > context_tokens - first_position) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if ((head_dim != 64 && head_dim != 128) || context_tokens * kv_heads * head_dim * 2 >= ((size_t)1 << 31) ||
+        seqs * layers > 65535 || kv_heads > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    if (count == 0) {
+        return TE_STATUS_OK;
+    }
+    return launch_value_transpose(reinterpret_cast<const f16 *>(value_cache), reinterpret_cast<f16 *>(value_cache_t),
+                                  seqs * layers, first_position, count, context_tokens, kv_heads, head_dim,
+                                  te_hip::as_stream(stream));
+}
+
+extern "C" size_t te_hip_attention_prefill_vt_workspace_bytes(size_t seqs, size_t layers, size_t tokens,
+                                                             size_t base_position, size_t context_tokens,
+                                                             size_t heads, size_t kv_heads, size_t head_dim) {
+    if (check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim) !=
+        TE_STATUS_OK) {
+        return 0;
+    }
+    const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
+    return prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
+}
+
+extern "C" te_status te_hip_attention_prefill_vt_f16(
+    const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache_t,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    if (q_half == nullptr || key_cache == nullptr || value_cache_t == nullptr || out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_status st = check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    const int splits = splits_for(workspace, workspace_bytes, seqs, layers, tokens, base_position, heads, head_dim,
+                                  &st);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    PrefillArgs a = {};
+    a.q = reinterpret_cast<const f16 *>(q_half);
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_t = reinterpret_cast<const f16 *>(value_cache_t);
+    return run_prefill(a, splits, workspace, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads,
+                       head_dim, out, te_hip::as_stream(stream));
+}
+
+extern "C" te_status te_hip_attention_prefill_step_vt_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *value_cache_t,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    if (query == nullptr || k_new == nullptr || v_new == nullptr || rope_cos == nullptr || rope_sin == nullptr ||
+        key_cache == nullptr || value_cache == nullptr || value_cache_t == nullptr || out == nullptr) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    te_status st = check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    if (seqs > TE_HIP_MAX_SEQS || tokens > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    const int splits = splits_for(workspace, workspace_bytes, seqs, layers, tokens, base_position, heads, head_dim,
+                                  &st);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    hipStream_t strm = te_hip::as_stream(stream);
+    st = te_hip::launch_kv_append(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache, seqs,
+                                  layers, tokens, base_position, context_tokens, kv_heads, head_dim, strm);
+    if (st == TE_STATUS_OK) {
+        st = launch_value_transpose(reinterpret_cast<const f16 *>(value_cache), reinterpret_cast<f16 *>(value_cache_t),
+                                    seqs * layers, base_position, tokens, context_tokens, kv_heads, head_dim, strm);
+    }
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    PrefillArgs a = {};
+    a.q32 = query;
+    a.q_bias = q_bias;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.key_cache = reinterpret_cast<const f16 *>(key_cache);
+    a.value_t = reinterpret_cast<const f16 *>(value_cache_t);
+    return run_prefill(a, splits, workspace, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads,
+                       head_dim, out, strm);
+}
+
+// ---- entry points over the plain value cache: V^T is built per call --------
 
 extern "C" te_status te_hip_attention_prefill_f16(
     const uint16_t *q_half, const uint16_t *key_cache, const uint16_t *value_cache,
@@ -670,12 +1044,27 @@ extern "C" te_status te_hip_attention_prefill_f16(
     if (st != TE_STATUS_OK) {
         return st;
     }
+    // V^T of positions 0 .. base + tokens in a library-owned buffer: whole
+    // calls are serialized on it (calls must share one stream).
+    std::lock_guard<std::mutex> lock(te_hip::library_mutex());
+    void *vt = nullptr;
+    st = te_hip::library_buffer(te_hip::kLibBufPrefillVt, vt_bytes(seqs, layers, context_tokens, kv_heads, head_dim),
+                                &vt);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    hipStream_t strm = te_hip::as_stream(stream);
+    st = launch_value_transpose(reinterpret_cast<const f16 *>(value_cache), static_cast<f16 *>(vt), seqs * layers, 0,
+                                base_position + tokens, context_tokens, kv_heads, head_dim, strm);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
     PrefillArgs a = {};
     a.q = reinterpret_cast<const f16 *>(q_half);
     a.key_cache = reinterpret_cast<const f16 *>(key_cache);
-    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
-    a.out = out;
-    return launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
+    a.value_t = static_cast<const f16 *>(vt);
+    return run_prefill(a, 1, nullptr, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim,
+                       out, strm);
 }
 
 extern "C" size_t te_hip_attention_prefill_workspace_bytes(size_t seqs, size_t layers, size_t tokens,
@@ -686,7 +1075,8 @@ extern "C" size_t te_hip_attention_prefill_workspace_bytes(size_t seqs, size_t l
         return 0;
     }
     const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
-    return prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
+    return prefill_workspace(splits, seqs, layers, tokens, heads, head_dim) +
+           vt_bytes(seqs, layers, context_tokens, kv_heads, head_dim);
 }
 
 extern "C" te_status te_hip_attention_prefill_split_f16(
@@ -701,36 +1091,27 @@ extern "C" te_status te_hip_attention_prefill_split_f16(
     if (st != TE_STATUS_OK) {
         return st;
     }
-    const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
-    const size_t need = prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    if (workspace == nullptr) {
         return TE_STATUS_INVALID_ARGUMENT;
+    }
+    const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
+    const size_t part = prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
+    if (workspace_bytes < part + vt_bytes(seqs, layers, context_tokens, kv_heads, head_dim)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    f16 *vt = reinterpret_cast<f16 *>(static_cast<unsigned char *>(workspace) + part);
+    hipStream_t strm = te_hip::as_stream(stream);
+    st = launch_value_transpose(reinterpret_cast<const f16 *>(value_cache), vt, seqs * layers, 0,
+                                base_position + tokens, context_tokens, kv_heads, head_dim, strm);
+    if (st != TE_STATUS_OK) {
+        return st;
     }
     PrefillArgs a = {};
     a.q = reinterpret_cast<const f16 *>(q_half);
     a.key_cache = reinterpret_cast<const f16 *>(key_cache);
-    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
-    a.out = out;
-    a.splits = splits;
-    if (splits > 1) {
-        const size_t parts = (size_t)splits * seqs * layers * tokens * heads;
-        a.part_o = static_cast<float *>(workspace);
-        a.part_ml = a.part_o + parts * head_dim;
-    }
-    st = launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
-    if (st != TE_STATUS_OK || splits == 1) {
-        return st;
-    }
-    const int items = (int)(tokens * heads);
-    const int per_block = 256 / (int)(head_dim / 4);
-    const dim3 grid((unsigned)((items + per_block - 1) / per_block), (unsigned)(seqs * layers));
-    hipStream_t strm = te_hip::as_stream(stream);
-    if (head_dim == 128) {
-        prefill_merge_kernel<128><<<grid, 256, 0, strm>>>(a.part_o, a.part_ml, splits, items, out);
-    } else {
-        prefill_merge_kernel<64><<<grid, 256, 0, strm>>>(a.part_o, a.part_ml, splits, items, out);
-    }
-    return te_hip::launch_status();
+    a.value_t = vt;
+    return run_prefill(a, splits, workspace, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads,
+                       head_dim, out, strm);
 }
 
 extern "C" te_status te_hip_attention_prefill_step_f16(
@@ -751,9 +1132,20 @@ extern "C" te_status te_hip_attention_prefill_step_f16(
     if (seqs > TE_HIP_MAX_SEQS || tokens > 65535) {
         return TE_STATUS_UNSUPPORTED;
     }
+    std::lock_guard<std::mutex> lock(te_hip::library_mutex());
+    void *vt = nullptr;
+    st = te_hip::library_buffer(te_hip::kLibBufPrefillVt, vt_bytes(seqs, layers, context_tokens, kv_heads, head_dim),
+                                &vt);
+    if (st != TE_STATUS_OK) {
+        return st;
+    }
+    hipStream_t strm = te_hip::as_stream(stream);
     st = te_hip::launch_kv_append(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache, seqs,
-                                  layers, tokens, base_position, context_tokens, kv_heads, head_dim,
-                                  te_hip::as_stream(stream));
+                                  layers, tokens, base_position, context_tokens, kv_heads, head_dim, strm);
+    if (st == TE_STATUS_OK) {
+        st = launch_value_transpose(reinterpret_cast<const f16 *>(value_cache), static_cast<f16 *>(vt), seqs * layers,
+                                    0, base_position + tokens, context_tokens, kv_heads, head_dim, strm);
+    }
     if (st != TE_STATUS_OK) {
         return st;
     }
@@ -763,7 +1155,7 @@ extern "C" te_status te_hip_attention_prefill_step_f16(
     a.rope_cos = rope_cos;
     a.rope_sin = rope_sin;
     a.key_cache = reinterpret_cast<const f16 *>(key_cache);
-    a.value_cache = reinterpret_cast<const f16 *>(value_cache);
-    a.out = out;
-    return launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim, stream);
+    a.value_t = static_cast<const f16 *>(vt);
+    return run_prefill(a, 1, nullptr, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim,
+                       out, strm);
 }

@@ -203,6 +203,13 @@ def _configure_library(lib: ctypes.CDLL) -> None:
          [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _szp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp])
     _sig(lib, "te_hip_attention_decode_chunking", [_szp, _sz, _sz, _sz, _sz, _int, _szp, _szp])
     _sig(lib, "te_hip_attention_prefill_f16", [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp])
+    _sig(lib, "te_hip_value_t_bytes", [_sz] * 5, _sz)
+    _sig(lib, "te_hip_value_transpose_f16", [_vp, _vp] + [_sz] * 7 + [_vp])
+    _sig(lib, "te_hip_attention_prefill_vt_workspace_bytes", [_sz] * 8, _sz)
+    _sig(lib, "te_hip_attention_prefill_vt_f16",
+         [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _vp])
+    _sig(lib, "te_hip_attention_prefill_step_vt_f16",
+         [_vp] * 11 + [_sz] * 8 + [_vp, _vp, _sz, _vp])
     _sig(lib, "te_hip_attention_prefill_workspace_bytes", [_sz] * 8, _sz)
     _sig(lib, "te_hip_attention_prefill_split_f16",
          [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _vp])
