@@ -780,3 +780,34 @@ def test_prefill_step_vt_matches_plain_step(seqs, layers, h, kv, d, tokens, base
     err = float((split - ref).abs().max())
     print(f"fused step V^T H{h} d{d} L{tokens} base{base}: split vs one split {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("growth", [0.0, 0.02, 0.1, 0.2])
+def test_prefill_rising_scores_rescale(oracle_mod, growth):
+    """Scores that keep rising along the keys (key p scaled by 1 + growth * p /
+    16, q = k direction shared), so later blocks exceed an earlier reference by
+    far more than 2^16 in the weights: the exact rescale path must run, with
+    and without a key split, and every row must still match the oracle."""
+    h, kv, d, tokens, base = 4, 1, 128, 300, 20
+    ctx = base + tokens
+    g = np.random.default_rng(5)
+    dirn = g.standard_normal(d).astype(np.float32)
+    dirn /= np.linalg.norm(dirn)
+    k = (g.standard_normal((ctx, kv, d)) * 0.3 + dirn * 8.0).astype(np.float32)
+    k *= (1.0 + growth * np.arange(ctx, dtype=np.float32) / 16.0)[:, None, None]
+    v = g.standard_normal((ctx, kv, d)).astype(np.float32)
+    q = (g.standard_normal((tokens, h, d)) * 0.3 + dirn * 8.0).astype(np.float32)
+    kc, vc, q16 = S.to_f16_bits(k), S.to_f16_bits(v), S.to_f16_bits(q)
+    want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q16), kc, vc, tokens, base, ctx, h, kv, d)
+    qd = f16_dev(q16.reshape(1, 1, tokens, h, d))
+    kd = f16_dev(kc.reshape(1, 1, ctx, kv, d))
+    vd = f16_dev(vc.reshape(1, 1, ctx, kv, d))
+    vt = A.value_t_buffer(1, 1, ctx, kv, d)
+    A.value_transpose(vd, vt)
+    ws = A.prefill_vt_workspace(1, 1, tokens, h, kv, d, base_position=base, context_tokens=ctx)
+    one = A.attention_prefill_vt(qd, kd, vt, base_position=base).cpu().numpy().reshape(tokens, h, d)
+    split = A.attention_prefill_vt(qd, kd, vt, base_position=base, workspace=ws).cpu().numpy().reshape(tokens, h, d)
+    assert np.isfinite(one).all() and np.isfinite(split).all()
+    err = max(maxabs(one, want), maxabs(split, want))
+    print(f"prefill rising scores (growth {growth}): max abs err {err:.3e}")
+    assert err <= TOL
