@@ -465,6 +465,79 @@ TE_API te_status te_hip_decode_all_layers_f16(
     uint32_t *out_token_id, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * One decode token through one layer: te_hip_decode_all_layers_f16 with
+ * layers == 1 and the layer's offsets, norms, biases and cache slice passed
+ * directly -- the twin of te_metal_decode_layer_f32 (metal_backend.h:206-237,
+ * called per layer by qwen.c:1392-1462), without the head.  The workspace is
+ * sized by te_hip_decode_all_layers_workspace_bytes(position, ..., vocab 0).
+ */
+TE_API te_status te_hip_decode_layer_f16(
+    const void *mapping, size_t mapping_len,
+    uint64_t q_offset, uint64_t k_offset, uint64_t v_offset, uint64_t output_offset,
+    uint64_t gate_offset, uint64_t up_offset, uint64_t down_offset, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weight, const float *ffn_norm_weight,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin, uint16_t *key_cache, uint16_t *value_cache,
+    size_t position, size_t context_tokens, size_t hidden, size_t kv, size_t heads, size_t kv_heads,
+    size_t head_dim, size_t ffn, float epsilon, float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * A chunk of `batch` prompt tokens at positions base_position .. base_position
+ * + batch - 1 through every layer: replaces te_metal_prefill_all_layers_f32
+ * (metal_backend.h:311-343, called by te_qwen_prefill_all_layers_exact,
+ * qwen.c:1640-1797), with the same arguments and per-layer order, and the
+ * result of the per-token CPU loop for each row (qwen.c:774-824: row t is
+ * decode at position base_position + t).  Differences from the Metal slot,
+ * all device-resident:
+ *   - hidden_in / out are [batch][hidden] (out may equal hidden_in); out gets
+ *     every row's final hidden state;
+ *   - key_cache / value_cache are the fp16 caches [layers][context_tokens][kv],
+ *     and value_cache_t their transposed value copy [layers][kv_heads]
+ *     [head_dim][ctx_pad] (te_hip_value_t_bytes(1, layers, ...)), which must
+ *     hold positions 0 .. base_position - 1 (te_hip_value_transpose_f16 builds
+ *     it from value_cache); the chunk's k / v go to all three;
+ *   - base_position (the reference always starts at 0) allows chunked
+ *     prefill after a cached prefix;
+ *   - mapping, offsets, rope tables as te_hip_decode_all_layers_f16;
+ *   - workspace: te_hip_prefill_all_layers_workspace_bytes(batch, hidden, kv,
+ *     ffn) bytes, 256-byte aligned.
+ * The projections are the batched-prefill GEMM (te_hip_gemm_q_f32: each
+ * activation row rounded per 32-value block to 15 bits of its largest
+ * magnitude, exact int8 MFMA products); the attention is
+ * te_hip_attention_prefill_step_vt_f16.  Asynchronous on `stream`.  Checks as
+ * te_hip_decode_all_layers_f16; Q4_0 / Q8_0 layer weights at 2-byte aligned
+ * addresses only (other types or alignments -> UNSUPPORTED, the reference's
+ * cue to take the per-token path); batch <= 65535.
+ */
+TE_API size_t te_hip_prefill_all_layers_workspace_bytes(size_t batch, size_t hidden, size_t kv, size_t ffn);
+TE_API te_status te_hip_prefill_all_layers_f16(
+    const void *mapping, size_t mapping_len,
+    const uint64_t *q_offsets, const uint64_t *k_offsets, const uint64_t *v_offsets,
+    const uint64_t *output_offsets, const uint64_t *gate_offsets, const uint64_t *up_offsets,
+    const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weights, const float *ffn_norm_weights,
+    const float *q_biases, const float *k_biases, const float *v_biases,
+    const float *rope_cos, const float *rope_sin, uint16_t *key_cache, uint16_t *value_cache,
+    uint16_t *value_cache_t, size_t base_position, size_t batch, size_t context_tokens, size_t hidden, size_t kv,
+    size_t heads, size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out,
+    void *workspace, size_t workspace_bytes, void *stream);
+
+/* One layer of the chunk: te_hip_prefill_all_layers_f16 with layers == 1 and
+ * the layer's arguments passed directly -- the twin of
+ * te_metal_prefill_layer_f32 (metal_backend.h:278-309, called per layer by
+ * qwen.c:1799-1870). */
+TE_API te_status te_hip_prefill_layer_f16(
+    const void *mapping, size_t mapping_len,
+    uint64_t q_offset, uint64_t k_offset, uint64_t v_offset, uint64_t output_offset,
+    uint64_t gate_offset, uint64_t up_offset, uint64_t down_offset, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weight, const float *ffn_norm_weight,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin, uint16_t *key_cache, uint16_t *value_cache,
+    uint16_t *value_cache_t, size_t base_position, size_t batch, size_t context_tokens, size_t hidden, size_t kv,
+    size_t heads, size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out,
+    void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Measurement only, no counterpart in the reference: `blocks` workgroups of 8
  * waves each run `iters` rounds of 8 independent fp16 16x16x32 MFMAs on
  * register operands (blocks*8*iters*8*16384 FLOP), so a benchmark can report

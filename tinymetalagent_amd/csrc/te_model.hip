@@ -1142,15 +1142,19 @@ struct te_context {
     std::vector<void *> allocations;
     // the tokens whose K / V fill cache positions 0 .. history.size() - 1
     std::vector<uint32_t> history;
-    // batched prompt prefill: chunk rows of hidden states, projections,
-    // attention output, gate / up, the GEMM's activation digits, token ids
+    // batched prompt prefill: chunk rows of hidden states, token ids, the
+    // layer flow's workspace, and the transposed value copy V^T the prefill
+    // attention reads, current for positions 0 .. vt_valid - 1 (the decode
+    // path appends to the value cache only; a prefill chunk first brings V^T
+    // up to its base position)
     bool batch_ok = false;
     size_t chunk = 0;
-    float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *patt = nullptr, *pg = nullptr, *pu = nullptr;
-    void *pact = nullptr;
+    float *px = nullptr;
     uint32_t *pids = nullptr;
-    float *ppart = nullptr;  // split-K partial sums
-    size_t ppart_bytes = 0;
+    void *pws = nullptr;
+    size_t pws_bytes = 0;
+    uint16_t *vt = nullptr;
+    size_t vt_valid = 0;
 };
 
 namespace {
@@ -1161,6 +1165,7 @@ void release_state(te_context *c) {
     }
     c->allocations.clear();
     c->history.clear();
+    c->vt_valid = 0;
     c->ready = false;
 }
 
@@ -1324,21 +1329,21 @@ te_status init_state(te_context *c) {
     if (c->batch_ok) {
         c->chunk = std::min<size_t>(512, c->ctx);
         const size_t ch = c->chunk;
-        unsigned char *act = nullptr;
+        const size_t vt_bytes = te_hip_value_t_bytes(1, c->layers, c->ctx, c->kv_heads, c->head_dim);
+        c->pws_bytes = te_hip_prefill_all_layers_workspace_bytes(ch, c->hidden, c->kv, c->ffn);
+        unsigned char *pws = nullptr;
         if ((s = dev_alloc(c, &c->px, ch * c->hidden)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->pq, ch * c->hidden)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->pk, ch * c->kv)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->pv, ch * c->kv)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->patt, ch * c->hidden)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->pg, ch * c->ffn)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->pu, ch * c->ffn)) != TE_STATUS_OK ||
             (s = dev_alloc(c, &c->pids, ch)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &c->ppart, 8 * ch * c->hidden)) != TE_STATUS_OK ||
-            (s = dev_alloc(c, &act, te_hip::act_buffer_bytes(ch, std::max(c->hidden, c->ffn)))) != TE_STATUS_OK) {
+            (s = dev_alloc(c, &pws, c->pws_bytes)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &c->vt, vt_bytes / sizeof(uint16_t))) != TE_STATUS_OK) {
             return s;
         }
-        c->pact = act;
-        c->ppart_bytes = 8 * ch * c->hidden * sizeof(float);
+        c->pws = pws;
+        // V^T positions past a sequence must be finite: start from zeros
+        if (hipMemset(c->vt, 0, vt_bytes) != hipSuccess) {
+            return TE_STATUS_RUNTIME_ERROR;
+        }
+        c->vt_valid = 0;
     }
     c->ready = true;
     return TE_STATUS_OK;
@@ -1346,16 +1351,21 @@ te_status init_state(te_context *c) {
 
 // Prompt tokens ids[start .. end) at positions start .. end - 1, `chunk` rows
 // at a time through every layer (te_qwen_prefill_prompt_batch,
-// qwen.c:630-905): per layer RMSNorm + Q / K / V GEMMs, bias + RoPE + fp16
-// append + causal MFMA attention from the chunk's base position
-// (te_hip_attention_prefill_step_f16), Wo GEMM + residual, RMSNorm + gate / up
-// GEMMs, SwiGLU + down GEMM + residual.  The last row's hidden state is left
-// in hidden_buf.
+// qwen.c:630-905) by te_hip_prefill_all_layers_f16: per layer RMSNorm + Q / K
+// / V GEMMs, bias + RoPE + fp16 append + causal MFMA attention from the
+// chunk's base position, Wo GEMM + residual, RMSNorm + gate / up GEMMs,
+// SwiGLU + down GEMM + residual.  TINYENGINE_PREFILL_ALL_LAYERS=0 runs the
+// same flow one layer per call (te_hip_prefill_layer_f16), as the reference's
+// switch selects its per-layer Metal path (qwen.c:1646-1649).  The last row's
+// hidden state is left in hidden_buf.
 te_status prefill_batch(te_context *c, const uint32_t *ids, size_t start, size_t end) {
     te_model *m = c->model;
     const unsigned char *base = m->d_mapping;
     const float eps = m->info.rms_norm_epsilon;
-    const size_t H = c->hidden, KV = c->kv, F = c->ffn;
+    const size_t H = c->hidden;
+    const char *all = getenv("TINYENGINE_PREFILL_ALL_LAYERS");
+    const bool per_layer = all != nullptr && strcmp(all, "0") == 0;
+    const size_t vt_layer = te_hip_value_t_bytes(1, 1, c->ctx, c->kv_heads, c->head_dim) / sizeof(uint16_t);
     te_status s = TE_STATUS_OK;
     for (size_t p0 = start; p0 < end && s == TE_STATUS_OK; p0 += c->chunk) {
         const size_t M = std::min(c->chunk, end - p0);
@@ -1363,35 +1373,40 @@ te_status prefill_batch(te_context *c, const uint32_t *ids, size_t start, size_t
             return TE_STATUS_RUNTIME_ERROR;
         }
         s = te_hip::launch_dequant_rows(base + c->embd_off, c->embd_type, H, c->pids, M, c->px, nullptr);
-        for (size_t l = 0; l < c->layers && s == TE_STATUS_OK; ++l) {
-            auto gemm = [&](int w, size_t n, size_t k, float *out, const float *resid) {
-                return te_hip::launch_gemm_q(base + c->offs[w][l], c->type, c->pact, M, n, k, out, resid, c->ppart,
-                                             c->ppart_bytes, nullptr);
-            };
-            const size_t kv_off = l * c->ctx * KV;
-            if ((s = te_hip::launch_quant_act(1, c->px, nullptr, c->attn_norm + l * H, eps, M, H, c->pact,
-                                              nullptr)) != TE_STATUS_OK ||
-                (s = gemm(0, H, H, c->pq, nullptr)) != TE_STATUS_OK ||
-                (s = gemm(1, KV, H, c->pk, nullptr)) != TE_STATUS_OK ||
-                (s = gemm(2, KV, H, c->pv, nullptr)) != TE_STATUS_OK ||
-                (s = te_hip_attention_prefill_step_f16(c->pq, c->pk, c->pv, c->qb + l * H, c->kb + l * KV,
-                                                       c->vb + l * KV, c->cos, c->sin, c->kc + kv_off,
-                                                       c->vc + kv_off, 1, 1, M, p0, c->ctx, c->heads, c->kv_heads,
-                                                       c->head_dim, c->patt, nullptr)) != TE_STATUS_OK ||
-                (s = te_hip::launch_quant_act(0, c->patt, nullptr, nullptr, 0.0f, M, H, c->pact, nullptr)) !=
-                    TE_STATUS_OK ||
-                (s = gemm(3, H, H, c->px, c->px)) != TE_STATUS_OK ||
-                (s = te_hip::launch_quant_act(1, c->px, nullptr, c->ffn_norm + l * H, eps, M, H, c->pact,
-                                              nullptr)) != TE_STATUS_OK ||
-                (s = gemm(4, F, H, c->pg, nullptr)) != TE_STATUS_OK ||
-                (s = gemm(5, F, H, c->pu, nullptr)) != TE_STATUS_OK ||
-                (s = te_hip::launch_quant_act(2, c->pg, c->pu, nullptr, 0.0f, M, F, c->pact, nullptr)) !=
-                    TE_STATUS_OK ||
-                (s = gemm(6, H, F, c->px, c->px)) != TE_STATUS_OK) {
-                break;
+        if (s == TE_STATUS_OK && c->vt_valid < p0) {
+            // positions the decode path appended since V^T was last current
+            s = te_hip_value_transpose_f16(c->vc, c->vt, 1, c->layers, c->vt_valid, p0 - c->vt_valid, c->ctx,
+                                           c->kv_heads, c->head_dim, nullptr);
+        }
+        if (s != TE_STATUS_OK) {
+            break;
+        }
+        const uint64_t *o[7];
+        for (int w = 0; w < 7; ++w) {
+            o[w] = c->offs[w].data();
+        }
+        if (!per_layer) {
+            s = te_hip_prefill_all_layers_f16(base, m->mapping_len, o[0], o[1], o[2], o[3], o[4], o[5], o[6],
+                                              c->layers, c->type, c->px, c->attn_norm, c->ffn_norm, c->qb, c->kb,
+                                              c->vb, c->cos, c->sin, c->kc, c->vc, c->vt, p0, M, c->ctx, H, c->kv,
+                                              c->heads, c->kv_heads, c->head_dim, c->ffn, eps, c->px, c->pws,
+                                              c->pws_bytes, nullptr);
+        } else {
+            const size_t ckv = c->ctx * c->kv;
+            for (size_t l = 0; l < c->layers && s == TE_STATUS_OK; ++l) {
+                s = te_hip_prefill_layer_f16(base, m->mapping_len, o[0][l], o[1][l], o[2][l], o[3][l], o[4][l],
+                                             o[5][l], o[6][l], c->type, c->px, c->attn_norm + l * H,
+                                             c->ffn_norm + l * H, c->qb + l * H, c->kb + l * c->kv, c->vb + l * c->kv,
+                                             c->cos, c->sin, c->kc + l * ckv, c->vc + l * ckv, c->vt + l * vt_layer,
+                                             p0, M, c->ctx, H, c->kv, c->heads, c->kv_heads, c->head_dim, c->ffn,
+                                             eps, c->px, c->pws, c->pws_bytes, nullptr);
             }
         }
-        if (s == TE_STATUS_OK && p0 + M == end &&
+        if (s != TE_STATUS_OK) {
+            break;
+        }
+        c->vt_valid = p0 + M;
+        if (p0 + M == end &&
             hipMemcpy(c->hidden_buf, c->px + (M - 1) * H, H * sizeof(float), hipMemcpyDeviceToDevice) !=
                 hipSuccess) {
             s = TE_STATUS_RUNTIME_ERROR;
@@ -1612,6 +1627,7 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         }
     }
     c->history.resize(start);
+    c->vt_valid = std::min(c->vt_valid, start);
     // several new prompt tokens go through the batched prefill unless
     // TINYENGINE_BATCH_PREFILL=0 (the reference's switch, qwen.c:346-347)
     const char *bp = getenv("TINYENGINE_BATCH_PREFILL");
@@ -1633,6 +1649,7 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         }
     }
     if (!batched) {
+        c->vt_valid = std::min(c->vt_valid, start);  // the per-token path appends to the value cache only
         for (size_t i = start; i < ids.size(); ++i) {
             if ((s = forward(c, ids[i], i, greedy && i + 1 == ids.size())) != TE_STATUS_OK) {
                 c->history.clear();

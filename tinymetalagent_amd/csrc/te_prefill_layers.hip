@@ -1,0 +1,200 @@
+// A chunk of prompt tokens through every layer of a Qwen2 model on the GPU:
+// the HIP twin of the reference's te_metal_prefill_all_layers_f32
+// (c/src/metal_backend.h:311-343), which te_qwen_prefill_all_layers_exact
+// calls for a whole prompt (qwen.c:1640-1797).  Row t of the chunk is the
+// token at position base_position + t; per layer, for all rows at once:
+//
+//   norm = rmsnorm(x, attn_norm[l])                               (te_rmsnorm_f32)
+//   q, k, v = norm Wq^T + bq, norm Wk^T + bk, norm Wv^T + bv; RoPE q, k; append k, v
+//   attn = causal attention: row t over positions 0 .. base + t  (qwen.c:810-824)
+//   x += attn Wo^T
+//   norm = rmsnorm(x, ffn_norm[l])
+//   x += (silu(norm Wg^T) * (norm Wu^T)) Wd^T                     (te_swiglu_f32)
+//
+// Launches per layer (one stream, no host synchronisation): the GEMM's
+// activation digits with RMSNorm folded in, then the Q, K and V GEMMs
+// (te_gemm.hip); the fused prefill step keeping V^T (bias + RoPE + fp16
+// append into the K / V caches and V^T, then the MFMA causal attention,
+// te_prefill.hip); the digits of the attention output and the Wo GEMM with
+// the residual in its epilogue; RMSNorm digits, gate and up GEMMs; SwiGLU
+// digits and the down GEMM with the residual.
+//
+// Differences from the Metal slot, all device-resident: the K / V caches are
+// the HIP path's fp16 caches [layers][context_tokens][kv] plus the transposed
+// value copy V^T [layers][kv_heads][head_dim][ctx_pad] the prefill kernel
+// reads; the chunk starts at base_position (the reference always starts at 0,
+// metal_backend_layers.mm.inc:2205-2222); the weights are the model file's
+// bytes in HBM at the reference's absolute tensor offsets.
+#include "te_hip_common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+struct ChunkBuffers {
+    float *q, *k, *v, *attn, *gate, *up, *part;
+    void *act;
+    size_t part_bytes;
+};
+
+// Byte layout of the workspace, in carve-up order: the GEMM outputs, the
+// split-K partial sums (up to 8 splits of a hidden-wide output), the
+// activation digits.
+size_t carve(size_t batch, size_t hidden, size_t kv, size_t ffn, unsigned char *base, ChunkBuffers *b) {
+    const size_t floats[7] = {batch * hidden, batch * kv, batch * kv, batch * hidden, batch * ffn, batch * ffn,
+                              8 * batch * hidden};
+    float **slots[7] = {&b->q, &b->k, &b->v, &b->attn, &b->gate, &b->up, &b->part};
+    size_t off = 0;
+    for (int i = 0; i < 7; ++i) {
+        if (base != nullptr) {
+            *slots[i] = reinterpret_cast<float *>(base + off);
+        }
+        off += align_up(floats[i] * sizeof(float));
+    }
+    if (base != nullptr) {
+        b->act = base + off;
+        b->part_bytes = floats[6] * sizeof(float);
+    }
+    return off + align_up(te_hip::act_buffer_bytes(batch, std::max(hidden, ffn)));
+}
+
+bool tensor_fits(uint64_t offset, size_t rows, size_t row_bytes, size_t mapping_len) {
+    return row_bytes != 0 && rows <= mapping_len / row_bytes && offset <= mapping_len - rows * row_bytes;
+}
+
+}  // namespace
+
+extern "C" size_t te_hip_prefill_all_layers_workspace_bytes(size_t batch, size_t hidden, size_t kv, size_t ffn) {
+    if (batch == 0 || hidden == 0 || kv == 0 || ffn == 0) {
+        return 0;
+    }
+    return carve(batch, hidden, kv, ffn, nullptr, nullptr);
+}
+
+extern "C" te_status te_hip_prefill_all_layers_f16(
+    const void *mapping, size_t mapping_len, const uint64_t *q_offsets, const uint64_t *k_offsets,
+    const uint64_t *v_offsets, const uint64_t *output_offsets, const uint64_t *gate_offsets,
+    const uint64_t *up_offsets, const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weights, const float *ffn_norm_weights, const float *q_biases,
+    const float *k_biases, const float *v_biases, const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *value_cache_t, size_t base_position, size_t batch,
+    size_t context_tokens, size_t hidden, size_t kv, size_t heads, size_t kv_heads, size_t head_dim, size_t ffn,
+    float epsilon, float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    // the reference's argument checks (qwen.c:1650-1652, metal_backend.mm)
+    if (mapping == nullptr || q_offsets == nullptr || k_offsets == nullptr || v_offsets == nullptr ||
+        output_offsets == nullptr || gate_offsets == nullptr || up_offsets == nullptr || down_offsets == nullptr ||
+        hidden_in == nullptr || attn_norm_weights == nullptr || ffn_norm_weights == nullptr || q_biases == nullptr ||
+        k_biases == nullptr || v_biases == nullptr || rope_cos == nullptr || rope_sin == nullptr ||
+        key_cache == nullptr || value_cache == nullptr || value_cache_t == nullptr || out == nullptr ||
+        workspace == nullptr || layers == 0 || batch == 0 || hidden == 0 || kv == 0 || heads == 0 ||
+        kv_heads == 0 || head_dim == 0 || ffn == 0 || context_tokens == 0 || base_position > context_tokens ||
+        batch > context_tokens - base_position || epsilon <= 0.0f) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (hidden != heads * head_dim || kv != kv_heads * head_dim || heads % kv_heads != 0 ||
+        (head_dim != 64 && head_dim != 128) || (ggml_type != 2 && ggml_type != 8) || hidden % 32 != 0 ||
+        ffn % 32 != 0 || batch > 65535 || context_tokens > (1u << 30)) {
+        return TE_STATUS_UNSUPPORTED;  // the GEMM takes Q4_0 / Q8_0 rows of whole blocks
+    }
+    const size_t rb_hidden = te_hip::ggml_row_bytes(ggml_type, hidden);
+    const size_t rb_ffn = te_hip::ggml_row_bytes(ggml_type, ffn);
+    const unsigned char *m = static_cast<const unsigned char *>(mapping);
+    for (size_t l = 0; l < layers; ++l) {
+        const struct {
+            uint64_t off;
+            size_t rows, row_bytes;
+        } t[7] = {{q_offsets[l], hidden, rb_hidden},     {k_offsets[l], kv, rb_hidden},
+                  {v_offsets[l], kv, rb_hidden},         {output_offsets[l], hidden, rb_hidden},
+                  {gate_offsets[l], ffn, rb_hidden},     {up_offsets[l], ffn, rb_hidden},
+                  {down_offsets[l], hidden, rb_ffn}};
+        for (const auto &e : t) {
+            if (!tensor_fits(e.off, e.rows, e.row_bytes, mapping_len)) {
+                return TE_STATUS_INVALID_ARGUMENT;
+            }
+            if (((size_t)(m + e.off) & 1u) != 0) {
+                return TE_STATUS_UNSUPPORTED;  // the GEMM reads 16-bit words of the blocks
+            }
+        }
+    }
+    if (((size_t)workspace & (kAlign - 1)) != 0) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    ChunkBuffers b = {};
+    if (workspace_bytes < carve(batch, hidden, kv, ffn, static_cast<unsigned char *>(workspace), &b)) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    const hipStream_t st = te_hip::as_stream(stream);
+    if (out != hidden_in &&
+        hipMemcpyAsync(out, hidden_in, batch * hidden * sizeof(float), hipMemcpyDeviceToDevice, st) != hipSuccess) {
+        return TE_STATUS_RUNTIME_ERROR;
+    }
+    const size_t ctx_kv = context_tokens * kv;
+    const size_t vt_layer = te_hip_value_t_bytes(1, 1, context_tokens, kv_heads, head_dim) / sizeof(uint16_t);
+    te_status s = TE_STATUS_OK;
+    for (size_t l = 0; l < layers && s == TE_STATUS_OK; ++l) {
+        auto gemm = [&](const uint64_t *offs, size_t n, size_t k, float *y, const float *resid) {
+            return te_hip::launch_gemm_q(m + offs[l], ggml_type, b.act, batch, n, k, y, resid, b.part, b.part_bytes,
+                                         st);
+        };
+        if ((s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights + l * hidden, epsilon, batch, hidden,
+                                          b.act, st)) != TE_STATUS_OK ||
+            (s = gemm(q_offsets, hidden, hidden, b.q, nullptr)) != TE_STATUS_OK ||
+            (s = gemm(k_offsets, kv, hidden, b.k, nullptr)) != TE_STATUS_OK ||
+            (s = gemm(v_offsets, kv, hidden, b.v, nullptr)) != TE_STATUS_OK ||
+            (s = te_hip_attention_prefill_step_vt_f16(
+                 b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
+                 key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
+                 base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream)) !=
+                TE_STATUS_OK ||
+            (s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st)) !=
+                TE_STATUS_OK ||
+            (s = gemm(output_offsets, hidden, hidden, out, out)) != TE_STATUS_OK ||
+            (s = te_hip::launch_quant_act(1, out, nullptr, ffn_norm_weights + l * hidden, epsilon, batch, hidden,
+                                          b.act, st)) != TE_STATUS_OK ||
+            (s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr)) != TE_STATUS_OK ||
+            (s = gemm(up_offsets, ffn, hidden, b.up, nullptr)) != TE_STATUS_OK ||
+            (s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act, st)) != TE_STATUS_OK ||
+            (s = gemm(down_offsets, hidden, ffn, out, out)) != TE_STATUS_OK) {
+            break;
+        }
+    }
+    return s;
+}
+
+// ---- single-layer twins ------------------------------------------------------
+
+extern "C" te_status te_hip_prefill_layer_f16(
+    const void *mapping, size_t mapping_len, uint64_t q_offset, uint64_t k_offset, uint64_t v_offset,
+    uint64_t output_offset, uint64_t gate_offset, uint64_t up_offset, uint64_t down_offset, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weight, const float *ffn_norm_weight, const float *q_bias,
+    const float *k_bias, const float *v_bias, const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+    uint16_t *value_cache, uint16_t *value_cache_t, size_t base_position, size_t batch, size_t context_tokens,
+    size_t hidden, size_t kv, size_t heads, size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    return te_hip_prefill_all_layers_f16(mapping, mapping_len, &q_offset, &k_offset, &v_offset, &output_offset,
+                                         &gate_offset, &up_offset, &down_offset, 1, ggml_type, hidden_in,
+                                         attn_norm_weight, ffn_norm_weight, q_bias, k_bias, v_bias, rope_cos,
+                                         rope_sin, key_cache, value_cache, value_cache_t, base_position, batch,
+                                         context_tokens, hidden, kv, heads, kv_heads, head_dim, ffn, epsilon, out,
+                                         workspace, workspace_bytes, stream);
+}
+
+extern "C" te_status te_hip_decode_layer_f16(
+    const void *mapping, size_t mapping_len, uint64_t q_offset, uint64_t k_offset, uint64_t v_offset,
+    uint64_t output_offset, uint64_t gate_offset, uint64_t up_offset, uint64_t down_offset, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weight, const float *ffn_norm_weight, const float *q_bias,
+    const float *k_bias, const float *v_bias, const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+    uint16_t *value_cache, size_t position, size_t context_tokens, size_t hidden, size_t kv, size_t heads,
+    size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out, void *workspace,
+    size_t workspace_bytes, void *stream) {
+    return te_hip_decode_all_layers_f16(mapping, mapping_len, &q_offset, &k_offset, &v_offset, &output_offset,
+                                        &gate_offset, &up_offset, &down_offset, 1, ggml_type, hidden_in,
+                                        attn_norm_weight, ffn_norm_weight, q_bias, k_bias, v_bias, rope_cos, rope_sin,
+                                        key_cache, value_cache, position, context_tokens, hidden, kv, heads, kv_heads,
+                                        head_dim, ffn, epsilon, out, 0, 0, nullptr, 0, nullptr, workspace,
+                                        workspace_bytes, stream);
+}

@@ -61,3 +61,35 @@ def decode_all_layers(mapping: torch.Tensor, offsets: dict, layers: int, ggml_ty
         _ptr(output_norm) if want_token else None, vocab if want_token else 0,
         _ptr(token_out) if want_token else None, _ptr(ws), ws.numel(), _stream(stream)))
     return (out, token_out) if want_token else out
+
+
+def prefill_workspace(batch: int, hidden: int, kv: int, ffn: int, device="cuda") -> torch.Tensor:
+    n = int(load_library().te_hip_prefill_all_layers_workspace_bytes(batch, hidden, kv, ffn))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def prefill_all_layers(mapping: torch.Tensor, offsets: dict, layers: int, ggml_type: int, hidden_in: torch.Tensor,
+                       attn_norm: torch.Tensor, ffn_norm: torch.Tensor, q_bias: torch.Tensor, k_bias: torch.Tensor,
+                       v_bias: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+                       key_cache: torch.Tensor, value_cache: torch.Tensor, value_t: torch.Tensor,
+                       base_position: int, context_tokens: int, heads: int, kv_heads: int, head_dim: int, ffn: int,
+                       epsilon: float, *, out=None, ws=None, stream=None) -> torch.Tensor:
+    """te_hip_prefill_all_layers_f16: hidden_in [batch, hidden] at positions
+    base_position .. base_position + batch - 1 through every layer; returns the
+    final hidden states [batch, hidden] and appends every layer's k / v (and
+    V^T) for those positions."""
+    batch = hidden_in.shape[0]
+    hidden = heads * head_dim
+    kv = kv_heads * head_dim
+    arrays = [(ctypes.c_uint64 * layers)(*[int(o) for o in offsets[n]]) for n in _NAMES]
+    if out is None:
+        out = torch.empty_like(hidden_in)
+    if ws is None:
+        ws = prefill_workspace(batch, hidden, kv, ffn, hidden_in.device)
+    check(load_library().te_hip_prefill_all_layers_f16(
+        _ptr(mapping), mapping.numel(), *[ctypes.cast(a, ctypes.POINTER(ctypes.c_uint64)) for a in arrays],
+        layers, ggml_type, _ptr(hidden_in), _ptr(attn_norm), _ptr(ffn_norm), _ptr(q_bias), _ptr(k_bias),
+        _ptr(v_bias), _ptr(rope_cos), _ptr(rope_sin), _ptr(key_cache), _ptr(value_cache), _ptr(value_t),
+        base_position, batch, context_tokens, hidden, kv, heads, kv_heads, head_dim, ffn, epsilon, _ptr(out),
+        _ptr(ws), ws.numel(), _stream(stream)))
+    return out

@@ -229,6 +229,16 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_hip_gemm_act_bytes", [_sz, _sz], _sz)
     _sig(lib, "te_hip_gemm_q_f32", [_vp, ctypes.c_uint32, _vp, _vp, _vp, ctypes.c_float, _int, _sz, _sz, _sz, _vp,
                                     _vp, _vp, _vp, _sz, _vp])
+    _sig(lib, "te_hip_prefill_all_layers_workspace_bytes", [_sz] * 4, _sz)
+    _sig(lib, "te_hip_prefill_all_layers_f16",
+         [_vp, _sz] + [_u64p] * 7 + [_sz, ctypes.c_uint32] + [_vp] * 11 + [_sz] * 9
+         + [ctypes.c_float, _vp, _vp, _sz, _vp])
+    _sig(lib, "te_hip_prefill_layer_f16",
+         [_vp, _sz] + [ctypes.c_uint64] * 7 + [ctypes.c_uint32] + [_vp] * 11 + [_sz] * 9
+         + [ctypes.c_float, _vp, _vp, _sz, _vp])
+    _sig(lib, "te_hip_decode_layer_f16",
+         [_vp, _sz] + [ctypes.c_uint64] * 7 + [ctypes.c_uint32] + [_vp] * 10 + [_sz] * 8
+         + [ctypes.c_float, _vp, _vp, _sz, _vp])
     _sig(lib, "te_hip_decode_all_layers_workspace_bytes", [_sz] * 8, _sz)
     _sig(lib, "te_hip_decode_all_layers_f16",
          [_vp, _sz] + [_u64p] * 7 + [_sz, ctypes.c_uint32] + [_vp] * 10 + [_sz] * 8
