@@ -137,9 +137,11 @@ def profile_sequence(torch, A) -> None:
     kp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
     vp = torch.randn((1, 1, Lp, KV, D), generator=g, device=dev).half()
     po = torch.empty((1, 1, Lp, H, D), dtype=torch.float32, device=dev)
-    settle(torch, lambda: A.attention_prefill(qh, kp, vp, out=po))
+    vt = A.value_t_buffer(1, 1, Lp, KV, D)
+    A.value_transpose(vp, vt)
+    settle(torch, lambda: A.attention_prefill_vt(qh, kp, vt, out=po))
     for _ in range(5):
-        A.attention_prefill(qh, kp, vp, out=po)
+        A.attention_prefill_vt(qh, kp, vt, out=po)
     torch.cuda.synchronize()
     src = torch.ones(128 << 20, dtype=torch.float32, device=dev)  # 512 MiB
     dst = torch.empty_like(src)
@@ -270,11 +272,31 @@ def mfma_ceilings(torch, timer) -> dict:
             "hipblaslt_fp16_gemm_8192_tflops": round(2.0 * n ** 3 / (gemm_ms * 1e-3) / 1e12, 1)}
 
 
-def cpu_baseline(q_layer, k_layer, v_layer, heads, kv, d, ctx_len: int, layers: int, seconds: float) -> dict:
-    """Reference CPU decode attention on one layer, one pinned core, median of reps."""
+def cpu_baseline(sample: dict, heads, kv, d, ctx_len: int, layers: int, seconds: float) -> dict:
+    """Reference CPU decode attention on one layer, one pinned core, median of
+    reps; and the GPU fused step's output for that layer checked against it.
+
+    The reference step at position ctx_len (qwen.c's per-layer order): rotate q
+    and k with te_rope_f32, store k and v at row ctx_len of the cache as fp16,
+    then te_attention_decode_f32 over rows 0..ctx_len.  The GPU's layer-0 output
+    of the same fused step (sample["out"]) must agree with it to fp16-cache
+    rounding: max_abs_err_vs_reference is reported beside the timing."""
+    import numpy as np
+
     import oracle
 
     use_ref = oracle.ref_lib() is not None
+    q_layer = oracle.rope_f32(sample["q"], heads, d, ctx_len, THETA, use_ref=use_ref)
+    k_row = oracle.rope_f32(sample["k"], kv, d, ctx_len, THETA, use_ref=use_ref)
+    k_layer = sample["kc"].copy()
+    v_layer = sample["vc"].copy()
+    k_layer[ctx_len] = k_row.astype(np.float16).astype(np.float32)
+    v_layer[ctx_len] = sample["v"].astype(np.float16).astype(np.float32)
+    want = oracle.attention_decode_f32(q_layer, k_layer, v_layer, ctx_len, heads, kv, d, use_ref=use_ref)
+    err = float(np.abs(sample["out"] - want).max())
+    # the cache row the GPU appended, against the reference's rotated fp16 k and v
+    row_err = max(float(np.abs(sample["kc"][ctx_len] - k_layer[ctx_len]).max()),
+                  float(np.abs(sample["vc"][ctx_len] - v_layer[ctx_len]).max()))
     cpus = sorted(os.sched_getaffinity(0))
     old = set(cpus)
     os.sched_setaffinity(0, {cpus[0]})
@@ -306,6 +328,8 @@ def cpu_baseline(q_layer, k_layer, v_layer, heads, kv, d, ctx_len: int, layers: 
                    f" core, median; x{layers} layers = {med * layers * 1e3:.1f} ms per decode step"),
         "cpu_model": model,
         "host_cpus_visible": len(cpus),
+        "max_abs_err_vs_reference": err,
+        "appended_row_max_abs_err_vs_reference": row_err,
     }
 
 
@@ -405,6 +429,19 @@ def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_s
 
     step_ms = timer(step_fused, reps, warmup=warmup)
     spread = timer.spread(step_fused, reps)
+    sample = None
+    if keep_cpu_sample:
+        # The fused step leaves q, k, v in place: one more step on set 0 and its
+        # layer-0 output, with the inputs that made it, for the reference check.
+        step_fused(0)
+        torch.cuda.synchronize()
+        q, k, v, kc, vc = sets[0]
+        sample = dict(q=q[0, 0, 0].reshape(-1).float().cpu().numpy().copy(),
+                      k=k[0, 0, 0].reshape(-1).float().cpu().numpy().copy(),
+                      v=v[0, 0, 0].reshape(-1).float().cpu().numpy().copy(),
+                      kc=kc[0, 0].float().cpu().numpy().reshape(ctx, -1).copy(),
+                      vc=vc[0, 0].float().cpu().numpy().reshape(ctx, -1).copy(),
+                      out=out[0, 0].reshape(-1).cpu().numpy().copy())
     fsplitk_ms = timer(step_splitk, reps)
     step3_ms = timer(step_3launch, reps)
     splitk_ms = timer(splitk, reps)
@@ -449,21 +486,29 @@ def decode_case(torch, A, timer, *, heads, kv, d, layers, positions, reps, min_s
         res["per_layer_graph_ms"] = timer(lambda i: graph.replay(), max(5, reps // 5))
         res["per_layer_graph_matches_eager"] = same
         del graph
-    if keep_cpu_sample:
-        q, k, v, kc, vc = sets[0]
-        res["cpu_sample"] = (q[0, 0, 0].reshape(-1).float().cpu().numpy().copy(),
-                             kc[0, 0].float().cpu().numpy().reshape(-1).copy(),
-                             vc[0, 0].float().cpu().numpy().reshape(-1).copy())
+    if sample is not None:
+        res["cpu_sample"] = sample
     del sets
     torch.cuda.empty_cache()
     return res
 
 
-def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, reps=10, split=False):
-    """Causal prefill of `chunks` chunks of `tokens` tokens starting at position `base`
-    (one layer): per chunk RoPE + fp16 append of the chunk, then attention over
-    positions 0..base+(c+1)*tokens-1.  Returns the attention-kernel time summed over
-    chunks; with `split`, also the key-split entry point (partials + merge launch)."""
+def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, reps=10, split=False,
+                 check_rows=None):
+    """Causal prefill of `chunks` chunks of `tokens` tokens starting at position
+    `base` (one layer).  The prefix (positions < base) and every chunk's K/V are
+    in the cache, and V^T of the whole cache is built once beforehand, as a
+    caller that keeps V^T current has it.  Timed per chunk sequence:
+      attention  te_hip_attention_prefill_vt_f16, one split (the headline kernel)
+      split      the same with the library's key split (partials + merge launch)
+      step       te_hip_attention_prefill_step_vt_f16: bias + RoPE + fp16 append
+                 of the chunk's k/v, its V^T, and the attention (the whole
+                 BASELINE config-3 step)
+      plain      te_hip_attention_prefill_f16, which builds V^T of the prefix
+                 itself on every call
+      rope       te_hip_rope_kv_append_f16 of q, k, v (the unfused step's first half)
+    With check_rows, also the largest difference of those rows of the last chunk
+    from the reference decode at position base + t (the oracle)."""
     dev = "cuda"
     ctx = base + chunks * tokens
     g = torch.Generator(device=dev).manual_seed(43)
@@ -478,38 +523,61 @@ def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, rep
     out = torch.empty((1, 1, tokens, heads, d), dtype=torch.float32, device=dev)
     for c in range(chunks):
         A.rope_kv_append(q[c], k[c], v[c], cos, sin, kc, vc, base_position=base + c * tokens, q_half=qh[c])
+    vt = A.value_t_buffer(1, 1, ctx, kv, d)
+    A.value_transpose(vc, vt)
+    bases = [base + c * tokens for c in range(chunks)]
+    ws = [A.prefill_vt_workspace(1, 1, tokens, heads, kv, d, base_position=b, context_tokens=ctx) for b in bases]
 
     def attn(i):
         for c in range(chunks):
-            A.attention_prefill(qh[c], kc, vc, base_position=base + c * tokens, out=out)
+            A.attention_prefill_vt(qh[c], kc, vt, base_position=bases[c], out=out)
+
+    def attn_split(i):
+        for c in range(chunks):
+            A.attention_prefill_vt(qh[c], kc, vt, base_position=bases[c], out=out, workspace=ws[c])
+
+    def step_vt(i):
+        for c in range(chunks):
+            A.prefill_step_vt(q0[c], k0[c], v0[c], cos, sin, kc, vc, vt, base_position=bases[c], out=out,
+                              workspace=ws[c])
+
+    def plain(i):
+        for c in range(chunks):
+            A.attention_prefill(qh[c], kc, vc, base_position=bases[c], out=out)
 
     def rope(i):
         for c in range(chunks):
-            A.rope_kv_append(q[c], k[c], v[c], cos, sin, kc, vc, base_position=base + c * tokens, q_half=qh[c])
-
-    def step_fused(i):
-        for c in range(chunks):
-            A.prefill_step(q0[c], k0[c], v0[c], cos, sin, kc, vc, base_position=base + c * tokens, out=out)
+            A.rope_kv_append(q[c], k[c], v[c], cos, sin, kc, vc, base_position=bases[c], q_half=qh[c])
 
     attn_ms = timer(attn, reps, warmup=2)
-    rope_ms = timer(rope, reps, warmup=1)
-    step_ms = timer(step_fused, reps, warmup=2)
-    flops = sum(prefill_flops(heads, d, tokens, base + c * tokens) for c in range(chunks))
-    res = dict(attention_ms=attn_ms, rope_append_ms=rope_ms, step_ms=step_ms, flops=flops,
-               tflops=flops / (attn_ms * 1e-3) / 1e12)
+    res = dict(attention_ms=attn_ms)
+    if check_rows:
+        import numpy as np
+
+        import oracle
+
+        attn(0)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(tokens, heads, d)
+        kb = kc[0, 0].cpu().view(torch.int16).numpy().view(np.uint16)
+        vb = vc[0, 0].cpu().view(torch.int16).numpy().view(np.uint16)
+        qf = qh[chunks - 1].float().cpu().numpy().reshape(tokens, heads, d)
+        worst = 0.0
+        for t in check_rows:
+            want = oracle.attention_decode_f16kv(qf[t].reshape(1, 1, heads, d).copy(), kb, vb, None,
+                                                 bases[-1] + t, 1, 1, ctx, heads, kv, d)
+            worst = max(worst, float(np.abs(got[t] - want.reshape(heads, d)).max()))
+        res["check"] = dict(max_abs_err=worst, rows=len(check_rows))
+    res["step_ms"] = timer(step_vt, reps, warmup=2)
+    res["plain_ms"] = timer(plain, reps, warmup=1)
+    res["rope_append_ms"] = timer(rope, reps, warmup=1)
+    flops = sum(prefill_flops(heads, d, tokens, b) for b in bases)
+    res.update(flops=flops, tflops=flops / (attn_ms * 1e-3) / 1e12)
     if split:
-        ws = [A.prefill_workspace(1, 1, tokens, heads, kv, d, base_position=base + c * tokens, context_tokens=ctx)
-              for c in range(chunks)]
-
-        def attn_split(i):
-            for c in range(chunks):
-                A.attention_prefill_split(qh[c], kc, vc, base_position=base + c * tokens, out=out, workspace=ws[c])
-
         res["split_ms"] = timer(attn_split, reps, warmup=2)
         res["split_tflops"] = flops / (res["split_ms"] * 1e-3) / 1e12
         res["splits"] = [1 if w is None else w.numel() // (tokens * heads * (d + 2) * 4) for w in ws]
-        del ws
-    del kc, vc, q0, k0, v0, q, k, v, qh, out
+    del kc, vc, vt, ws, q0, k0, v0, q, k, v, qh, out
     torch.cuda.empty_cache()
     return res
 
@@ -846,7 +914,8 @@ def main():
     gpu_warmup(torch, A, args.warmup_seconds)
     dec = decode_case(torch, A, timer, heads=H, kv=KV, d=D, layers=LAYERS, positions=[args.ctx], reps=K,
                       keep_cpu_sample=not args.no_cpu_baseline, warmup=args.warmup, per_layer=True)
-    pre = prefill_case(torch, A, timer, heads=H, kv=KV, d=D, tokens=4096, reps=max(5, K // 5))
+    pre = prefill_case(torch, A, timer, heads=H, kv=KV, d=D, tokens=4096, reps=max(5, K // 5),
+                       check_rows=None if args.no_cpu_baseline else (0, 1, 63, 64, 1000, 2047, 4000, 4095))
     ceil = mfma_ceilings(torch, timer)
     us_per_layer = dec["step_ms"] * 1e3 / LAYERS
     line = {
@@ -898,15 +967,17 @@ def main():
             "step_frac_hbm_peak": r(dec["step_gbs"] / HBM_PEAK_GBS),
         },
         "prefill": {
-            "workload": "Qwen2.5-3B causal prefill attention, L=4096, one layer per launch (BASELINE configs[2])",
+            "workload": "Qwen2.5-3B causal prefill attention, L=4096, one layer per launch (BASELINE configs[2]); "
+                        "K and V^T (the transposed value copy the engine keeps) resident",
             "attention_us": r(pre["attention_ms"] * 1e3, 2),
             "rope_append_us": r(pre["rope_append_ms"] * 1e3, 2),
-            # the whole prefill step: separate RoPE+append then attention, and the
-            # fused step (K/V append launch + attention with q RoPE on load)
-            "step_unfused_us": r((pre["rope_append_ms"] + pre["attention_ms"]) * 1e3, 2),
+            # the whole prefill step (bias + RoPE + fp16 K/V append + V^T of the
+            # chunk + attention), as the engine runs it per layer
             "step_fused_us": r(pre["step_ms"] * 1e3, 2),
+            # te_hip_attention_prefill_f16 (plain V layout: builds V^T itself per call)
+            "plain_entry_us": r(pre["plain_ms"] * 1e3, 2),
             "tflops": round(pre["tflops"], 1),
-            "roofline": {"bound": "mfma", "kernel": "prefill_causal_f16_kernel<128>",
+            "roofline": {"bound": "mfma", "kernel": "prefill_causal_f16_kernel (V^T operand layout)",
                          "achieved": round(pre["tflops"], 1), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": r(pre["tflops"] / FP16_MFMA_PEAK_TFLOPS), "flops_per_launch": pre["flops"]},
             # achievable fp16 MFMA rates measured in this run (see mfma_ceilings)
@@ -914,6 +985,10 @@ def main():
                              frac_of_hipblaslt_gemm=r(pre["tflops"] / ceil["hipblaslt_fp16_gemm_8192_tflops"])),
         },
     }
+    if "check" in pre:
+        line["prefill"]["max_abs_err_vs_reference"] = pre["check"]["max_abs_err"]
+        line["prefill"]["reference_check"] = (f"{pre['check']['rows']} rows of the L=4096 output against the "
+                                              "oracle's per-token decode over the fp16 cache (row t = decode at t)")
     if not args.quick:
         cfgs = {}
         reps = max(10, K // 2)
@@ -939,9 +1014,11 @@ def main():
             p = prefill_case(torch, A, timer, heads=16, kv=2, d=128, tokens=L, reps=20, split=True)
             cfgs[f"3b_prefill_L{L}"] = dict(attention_us=r(p["attention_ms"] * 1e3, 2), tflops=round(p["tflops"], 1),
                                             frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
+                                            step_fused_us=r(p["step_ms"] * 1e3, 2),
                                             split_entry=split_fields(p))
         p = prefill_case(torch, A, timer, heads=12, kv=2, d=128, tokens=2048, base=0, chunks=8, reps=3, split=True)
         cfgs["1p5b_chunked_prefill_16k_from0"] = dict(chunks=8, chunk_tokens=2048, attention_ms=r(p["attention_ms"], 3),
+                                                     step_fused_ms=r(p["step_ms"], 3),
                                                      tflops=round(p["tflops"], 1),
                                                      frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
                                                      split_entry=split_fields(p))
@@ -949,6 +1026,7 @@ def main():
                          split=True)
         cfgs["1p5b_chunked_prefill_16k_after128k"] = dict(chunks=8, chunk_tokens=2048, base=131072,
                                                          attention_ms=r(p["attention_ms"], 3),
+                                                         step_fused_ms=r(p["step_ms"], 3),
                                                          tflops=round(p["tflops"], 1),
                                                          frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
                                                          split_entry=split_fields(p))
@@ -977,9 +1055,13 @@ def main():
             "prefill_gemm_down_q4_0": gemm_case(torch, 2, 512, 2048, 11008, pre=2),
         }
     if not args.no_cpu_baseline:
-        ql, kl, vl = dec["cpu_sample"]
-        cpu = cpu_baseline(ql, kl, vl, H, KV, D, args.ctx, LAYERS, args.cpu_seconds)
+        cpu = cpu_baseline(dec["cpu_sample"], H, KV, D, args.ctx, LAYERS, args.cpu_seconds)
         cpu["gpu_speedup"] = round(cpu["value"] / us_per_layer, 1)
+        line["decode"]["max_abs_err_vs_reference"] = cpu.pop("max_abs_err_vs_reference")
+        line["decode"]["appended_row_max_abs_err_vs_reference"] = cpu.pop("appended_row_max_abs_err_vs_reference")
+        line["decode"]["reference_check"] = (
+            f"layer 0 of the fused step at position {args.ctx} against {cpu['kind']} te_rope_f32 + fp16 store + "
+            f"te_attention_decode_f32 on the host")
         line["cpu_baseline"] = cpu
         if not args.quick:
             cp = cpu_prefill_baseline(H, KV, D)
