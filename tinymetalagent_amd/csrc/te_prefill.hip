@@ -221,14 +221,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     if (n_units % kXcds == 0) {
         unit = (unit % kXcds) * (n_units / kXcds) + unit / kXcds;
     }
-    const int pair = unit % (int)gridDim.x;
-    const int hg = unit / (int)gridDim.x;           // (z, kv head, head in group)
-    const int h_in = hg % a.group;
-    const int kvh = (hg / a.group) % a.kv_heads;
-    const int zz = hg / (a.group * a.kv_heads);
-    const int h = kvh * a.group + h_in;
-    const int sl = zz / a.splits;
-    const int split = zz % a.splits;
+    // (Heads are numbered kv head * group + head in group, so the head is
+    // just hg mod heads.)  32-bit unsigned divisions, and none for the split
+    // when there is one: every wave of the CU runs this on one scalar unit.
+    const unsigned pair_u = (unsigned)unit % gridDim.x;
+    const unsigned hg = (unsigned)unit / gridDim.x;  // (z, head)
+    const int pair = (int)pair_u;
+    const int h = (int)(hg % (unsigned)a.heads);
+    const int zz = (int)(hg / (unsigned)a.heads);
+    const int kvh = h / a.group;
+    const int sl = a.splits == 1 ? zz : (int)((unsigned)zz / (unsigned)a.splits);
+    const int split = a.splits == 1 ? 0 : zz - sl * a.splits;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -343,38 +346,37 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     // Key split `split` of a tile takes its steps [lo, lo + cnt) (of 128 keys);
     // with one split that is every step.  A tile's first step is staged in st0.
     auto tile_steps = [&](int qt) __attribute__((always_inline)) { return (tile_kmax(qt) / BN + 2) / 2; };
-    auto split_lo = [&](int n) __attribute__((always_inline)) { return (int)((long long)split * n / a.splits); };
-    auto split_cnt = [&](int n) __attribute__((always_inline)) {
-        return (int)((long long)(split + 1) * n / a.splits) - split_lo(n);
+    // (split * n < 2^22: at most 32 splits of fewer than 2^24 / 128 steps.)
+    auto split_lo = [&](int n) __attribute__((always_inline)) {
+        return a.splits == 1 ? 0 : (int)((unsigned)(split * n) / (unsigned)a.splits);
     };
-    if (split_cnt(tile_steps(long_tile)) > 0) {
-        stage_load(split_lo(tile_steps(long_tile)), tile_kmax(long_tile), st0);
-    }
-    for (int ti = 0; ti < n_tiles_wg; ++ti) {
-        const int qt = ti == 0 ? long_tile : pair;
-        const int wr0 = qt * BM + 32 * (wave & 3);  // first row of this wave
-        const int kmax = tile_kmax(qt);
-        const int n_all = tile_steps(qt);            // ceil(blocks / 2)
-        const int lo = split_lo(n_all);
-        const int cnt = split_cnt(n_all);
-        const int n_next = ti + 1 < n_tiles_wg ? tile_steps(pair) : 0;
-        const int lo_next = split_lo(n_next);
-        const int cnt_next = split_cnt(n_next);
-
-        // Q^T operand for the wave's two 16-row blocks.
-        f16x8 qop[2][KK];
+    auto split_cnt = [&](int n) __attribute__((always_inline)) {
+        return a.splits == 1 ? n : (int)((unsigned)((split + 1) * n) / (unsigned)a.splits) - split_lo(n);
+    };
+    // Q^T operand for the wave's two 16-row blocks.  fp16 queries are loaded
+    // raw (load_q16) before they are needed: the first tile's with its first
+    // K/V step, the second tile's right after the first tile's last step, so
+    // that load overlaps the merge; prep_q then scales them (and the fused
+    // step loads, rotates and scales its fp32 queries there).
+    f16x8 qop[2][KK];
+    auto load_q16 = [&](int qt) __attribute__((always_inline)) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int row = wr0 + 16 * nb + c;
+            const int row = qt * BM + 32 * (wave & 3) + 16 * nb + c;
+            const f16 *qrow = a.q + (((size_t)sl * a.tokens + (row < a.tokens ? row : 0)) * a.heads + h) * D;
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                qop[nb][kk] = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
+            }
+        }
+    };
+    auto prep_q = [&](int qt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int row = qt * BM + 32 * (wave & 3) + 16 * nb + c;
             const bool ok = row < a.tokens;
             if (a.q32 != nullptr) {
                 load_q_rope<D>(a, sl, sl % a.layers, h, ok ? row : 0, g, qop[nb]);
-            } else {
-                const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    qop[nb][kk] = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
-                }
             }
             // The softmax scale log2(e)/sqrt(D) rides in the operand: q' =
             // fp16(q * qscale), so S^T comes out in log2 units and p =
@@ -387,6 +389,33 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                 }
             }
         }
+    };
+    // Barrier over LDS traffic only: the waves' LDS reads and writes are done
+    // and visible, while global stores (the output rows) stay in flight.
+    auto lds_barrier = []() __attribute__((always_inline)) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+
+    if (split_cnt(tile_steps(long_tile)) > 0) {
+        stage_load(split_lo(tile_steps(long_tile)), tile_kmax(long_tile), st0);
+    }
+    if (a.q32 == nullptr) {
+        load_q16(long_tile);
+    }
+    bool first_staged = true;  // the tile's first step is in LDS (waited for) when it starts
+    for (int ti = 0; ti < n_tiles_wg; ++ti) {
+        const int qt = ti == 0 ? long_tile : pair;
+        const int wr0 = qt * BM + 32 * (wave & 3);  // first row of this wave
+        const int kmax = tile_kmax(qt);
+        const int n_all = tile_steps(qt);            // ceil(blocks / 2)
+        const int lo = split_lo(n_all);
+        const int cnt = split_cnt(n_all);
+        const int n_next = ti + 1 < n_tiles_wg ? tile_steps(pair) : 0;
+        const int lo_next = split_lo(n_next);
+        const int cnt_next = split_cnt(n_next);
+        prep_q(qt);
 
         float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
         // QK^T accumulators start at -m_ref (0 while m_ref is -inf), so the
@@ -581,14 +610,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             stage_wait();
             __syncthreads();
         };
-        stage_wait();
-        __syncthreads();
+        if (ti == 0 || !first_staged) {
+            // The kernel's first step (and a step staged after an empty key
+            // range below) is waited for here; every other tile's first step
+            // landed during the previous tile's last step, whose wait and
+            // barrier cover it, so the output stores of that tile's merge
+            // stay in flight.
+            stage_wait();
+            __syncthreads();
+        }
         for (int j = 0; j < cnt; j += 2) {
             body(std::integral_constant<int, 0>(), j);
             body(std::integral_constant<int, 1>(), j + 1);
         }
-        if (cnt == 0 && cnt_next > 0) {
-            stage_load(lo_next, tile_kmax(pair), st0);  // nothing of this tile was staged: st0 is free
+        first_staged = cnt > 0;
+        if (ti + 1 < n_tiles_wg && a.q32 == nullptr) {
+            load_q16(pair);  // qop is dead after the last step: the next tile's queries load across the merge
         }
 
         // ---- merge the two key halves through LDS, normalise, store ----
@@ -654,13 +691,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         } else {
             put(o[0], mref[0], l[0]);
         }
-        __syncthreads();
+        lds_barrier();
         if (half == 0) {
             finish(o[0], mref[0], l[0], 0);
         } else {
             finish(o[1], mref[1], l[1], 1);
         }
-        __syncthreads();  // exchange reads finish before st1 is staged again
+        lds_barrier();  // exchange reads finish before st1 is staged again
+        if (cnt == 0 && cnt_next > 0) {
+            // Nothing of this tile was staged (an empty key range of the
+            // split), so st0 is free; staged after the merge, so no LDS DMA
+            // is in flight across the merge barriers.
+            stage_load(lo_next, tile_kmax(pair), st0);
+        }
     }
 }
 
