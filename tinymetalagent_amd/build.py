@@ -91,5 +91,64 @@ def build(verbose: bool = False) -> Path:
     return LIBRARY
 
 
+# Host-sanitizer build (CPU testing only): the host code of the GGUF loader,
+# tokenizer and C ABI (te_model.hip, te_abi.c) compiled with AddressSanitizer
+# and UndefinedBehaviorSanitizer, linked with the other objects of the normal
+# build into a separate library.  GPU code is compiled as usual (the
+# sanitizer flags apply to the host pass only).  Load it with the clang ASan
+# runtime preloaded (asan_runtime()) and TINYENGINE_LIBRARY pointing at it.
+SAN_BUILD = PKG / "_build_san"
+SAN_LIBRARY = SAN_BUILD / "libtinyengine_san.so"
+SAN_SOURCES = ["te_model.hip"]
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer", "-g"]
+
+
+def asan_runtime() -> Path:
+    """The clang AddressSanitizer runtime that the sanitized library needs preloaded."""
+    llvm = Path(_hipcc()).resolve().parent.parent / "lib" / "llvm"
+    for cand in sorted(llvm.glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")) + \
+            sorted(Path("/opt/rocm/lib/llvm").glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")):
+        return cand
+    raise RuntimeError("clang AddressSanitizer runtime not found")
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    """Build libtinyengine_san.so (needs the objects of build() for the rest)."""
+    hipcc = _hipcc()
+    clang = Path(hipcc).resolve().parent.parent / "lib" / "llvm" / "bin" / "clang"
+    if not clang.is_file():
+        clang = Path("/opt/rocm/lib/llvm/bin/clang")
+    SAN_BUILD.mkdir(exist_ok=True)
+    objs = []
+    for src in HIP_SOURCES:
+        if src in SAN_SOURCES:
+            obj = SAN_BUILD / (Path(src).stem + ".o")
+            cmd = [hipcc, *HIP_FLAGS, *SAN_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        else:
+            obj = BUILD / (Path(src).stem + ".o")
+            if not obj.is_file():
+                raise RuntimeError(f"{obj} missing: run build() first")
+        objs.append(obj)
+    obj = SAN_BUILD / "te_abi.o"
+    cmd = [str(clang), "-std=c11", "-O1", "-g", "-fPIC", "-Wall", "-fsanitize=address,undefined",
+           "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", f"-I{INCLUDE}", "-D_POSIX_C_SOURCE=200809L",
+           "-c", str(CSRC / "te_abi.c"), "-o", str(obj)]
+    subprocess.run(cmd, check=True)
+    objs.append(obj)
+    link = [hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", "-fsanitize=address,undefined", "-fno-gpu-sanitize",
+            "-shared-libsan", *map(str, objs), "-o", str(SAN_LIBRARY)]
+    if verbose:
+        print(" ".join(link), flush=True)
+    subprocess.run(link, check=True)
+    return SAN_LIBRARY
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized(verbose="-v" in sys.argv))
+    else:
+        print(build(verbose="-v" in sys.argv))
