@@ -118,11 +118,22 @@ def q4_model(tmp_path_factory):
                          kv_heads=2, head_dim=64, ffn=256, n_merges=80)
 
 
-def test_generate_raw_greedy_vs_oracle(q4_model, monkeypatch):
+@pytest.mark.parametrize("path_env", [
+    {},
+    {"TINYENGINE_DECODE_ALL_LAYERS": "0"},
+    {"TINYENGINE_FUSED_DECODE_LAYER": "0"},
+    {"TINYENGINE_PREFILL_ALL_LAYERS": "0"},
+    {"TINYENGINE_PREFILL_ALL_LAYERS": "0", "TINYENGINE_FUSED_PREFILL_LAYER": "0"},
+], ids=["fused", "decode-per-layer", "decode-op-by-op", "prefill-per-layer", "prefill-token-by-token"])
+def test_generate_raw_greedy_vs_oracle(q4_model, monkeypatch, path_env):
+    """Greedy generation against the oracle's loop on every path the
+    reference's switches select (qwen.c:1392, :1484, :1646, :1799): the fused
+    all-layers flows, one fused layer per launch sequence, the layer as
+    separate operations, and the prompt token by token."""
     q = q4_model
     prompt = "<|im_start|>user\nhello world, the engine<|im_end|>\n<|im_start|>assistant\n"
     got, text = _gpu_generate(q["path"], prompt, 24, monkeypatch=monkeypatch,
-                              env={"TINYENGINE_TEMPERATURE": "0", "TINYENGINE_IGNORE_EOS": "1"})
+                              env={"TINYENGINE_TEMPERATURE": "0", "TINYENGINE_IGNORE_EOS": "1", **path_env})
     assert len(got) == 24
     pids = _prompt_ids(q, prompt)
     exact = _check_greedy(q, pids, got, 256)

@@ -1155,6 +1155,11 @@ struct te_context {
     size_t pws_bytes = 0;
     uint16_t *vt = nullptr;
     size_t vt_valid = 0;
+    // op-by-op decode (TINYENGINE_FUSED_DECODE_LAYER=0): activations and the
+    // split-K workspace, made on first use
+    float *ufw = nullptr;
+    void *udws = nullptr;
+    size_t udws_bytes = 0;
 };
 
 namespace {
@@ -1166,7 +1171,16 @@ void release_state(te_context *c) {
     c->allocations.clear();
     c->history.clear();
     c->vt_valid = 0;
+    c->ufw = nullptr;
+    c->udws = nullptr;
     c->ready = false;
+}
+
+// The reference's path switches: NAME=0 turns a fused path off (qwen.c:1392,
+// :1484-1491, :1646, :1799).
+bool env_off(const char *name) {
+    const char *e = getenv(name);
+    return e != nullptr && strcmp(e, "0") == 0;
 }
 
 template <typename T>
@@ -1363,8 +1377,14 @@ te_status prefill_batch(te_context *c, const uint32_t *ids, size_t start, size_t
     const unsigned char *base = m->d_mapping;
     const float eps = m->info.rms_norm_epsilon;
     const size_t H = c->hidden;
-    const char *all = getenv("TINYENGINE_PREFILL_ALL_LAYERS");
-    const bool per_layer = all != nullptr && strcmp(all, "0") == 0;
+    // TINYENGINE_PREFILL_ALL_LAYERS=0: one layer-flow launch sequence per
+    // layer; with TINYENGINE_FUSED_PREFILL_LAYER=0 as well no batched path
+    // remains and the prompt goes token by token (UNSUPPORTED, as the
+    // reference's batch prefill falls back, qwen.c:348-356)
+    const bool per_layer = env_off("TINYENGINE_PREFILL_ALL_LAYERS");
+    if (per_layer && env_off("TINYENGINE_FUSED_PREFILL_LAYER")) {
+        return TE_STATUS_UNSUPPORTED;
+    }
     const size_t vt_layer = te_hip_value_t_bytes(1, 1, c->ctx, c->kv_heads, c->head_dim) / sizeof(uint16_t);
     te_status s = TE_STATUS_OK;
     for (size_t p0 = start; p0 < end && s == TE_STATUS_OK; p0 += c->chunk) {
@@ -1425,13 +1445,82 @@ te_status project_greedy(te_context *c) {
     return s == TE_STATUS_OK ? te_hip::launch_argmax(c->logits, c->vocab, c->token, nullptr) : s;
 }
 
-// One token at `position` through every layer; with `token_out`, also the
-// greedy next token into c->token.
+// TINYENGINE_DECODE_ALL_LAYERS=0: one fused decode-layer launch sequence per
+// layer (te_hip_decode_layer_f16), then the head.
+te_status forward_per_layer(te_context *c, size_t position, bool project) {
+    const size_t H = c->hidden, ckv = c->ctx * c->kv;
+    te_status s = TE_STATUS_OK;
+    for (size_t l = 0; l < c->layers && s == TE_STATUS_OK; ++l) {
+        s = te_hip_decode_layer_f16(c->model->d_mapping, c->model->mapping_len, c->offs[0][l], c->offs[1][l],
+                                    c->offs[2][l], c->offs[3][l], c->offs[4][l], c->offs[5][l], c->offs[6][l],
+                                    c->type, c->hidden_buf, c->attn_norm + l * H, c->ffn_norm + l * H,
+                                    c->qb + l * H, c->kb + l * c->kv, c->vb + l * c->kv, c->cos, c->sin,
+                                    c->kc + l * ckv, c->vc + l * ckv, position, c->ctx, H, c->kv, c->heads,
+                                    c->kv_heads, c->head_dim, c->ffn, c->model->info.rms_norm_epsilon,
+                                    c->hidden_buf, c->ws, c->ws_bytes, nullptr);
+    }
+    return s == TE_STATUS_OK && project ? project_greedy(c) : s;
+}
+
+// TINYENGINE_FUSED_DECODE_LAYER=0: the layer as separate operations through
+// the public entry points, in the reference's order (qwen.c te_qwen_forward_token):
+// RMSNorm, q/k/v GEMVs, the decode step (bias + RoPE + fp16 append + attention),
+// Wo GEMV, residual add, RMSNorm, gate/up GEMVs, SwiGLU, down GEMV, residual add.
+te_status forward_unfused(te_context *c, size_t position, bool project) {
+    const size_t H = c->hidden, KV = c->kv, F = c->ffn, ckv = c->ctx * c->kv;
+    te_status s = TE_STATUS_OK;
+    if (c->ufw == nullptr) {
+        c->udws_bytes = te_hip_attention_decode_workspace_bytes(nullptr, c->ctx - 1, 1, 1, c->heads, c->kv_heads,
+                                                                c->head_dim);
+        unsigned char *dws = nullptr;
+        if (c->udws_bytes == 0 || (s = dev_alloc(c, &c->ufw, 5 * H + 2 * KV + 3 * F)) != TE_STATUS_OK ||
+            (s = dev_alloc(c, &dws, c->udws_bytes)) != TE_STATUS_OK) {
+            return s != TE_STATUS_OK ? s : TE_STATUS_RUNTIME_ERROR;
+        }
+        c->udws = dws;
+    }
+    float *xn = c->ufw, *q = xn + H, *att = q + H, *proj = att + H, *dn = proj + H, *k = dn + H, *v = k + KV;
+    float *g = v + KV, *u = g + F, *act = u + F;
+    const unsigned char *base = c->model->d_mapping;
+    const float eps = c->model->info.rms_norm_epsilon;
+    float *x = c->hidden_buf;
+    for (size_t l = 0; l < c->layers && s == TE_STATUS_OK; ++l) {
+        auto mv = [&](int w, const float *in, size_t cols, size_t rows, float *out) {
+            return te_hip_matvec_f32(base + c->offs[w][l], c->type, in, cols, rows, out, nullptr);
+        };
+        if ((s = te_hip_rmsnorm_f32(x, c->attn_norm + l * H, 1, H, eps, xn, nullptr)) != TE_STATUS_OK ||
+            (s = mv(0, xn, H, H, q)) != TE_STATUS_OK || (s = mv(1, xn, H, KV, k)) != TE_STATUS_OK ||
+            (s = mv(2, xn, H, KV, v)) != TE_STATUS_OK ||
+            (s = te_hip_attention_decode_step_f16(q, k, v, c->qb + l * H, c->kb + l * KV, c->vb + l * KV, c->cos,
+                                                  c->sin, c->kc + l * ckv, c->vc + l * ckv, nullptr, position, 1, 1,
+                                                  c->ctx, c->heads, c->kv_heads, c->head_dim, att, c->udws,
+                                                  c->udws_bytes, nullptr)) != TE_STATUS_OK ||
+            (s = mv(3, att, H, H, proj)) != TE_STATUS_OK || (s = te_hip_add_f32(x, proj, H, x, nullptr)) != TE_STATUS_OK ||
+            (s = te_hip_rmsnorm_f32(x, c->ffn_norm + l * H, 1, H, eps, xn, nullptr)) != TE_STATUS_OK ||
+            (s = mv(4, xn, H, F, g)) != TE_STATUS_OK || (s = mv(5, xn, H, F, u)) != TE_STATUS_OK ||
+            (s = te_hip_swiglu_f32(g, u, F, act, nullptr)) != TE_STATUS_OK || (s = mv(6, act, F, H, dn)) != TE_STATUS_OK) {
+            break;
+        }
+        s = te_hip_add_f32(x, dn, H, x, nullptr);
+    }
+    return s == TE_STATUS_OK && project ? project_greedy(c) : s;
+}
+
+// One token at `position` through every layer; with `project`, also the
+// greedy next token into c->token.  TINYENGINE_FUSED_DECODE_LAYER=0 (which
+// also turns the all-layers path off, as in the reference) and
+// TINYENGINE_DECODE_ALL_LAYERS=0 select the slower paths above.
 te_status forward(te_context *c, uint32_t token, size_t position, bool project) {
     const te_status s = te_hip::launch_dequant_row(c->model->d_mapping + c->embd_off, c->embd_type, c->hidden,
                                                    token, c->hidden_buf, nullptr);
     if (s != TE_STATUS_OK) {
         return s;
+    }
+    if (env_off("TINYENGINE_FUSED_DECODE_LAYER")) {
+        return forward_unfused(c, position, project);
+    }
+    if (env_off("TINYENGINE_DECODE_ALL_LAYERS")) {
+        return forward_per_layer(c, position, project);
     }
     const uint64_t *o[7];
     for (int w = 0; w < 7; ++w) {
