@@ -359,3 +359,43 @@ def test_session_reuse_with_batched_prefill_vs_oracle(q4_model, monkeypatch):
     assert len(got) == 12
     exact = _check_greedy(q, _prompt_ids(q, turn2), got, 256)
     print(f"second turn with reuse: {exact}/12 steps decided beyond the tolerance, all equal")
+
+
+@pytest.mark.parametrize("path_env", [{}, {"TINYENGINE_FUSED_DECODE_LAYER": "0"}], ids=["fused", "op-by-op"])
+def test_profile_line(q4_model, monkeypatch, capfd, path_env):
+    """TINYENGINE_PROFILE=1 prints one line per generate call on stderr in the
+    reference's format (qwen.c:2262-2304: the same keys in the same order),
+    followed by this build's buckets; call counts follow the launches: one
+    per layer and matrix for the prompt chunk and for every forwarded token,
+    one head projection per next token."""
+    import re
+
+    q = q4_model
+    prompt = "qwen model attention"
+    n = 6
+    got, _ = _gpu_generate(q["path"], prompt, n, monkeypatch=monkeypatch,
+                           env={"TINYENGINE_TEMPERATURE": "0", "TINYENGINE_IGNORE_EOS": "1",
+                                "TINYENGINE_PROFILE": "1", **path_env})
+    assert len(got) == n
+    err = capfd.readouterr().err
+    lines = [ln for ln in err.splitlines() if ln.startswith("tinyengine_profile:")]
+    assert len(lines) == 1, err
+    line = lines[0]
+    print(line)
+    ref_keys = ("total_ms tokenize_ms init_ms embed_ms matvec_ms q k v o gate up down lm_head other").split()
+    keys = re.findall(r" (\w+)=", line)
+    assert tuple(keys[:len(ref_keys)]) == tuple(ref_keys)
+    f = dict(re.findall(r" (\w+)=([\d.]+(?:/\d+)?)", line))
+    ms = {k: float(v.split("/")[0]) for k, v in f.items()}
+    calls = {k: int(v.split("/")[1]) for k, v in f.items() if "/" in v}
+    layers = 2
+    forwards = n - 1  # the last emitted token is not run
+    for key in ("q", "k", "v", "o", "gate", "up", "down"):
+        assert calls[key] == layers * (1 + forwards), (key, calls[key])
+        assert ms[key] > 0.0
+    assert calls["lm_head"] == n
+    assert calls["attention"] >= layers * (1 + forwards)
+    buckets = sum(ms[k] for k in ("q", "k", "v", "o", "gate", "up", "down", "lm_head", "other"))
+    assert abs(buckets - ms["matvec_ms"]) <= 0.02 * len(ref_keys)
+    assert ms["total_ms"] >= ms["prefill_ms"] + ms["decode_ms"]
+    assert int(f["prompt_tokens"]) == len(_prompt_ids(q, prompt)) and int(f["generated_tokens"]) == n

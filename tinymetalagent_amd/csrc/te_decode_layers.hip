@@ -154,10 +154,15 @@ extern "C" te_status te_hip_decode_all_layers_f16(
     }
 
     const hipStream_t st = te_hip::as_stream(stream);
+    te_hip::prof_begin(st);
     if (out != hidden_in && hipMemcpyAsync(out, hidden_in, hidden * sizeof(float), hipMemcpyDeviceToDevice, st) !=
                                 hipSuccess) {
         return TE_STATUS_RUNTIME_ERROR;
     }
+    using te_hip::prof_mark;
+    const te_hip::ProfShare qkv_share[3] = {
+        {te_hip::kProfQ, (double)hidden}, {te_hip::kProfK, (double)kv}, {te_hip::kProfV, (double)kv}};
+    const te_hip::ProfShare gu_share[2] = {{te_hip::kProfGate, 1.0}, {te_hip::kProfUp, 1.0}};
     te_status s = TE_STATUS_OK;
     for (size_t l = 0; l < layers && s == TE_STATUS_OK; ++l) {
         const te_hip::GemvSeg qkv[3] = {{m + q_offsets[l], b.q, nullptr, hidden},
@@ -168,6 +173,7 @@ extern "C" te_status te_hip_decode_all_layers_f16(
         if (s != TE_STATUS_OK) {
             break;
         }
+        prof_mark(st, qkv_share, 3);
         const size_t cache_off = l * context_tokens * kv;
         s = te_hip_attention_decode_step_f16(b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv,
                                              v_biases + l * kv, rope_cos, rope_sin, key_cache + cache_off,
@@ -176,12 +182,14 @@ extern "C" te_status te_hip_decode_all_layers_f16(
         if (s != TE_STATUS_OK) {
             break;
         }
+        prof_mark(st, te_hip::kProfAttention);
         const te_hip::GemvSeg o = {m + output_offsets[l], out, out, hidden};
         s = te_hip::launch_gemv(ggml_type, te_hip::kGemvPlain, &o, 1, hidden, b.attn, nullptr, nullptr, 0.0f, b.xtmp,
                                 b.proj, st);
         if (s != TE_STATUS_OK) {
             break;
         }
+        prof_mark(st, te_hip::kProfO);
         const te_hip::GemvSeg gu[2] = {{m + gate_offsets[l], b.gate, nullptr, ffn},
                                        {m + up_offsets[l], b.up, nullptr, ffn}};
         s = te_hip::launch_gemv(ggml_type, te_hip::kGemvRmsNorm, gu, 2, hidden, out, nullptr,
@@ -189,15 +197,19 @@ extern "C" te_status te_hip_decode_all_layers_f16(
         if (s != TE_STATUS_OK) {
             break;
         }
+        prof_mark(st, gu_share, 2);
         const te_hip::GemvSeg d = {m + down_offsets[l], out, out, hidden};
         s = te_hip::launch_gemv(ggml_type, te_hip::kGemvSwiGLU, &d, 1, ffn, b.gate, b.up, nullptr, 0.0f, b.xtmp, b.proj, st);
+        prof_mark(st, te_hip::kProfDown);
     }
     if (s == TE_STATUS_OK && out_token_id != nullptr) {
         const te_hip::GemvSeg h = {m + head_offset, b.logits, nullptr, vocab};
         s = te_hip::launch_gemv(head_ggml_type, te_hip::kGemvRmsNorm, &h, 1, hidden, out, nullptr,
                                 output_norm_weight, epsilon, b.xtmp, b.proj, st);
+        prof_mark(st, te_hip::kProfLmHead);
         if (s == TE_STATUS_OK) {
             s = te_hip::launch_argmax(b.logits, vocab, out_token_id, st);
+            prof_mark(st, te_hip::kProfElementwise);
         }
     }
     return s;

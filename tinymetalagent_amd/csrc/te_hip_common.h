@@ -172,4 +172,33 @@ te_status launch_rope_rows(float *values, size_t heads, size_t head_dim, const f
 te_status launch_mma_kat(int mode, const float *query, const float *key_t, const float *value, int k_cols,
                          int q_base, float *out, hipStream_t stream);
 
+// In-library profiling of te_generate (TINYENGINE_PROFILE set and not "0",
+// the reference's switch, qwen.c:2216-2219).  While a thread's profile is
+// active, the layer flows record a HIP event on their stream after each piece
+// of work (prof_mark); prof_flush waits for the last one and adds the time
+// from the previous event to each piece's phases, split by the given shares
+// (the weight rows of a launch that covers several matrices).  The phases are
+// the reference's matvec buckets plus the embedding rows, the attention and
+// the other elementwise work (normalisation, activation quantisation, argmax).  Thread-local: contexts on other threads keep their own.
+enum ProfPhase {
+    kProfQ, kProfK, kProfV, kProfO, kProfGate, kProfUp, kProfDown, kProfLmHead, kProfOther,
+    kProfEmbed, kProfAttention, kProfElementwise, kProfCount
+};
+struct ProfShare {
+    ProfPhase phase;
+    double weight;
+};
+bool prof_active();
+void prof_start();                   // reset and activate this thread's profile
+void prof_stop();
+void prof_begin(hipStream_t stream);  // the reference point of the next mark
+void prof_mark(hipStream_t stream, const ProfShare *shares, int n);
+inline void prof_mark(hipStream_t stream, ProfPhase phase) {
+    const ProfShare one = {phase, 1.0};
+    prof_mark(stream, &one, 1);
+}
+te_status prof_flush();              // synchronise and account the recorded marks
+double prof_ms(ProfPhase phase);
+unsigned long long prof_calls(ProfPhase phase);
+
 }  // namespace te_hip

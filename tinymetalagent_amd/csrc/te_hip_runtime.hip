@@ -154,6 +154,119 @@ te_status mma_twin(int mode, const float *query, const float *key_t, const float
 
 namespace te_hip {
 
+namespace {
+
+struct ProfMark {
+    hipEvent_t ev;
+    double share[kProfCount];
+};
+
+// One thread's profile: a pool of events reused across flushes, the marks
+// recorded since the last flush, and the accumulated phase times.
+struct Profile {
+    bool active = false;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    hipEvent_t begin = nullptr;
+    std::vector<ProfMark> marks;
+    double ms[kProfCount] = {};
+    unsigned long long calls[kProfCount] = {};
+    // (the pool's events are not destroyed at thread exit: the runtime may
+    // already be gone then)
+    hipEvent_t next_event() {
+        if (used == pool.size()) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreate(&e) != hipSuccess) {
+                return nullptr;
+            }
+            pool.push_back(e);
+        }
+        return pool[used++];
+    }
+};
+
+thread_local Profile t_prof;
+
+}  // namespace
+
+bool prof_active() { return t_prof.active; }
+
+void prof_start() {
+    t_prof.active = true;
+    t_prof.used = 0;
+    t_prof.begin = nullptr;
+    t_prof.marks.clear();
+    for (int i = 0; i < kProfCount; ++i) {
+        t_prof.ms[i] = 0.0;
+        t_prof.calls[i] = 0;
+    }
+}
+
+void prof_stop() { t_prof.active = false; }
+
+void prof_begin(hipStream_t stream) {
+    if (!t_prof.active || t_prof.begin != nullptr) {
+        return;
+    }
+    hipEvent_t e = t_prof.next_event();
+    if (e != nullptr && hipEventRecord(e, stream) == hipSuccess) {
+        t_prof.begin = e;
+    }
+}
+
+void prof_mark(hipStream_t stream, const ProfShare *shares, int n) {
+    if (!t_prof.active) {
+        return;
+    }
+    prof_begin(stream);
+    hipEvent_t e = t_prof.next_event();
+    if (e == nullptr || hipEventRecord(e, stream) != hipSuccess) {
+        return;
+    }
+    ProfMark m = {};
+    m.ev = e;
+    double total = 0.0;
+    for (int i = 0; i < n; ++i) {
+        total += shares[i].weight;
+    }
+    for (int i = 0; i < n && total > 0.0; ++i) {
+        m.share[shares[i].phase] += shares[i].weight / total;
+    }
+    t_prof.marks.push_back(m);
+}
+
+te_status prof_flush() {
+    if (!t_prof.active || t_prof.marks.empty()) {
+        t_prof.begin = nullptr;
+        t_prof.used = 0;
+        return TE_STATUS_OK;
+    }
+    if (hipEventSynchronize(t_prof.marks.back().ev) != hipSuccess) {
+        return TE_STATUS_RUNTIME_ERROR;
+    }
+    hipEvent_t prev = t_prof.begin;
+    for (const ProfMark &m : t_prof.marks) {
+        float dt = 0.0f;
+        if (prev != nullptr && hipEventElapsedTime(&dt, prev, m.ev) == hipSuccess) {
+            for (int i = 0; i < kProfCount; ++i) {
+                if (m.share[i] > 0.0) {
+                    t_prof.ms[i] += dt * m.share[i];
+                    t_prof.calls[i] += 1;
+                }
+            }
+        }
+        prev = m.ev;
+    }
+    t_prof.marks.clear();
+    t_prof.begin = nullptr;
+    t_prof.used = 0;
+    return TE_STATUS_OK;
+}
+
+double prof_ms(ProfPhase phase) { return t_prof.ms[phase]; }
+
+unsigned long long prof_calls(ProfPhase phase) { return t_prof.calls[phase]; }
+
 std::mutex &library_mutex() { return g_mutex; }
 
 te_status library_buffer(LibraryBuffer which, size_t bytes, void **ptr) {

@@ -21,6 +21,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -1392,11 +1393,14 @@ te_status prefill_batch(te_context *c, const uint32_t *ids, size_t start, size_t
         if (hipMemcpy(c->pids, ids + p0, M * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess) {
             return TE_STATUS_RUNTIME_ERROR;
         }
+        te_hip::prof_begin(nullptr);
         s = te_hip::launch_dequant_rows(base + c->embd_off, c->embd_type, H, c->pids, M, c->px, nullptr);
+        te_hip::prof_mark(nullptr, te_hip::kProfEmbed);
         if (s == TE_STATUS_OK && c->vt_valid < p0) {
             // positions the decode path appended since V^T was last current
             s = te_hip_value_transpose_f16(c->vc, c->vt, 1, c->layers, c->vt_valid, p0 - c->vt_valid, c->ctx,
                                            c->kv_heads, c->head_dim, nullptr);
+            te_hip::prof_mark(nullptr, te_hip::kProfAttention);
         }
         if (s != TE_STATUS_OK) {
             break;
@@ -1442,7 +1446,12 @@ te_status project_greedy(te_context *c) {
     te_status s = te_hip::launch_gemv(c->head_type, te_hip::kGemvRmsNorm, &h, 1, c->hidden, c->hidden_buf, nullptr,
                                       c->out_norm, c->model->info.rms_norm_epsilon, xtmp,
                                       xtmp + ((std::max(c->hidden, c->ffn) + 63) / 64 * 64), nullptr);
-    return s == TE_STATUS_OK ? te_hip::launch_argmax(c->logits, c->vocab, c->token, nullptr) : s;
+    te_hip::prof_mark(nullptr, te_hip::kProfLmHead);
+    if (s == TE_STATUS_OK) {
+        s = te_hip::launch_argmax(c->logits, c->vocab, c->token, nullptr);
+        te_hip::prof_mark(nullptr, te_hip::kProfElementwise);
+    }
+    return s;
 }
 
 // TINYENGINE_DECODE_ALL_LAYERS=0: one fused decode-layer launch sequence per
@@ -1485,23 +1494,34 @@ te_status forward_unfused(te_context *c, size_t position, bool project) {
     const float eps = c->model->info.rms_norm_epsilon;
     float *x = c->hidden_buf;
     for (size_t l = 0; l < c->layers && s == TE_STATUS_OK; ++l) {
+        static const te_hip::ProfPhase kW[7] = {te_hip::kProfQ, te_hip::kProfK, te_hip::kProfV, te_hip::kProfO,
+                                                te_hip::kProfGate, te_hip::kProfUp, te_hip::kProfDown};
         auto mv = [&](int w, const float *in, size_t cols, size_t rows, float *out) {
-            return te_hip_matvec_f32(base + c->offs[w][l], c->type, in, cols, rows, out, nullptr);
+            const te_status r = te_hip_matvec_f32(base + c->offs[w][l], c->type, in, cols, rows, out, nullptr);
+            te_hip::prof_mark(nullptr, kW[w]);
+            return r;
         };
-        if ((s = te_hip_rmsnorm_f32(x, c->attn_norm + l * H, 1, H, eps, xn, nullptr)) != TE_STATUS_OK ||
+        auto ew = [](te_status r) {
+            te_hip::prof_mark(nullptr, te_hip::kProfElementwise);
+            return r;
+        };
+        if ((s = ew(te_hip_rmsnorm_f32(x, c->attn_norm + l * H, 1, H, eps, xn, nullptr))) != TE_STATUS_OK ||
             (s = mv(0, xn, H, H, q)) != TE_STATUS_OK || (s = mv(1, xn, H, KV, k)) != TE_STATUS_OK ||
             (s = mv(2, xn, H, KV, v)) != TE_STATUS_OK ||
             (s = te_hip_attention_decode_step_f16(q, k, v, c->qb + l * H, c->kb + l * KV, c->vb + l * KV, c->cos,
                                                   c->sin, c->kc + l * ckv, c->vc + l * ckv, nullptr, position, 1, 1,
                                                   c->ctx, c->heads, c->kv_heads, c->head_dim, att, c->udws,
                                                   c->udws_bytes, nullptr)) != TE_STATUS_OK ||
-            (s = mv(3, att, H, H, proj)) != TE_STATUS_OK || (s = te_hip_add_f32(x, proj, H, x, nullptr)) != TE_STATUS_OK ||
-            (s = te_hip_rmsnorm_f32(x, c->ffn_norm + l * H, 1, H, eps, xn, nullptr)) != TE_STATUS_OK ||
+            (te_hip::prof_mark(nullptr, te_hip::kProfAttention), false) ||
+            (s = mv(3, att, H, H, proj)) != TE_STATUS_OK ||
+            (s = ew(te_hip_add_f32(x, proj, H, x, nullptr))) != TE_STATUS_OK ||
+            (s = ew(te_hip_rmsnorm_f32(x, c->ffn_norm + l * H, 1, H, eps, xn, nullptr))) != TE_STATUS_OK ||
             (s = mv(4, xn, H, F, g)) != TE_STATUS_OK || (s = mv(5, xn, H, F, u)) != TE_STATUS_OK ||
-            (s = te_hip_swiglu_f32(g, u, F, act, nullptr)) != TE_STATUS_OK || (s = mv(6, act, F, H, dn)) != TE_STATUS_OK) {
+            (s = ew(te_hip_swiglu_f32(g, u, F, act, nullptr))) != TE_STATUS_OK ||
+            (s = mv(6, act, F, H, dn)) != TE_STATUS_OK) {
             break;
         }
-        s = te_hip_add_f32(x, dn, H, x, nullptr);
+        s = ew(te_hip_add_f32(x, dn, H, x, nullptr));
     }
     return s == TE_STATUS_OK && project ? project_greedy(c) : s;
 }
@@ -1511,11 +1531,13 @@ te_status forward_unfused(te_context *c, size_t position, bool project) {
 // also turns the all-layers path off, as in the reference) and
 // TINYENGINE_DECODE_ALL_LAYERS=0 select the slower paths above.
 te_status forward(te_context *c, uint32_t token, size_t position, bool project) {
+    te_hip::prof_begin(nullptr);
     const te_status s = te_hip::launch_dequant_row(c->model->d_mapping + c->embd_off, c->embd_type, c->hidden,
                                                    token, c->hidden_buf, nullptr);
     if (s != TE_STATUS_OK) {
         return s;
     }
+    te_hip::prof_mark(nullptr, te_hip::kProfEmbed);
     if (env_off("TINYENGINE_FUSED_DECODE_LAYER")) {
         return forward_unfused(c, position, project);
     }
@@ -1630,9 +1652,11 @@ te_status next_token(te_context *c, Sampler &sm, uint32_t &id) {
     if (sm.temperature > 0.0f) {
         const te_hip::GemvSeg h = {c->model->d_mapping + c->head_off, c->logits, nullptr, c->vocab};
         float *xtmp = static_cast<float *>(c->ws);  // the workspace's first pieces are scratch between tokens
+        te_hip::prof_begin(nullptr);
         te_status s = te_hip::launch_gemv(c->head_type, te_hip::kGemvRmsNorm, &h, 1, c->hidden, c->hidden_buf,
                                           nullptr, c->out_norm, c->model->info.rms_norm_epsilon, xtmp,
                                           xtmp + ((std::max(c->hidden, c->ffn) + 63) / 64 * 64), nullptr);
+        te_hip::prof_mark(nullptr, te_hip::kProfLmHead);
         if (s != TE_STATUS_OK) {
             return s;
         }
@@ -1668,8 +1692,63 @@ te_status emit(const te_model *m, uint32_t id, te_token_callback cb, void *ud) {
 }
 
 // te_qwen_generate_text (qwen.c:260-400) on the GPU.
+// TINYENGINE_PROFILE (set, not "0"): one line on stderr per generate call in
+// the reference's format (qwen.c:2262-2304: total, tokenize, init and
+// embedding times, then each matvec bucket as ms/calls), followed by this
+// build's attention and elementwise buckets and the prompt / generation
+// split.  GPU buckets are HIP-event times of the launches (te_hip::prof_*);
+// total, tokenize, init, prefill and decode are wall-clock.
+struct ProfileReport {
+    typedef std::chrono::steady_clock clock;
+    bool on = false;
+    clock::time_point t0 = clock::now(), mark = t0;
+    double tokenize_ms = 0.0, init_ms = 0.0, prefill_ms = 0.0, decode_ms = 0.0;
+    size_t prompt_tokens = 0;
+    uint32_t generated = 0;
+    ProfileReport() {
+        const char *e = getenv("TINYENGINE_PROFILE");
+        on = e != nullptr && strcmp(e, "0") != 0;
+        if (on) {
+            te_hip::prof_start();
+        }
+    }
+    double lap() {  // ms since the previous lap
+        const clock::time_point t = clock::now();
+        const double ms = std::chrono::duration<double, std::milli>(t - mark).count();
+        mark = t;
+        return ms;
+    }
+    ~ProfileReport() {
+        if (!on) {
+            return;
+        }
+        (void)te_hip::prof_flush();
+        const double total = std::chrono::duration<double, std::milli>(clock::now() - t0).count();
+        using namespace te_hip;
+        double matvec = 0.0;
+        for (ProfPhase p : {kProfQ, kProfK, kProfV, kProfO, kProfGate, kProfUp, kProfDown, kProfLmHead, kProfOther}) {
+            matvec += prof_ms(p);
+        }
+        auto b = [](ProfPhase p) { return std::make_pair(prof_ms(p), prof_calls(p)); };
+        const auto q = b(kProfQ), k = b(kProfK), v = b(kProfV), o = b(kProfO), g = b(kProfGate), u = b(kProfUp),
+                   d = b(kProfDown), h = b(kProfLmHead), x = b(kProfOther), at = b(kProfAttention),
+                   ew = b(kProfElementwise);
+        fprintf(stderr,
+                "tinyengine_profile: total_ms=%.2f tokenize_ms=%.2f init_ms=%.2f embed_ms=%.2f matvec_ms=%.2f "
+                "q=%.2f/%llu k=%.2f/%llu v=%.2f/%llu o=%.2f/%llu gate=%.2f/%llu up=%.2f/%llu "
+                "down=%.2f/%llu lm_head=%.2f/%llu other=%.2f/%llu attention=%.2f/%llu elementwise=%.2f/%llu "
+                "prefill_ms=%.2f decode_ms=%.2f prompt_tokens=%zu generated_tokens=%u\n",
+                total, tokenize_ms, init_ms, prof_ms(kProfEmbed), matvec, q.first, q.second, k.first, k.second,
+                v.first, v.second, o.first, o.second, g.first, g.second, u.first, u.second, d.first, d.second,
+                h.first, h.second, x.first, x.second, at.first, at.second, ew.first, ew.second, prefill_ms,
+                decode_ms, prompt_tokens, generated);
+        prof_stop();
+    }
+};
+
 te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_token_callback cb, void *ud,
                    bool chat) {
+    ProfileReport prof;
     te_model *m = c->model;
     std::string text;
     if (chat) {
@@ -1688,6 +1767,8 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
     if (s != TE_STATUS_OK || ids.empty()) {
         return s == TE_STATUS_OK ? TE_STATUS_RUNTIME_ERROR : s;
     }
+    prof.tokenize_ms = prof.lap();
+    prof.prompt_tokens = ids.size();
     std::lock_guard<std::mutex> lock(c->mutex);
     if ((s = check_shapes(c, ids.size() + (size_t)max_tokens)) != TE_STATUS_OK) {
         return s;
@@ -1698,6 +1779,7 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
             return s;
         }
     }
+    prof.init_ms = prof.lap();
     Sampler sm;
     const bool greedy = sm.temperature <= 0.0f;
     // Cache reuse across calls on one context: the positions whose tokens
@@ -1752,6 +1834,10 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         c->history.clear();
         return s;
     }
+    if (prof.on) {
+        (void)te_hip::prof_flush();
+        prof.prefill_ms = prof.lap();
+    }
     size_t position = ids.size();
     for (uint32_t g = 0; g < max_tokens; ++g) {
         if (stop_token(m, next)) {
@@ -1760,6 +1846,7 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         if ((s = emit(m, next, cb, ud)) != TE_STATUS_OK) {
             return s;
         }
+        ++prof.generated;
         if (g + 1 == max_tokens) {
             break;
         }
@@ -1771,7 +1858,13 @@ te_status generate(te_context *c, const char *prompt, uint32_t max_tokens, te_to
         if ((s = next_token(c, sm, next)) != TE_STATUS_OK) {
             return s;
         }
+        if (prof.on) {
+            (void)te_hip::prof_flush();  // one token's marks at a time
+        }
         ++position;
+    }
+    if (prof.on) {
+        prof.decode_ms = prof.lap();
     }
     return TE_STATUS_OK;
 }

@@ -134,31 +134,37 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
     }
     const size_t ctx_kv = context_tokens * kv;
     const size_t vt_layer = te_hip_value_t_bytes(1, 1, context_tokens, kv_heads, head_dim) / sizeof(uint16_t);
+    te_hip::prof_begin(st);
     te_status s = TE_STATUS_OK;
     for (size_t l = 0; l < layers && s == TE_STATUS_OK; ++l) {
+        // each piece of the layer, then its profile mark (no-op unless profiling)
+        auto done = [&](te_status r, te_hip::ProfPhase p) {
+            te_hip::prof_mark(st, p);
+            return r == TE_STATUS_OK;
+        };
         auto gemm = [&](const uint64_t *offs, size_t n, size_t k, float *y, const float *resid) {
             return te_hip::launch_gemm_q(m + offs[l], ggml_type, b.act, batch, n, k, y, resid, b.part, b.part_bytes,
                                          st);
         };
-        if ((s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights + l * hidden, epsilon, batch, hidden,
-                                          b.act, st)) != TE_STATUS_OK ||
-            (s = gemm(q_offsets, hidden, hidden, b.q, nullptr)) != TE_STATUS_OK ||
-            (s = gemm(k_offsets, kv, hidden, b.k, nullptr)) != TE_STATUS_OK ||
-            (s = gemm(v_offsets, kv, hidden, b.v, nullptr)) != TE_STATUS_OK ||
-            (s = te_hip_attention_prefill_step_vt_f16(
-                 b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
-                 key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
-                 base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream)) !=
-                TE_STATUS_OK ||
-            (s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st)) !=
-                TE_STATUS_OK ||
-            (s = gemm(output_offsets, hidden, hidden, out, out)) != TE_STATUS_OK ||
-            (s = te_hip::launch_quant_act(1, out, nullptr, ffn_norm_weights + l * hidden, epsilon, batch, hidden,
-                                          b.act, st)) != TE_STATUS_OK ||
-            (s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr)) != TE_STATUS_OK ||
-            (s = gemm(up_offsets, ffn, hidden, b.up, nullptr)) != TE_STATUS_OK ||
-            (s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act, st)) != TE_STATUS_OK ||
-            (s = gemm(down_offsets, hidden, ffn, out, out)) != TE_STATUS_OK) {
+        const te_hip::ProfPhase ew = te_hip::kProfElementwise;
+        if (!done(s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights + l * hidden, epsilon, batch,
+                                               hidden, b.act, st), ew) ||
+            !done(s = gemm(q_offsets, hidden, hidden, b.q, nullptr), te_hip::kProfQ) ||
+            !done(s = gemm(k_offsets, kv, hidden, b.k, nullptr), te_hip::kProfK) ||
+            !done(s = gemm(v_offsets, kv, hidden, b.v, nullptr), te_hip::kProfV) ||
+            !done(s = te_hip_attention_prefill_step_vt_f16(
+                      b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
+                      key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
+                      base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream),
+                  te_hip::kProfAttention) ||
+            !done(s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st), ew) ||
+            !done(s = gemm(output_offsets, hidden, hidden, out, out), te_hip::kProfO) ||
+            !done(s = te_hip::launch_quant_act(1, out, nullptr, ffn_norm_weights + l * hidden, epsilon, batch,
+                                               hidden, b.act, st), ew) ||
+            !done(s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr), te_hip::kProfGate) ||
+            !done(s = gemm(up_offsets, ffn, hidden, b.up, nullptr), te_hip::kProfUp) ||
+            !done(s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act, st), ew) ||
+            !done(s = gemm(down_offsets, hidden, ffn, out, out), te_hip::kProfDown)) {
             break;
         }
     }
