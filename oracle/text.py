@@ -9,7 +9,12 @@ Only tests/ import it.
 - chat_prompt: tokenizer.c:52-82.
 - xorshift_uniform / sample: c/src/qwen.c:1170-1250 (xorshift64*, top-k
   with the reference's replacement order, temperature softmax in fp64,
-  `r <= acc` choice).
+  `r <= acc` choice).  xorshift_uniform is pinned to the reference's own
+  te_qwen_rng_uniform, evaluated statement by statement from its source text
+  (tests/test_model_cpu.py::test_rng_matches_reference_source); sample is
+  pinned by what fixes it (top-k 1 and a vanishing temperature are argmax,
+  the candidates are the k largest logits, draw frequencies follow the
+  tempered softmax).
 - generate: c/src/qwen.c:261-400 (prompt, then tokens until eos / padding /
   max_tokens), each token through oracle.decode_all_layers (qwen.c:907-1087)
   on an fp16 KV cache.

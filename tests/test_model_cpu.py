@@ -363,3 +363,58 @@ def test_loader_survives_corrupted_files(tmp_path, qwen_file):
         else:
             assert not h.value
     assert 0 in seen and len(seen) >= 3
+
+
+def test_rng_matches_reference_source():
+    """Pins the oracle's xorshift64* (the sampler's generator) to the
+    reference's own te_qwen_rng_uniform (c/src/qwen.c:1170-1178), read as text
+    where the reference tree is present: each statement of that function is
+    evaluated over 64-bit integers by a small interpreter that accepts only the
+    statement forms it contains (shift-xor, the state store, the multiply and
+    the final scaling), and the result must equal oracle.text.xorshift_uniform
+    for many states.  A wrong shift, direction, order or constant in the
+    oracle fails; a change of the reference's function fails loudly."""
+    import re
+    from pathlib import Path
+
+    src_path = Path("/root/reference/c/src/qwen.c")
+    if not src_path.is_file():
+        pytest.skip("reference tree not present")
+    src = src_path.read_text()
+    m = re.search(r"static double te_qwen_rng_uniform\(te_qwen_state \*state\) \{(.*?)\n\}", src, re.S)
+    assert m, "te_qwen_rng_uniform not found"
+    body = re.sub(r"/\*.*?\*/", "", m.group(1), flags=re.S)
+    stmts = [s.strip() for s in body.split(";") if s.strip()]
+    mask = (1 << 64) - 1
+
+    def run(state):
+        env = {}
+        for s in stmts:
+            if re.fullmatch(r"uint64_t x = state->rng_state", s):
+                env["x"] = state
+            elif mm := re.fullmatch(r"x \^= x (>>|<<) (\d+)", s):
+                n = int(mm.group(2))
+                env["x"] ^= (env["x"] >> n) if mm.group(1) == ">>" else ((env["x"] << n) & mask)
+            elif re.fullmatch(r"state->rng_state = x", s):
+                env["state"] = env["x"]
+            elif mm := re.fullmatch(r"const uint64_t r = x \* (0x[0-9A-Fa-f]+)ULL", s):
+                env["r"] = (env["x"] * int(mm.group(1), 16)) & mask
+            elif mm := re.fullmatch(r"return \(double\)\(r >> (\d+)\) / ([0-9.]+)", s):
+                return (env["r"] >> int(mm.group(1))) / float(mm.group(2)), env["state"]
+            else:
+                raise AssertionError(f"unexpected statement in the reference's generator: {s!r}")
+        raise AssertionError("no return")
+
+    r = random.Random(3)
+    states = [0x9E3779B97F4A7C15, 1, 2, mask] + [r.getrandbits(64) | 1 for _ in range(200)]
+    for st in states:
+        want_u, want_s = run(st)
+        got_u, got_s = OT.xorshift_uniform(st)
+        assert (got_u, got_s) == (want_u, want_s), hex(st)
+    # a chain of draws from the reference default seed
+    st = 0x9E3779B97F4A7C15
+    for _ in range(1000):
+        want_u, want_s = run(st)
+        got_u, got_s = OT.xorshift_uniform(st)
+        assert got_u == want_u and got_s == want_s
+        st = got_s
