@@ -247,6 +247,194 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const unsigned char *__rest
     }
 }
 
+// The same products with the weights staged through LDS: each K step takes a
+// chunk of kWChunk GGUF blocks of the workgroup's 64 weight rows, read as
+// 16-byte coalesced loads (a row's chunk is contiguous: 144 B for Q4_0, 272 B
+// for Q8_0, 16-byte aligned when the tensor and its row length are), one
+// chunk ahead of its use and double-buffered in LDS with a row pitch of an odd
+// dword count, so the wave's 32 rows read a block without bank conflicts.  A
+// lane's block (fp16 scale + codes) is a 5-dword LDS window whose byte
+// alignment is the same for every lane (the block index's parity), unpacked by
+// byte alignment and nibble masks.  Activation digits are prefetched two
+// blocks ahead.  Needs row_bytes % 16 == 0 and a 16-byte aligned tensor;
+// split boundaries fall on whole chunks.
+constexpr int kWChunk = 8;
+
+template <uint32_t TYPE, bool RESID>
+__global__ __launch_bounds__(256) void gemm_q2_kernel(const unsigned char *__restrict__ w, size_t row_bytes,
+                                                      const int8_t *__restrict__ hi, const int8_t *__restrict__ lo,
+                                                      const float *__restrict__ scales, int M, int N, int K, int per,
+                                                      float *out, const float *resid, float *part) {
+    constexpr int BB = TYPE == kQ4_0 ? 18 : 34;     // bytes per GGUF block
+    constexpr int CB = kWChunk * BB;                // bytes of one row's chunk
+    constexpr int PITCH = CB + 4;                   // LDS row pitch (CB is a multiple of 16)
+    constexpr int RC = CB / 16;                     // 16-byte pieces per row chunk
+    constexpr int PIECES = 64 * RC;
+    constexpr int PPT = (PIECES + 255) / 256;       // pieces per thread
+    static_assert(CB % 16 == 0 && (PITCH / 4) % 2 == 1, "chunk layout");
+    __shared__ __align__(16) unsigned char w_lds[2][64 * PITCH];
+    __shared__ __align__(16) float s_lds[2][kWChunk][64];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 31, kh = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m_wg = blockIdx.y * 64, n_wg = blockIdx.x * 64;
+    const int m0 = m_wg + wm * 32, n0 = n_wg + wn * 32;
+    const int nb = K / 32;
+    const int kb0 = blockIdx.z * per, kb1 = min(nb, kb0 + per);
+    const size_t a_tile = (size_t)(min(m0, (M - 1) & ~31) >> 5) * nb;
+    const int a_lane = lr * 32 + kh * 16;
+    const int n_chunks = (kb1 - kb0 + kWChunk - 1) / kWChunk;
+
+    // chunk c's pieces and activation scales: global -> registers (a chunk
+    // ahead), then registers -> LDS buffer
+    constexpr int SPT = kWChunk * 64 / 256;  // scales per thread
+    uint4 wreg[PPT];
+    float sreg[SPT];
+    auto load_chunk = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int t = tid + 256 * i;
+            const int rr = t & 63, cb = kb0 + c * kWChunk + (t >> 6);
+            const int row = min(m_wg + rr, M - 1);
+            sreg[i] = cb < kb1 ? scales[(size_t)row * nb + cb] : 0.0f;
+        }
+        const size_t cbyte = (size_t)(kb0 + c * kWChunk) * BB;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int item = tid + 256 * i;
+            const int r = item / RC, j = item % RC;
+            const size_t off = cbyte + 16 * (size_t)j;
+            wreg[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (item < PIECES && off < row_bytes) {  // a piece is wholly in its row or wholly past it
+                const int row = min(n_wg + r, N - 1);
+                wreg[i] = *reinterpret_cast<const uint4 *>(w + (size_t)row * row_bytes + off);
+            }
+        }
+    };
+    auto store_chunk = [&](int c, int buf) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int item = tid + 256 * i;
+            if (item < PIECES) {
+                uint32_t *dst = reinterpret_cast<uint32_t *>(&w_lds[buf][(item / RC) * PITCH + 16 * (item % RC)]);
+                dst[0] = wreg[i].x;
+                dst[1] = wreg[i].y;
+                dst[2] = wreg[i].z;
+                dst[3] = wreg[i].w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int t = tid + 256 * i;
+            s_lds[buf][t >> 6][t & 63] = sreg[i];
+        }
+        (void)c;
+    };
+    // activation digits of block b (two blocks in flight ahead of use)
+    v4i ah[4], al[4];
+    auto load_a = [&](int b, int slot) {
+        if (b < kb1) {
+            const size_t o = ((a_tile + b) << 10) + a_lane;
+            ah[slot] = *reinterpret_cast<const v4i *>(hi + o);
+            al[slot] = *reinterpret_cast<const v4i *>(lo + o);
+        }
+    };
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc[r] = 0.0f;
+    }
+    if (n_chunks > 0) {
+        load_chunk(0);
+        store_chunk(0, 0);
+        load_a(kb0, 0);
+        load_a(kb0 + 1, 1);
+    }
+    __syncthreads();
+    for (int c = 0; c < n_chunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < n_chunks) {
+            load_chunk(c + 1);
+        }
+        const unsigned char *wrow = &w_lds[buf][(wn * 32 + lr) * PITCH];
+#pragma unroll
+        for (int bb = 0; bb < kWChunk; ++bb) {
+            const int b = kb0 + c * kWChunk + bb;
+            load_a(b + 2, (bb + 2) & 3);
+            if (b < kb1) {
+                // the block's fp16 scale and 16 codes of this lane's k half: a
+                // 5-dword window starting at the block's dword (Q8_0: the half's)
+                const int blk = bb * BB;                                  // compile-time per bb
+                const int start = TYPE == kQ4_0 ? blk : blk + 16 * kh;   // the lane's codes are at start + 2
+                const uint32_t *win = reinterpret_cast<const uint32_t *>(wrow + (start & ~3));
+                uint32_t dw[5];
+#pragma unroll
+                for (int i = 0; i < 5; ++i) {
+                    dw[i] = win[i];
+                }
+                // fp16 scale: bytes blk, blk + 1 (the same dword as the window's
+                // first for Q4_0)
+                const uint32_t dwin =
+                    TYPE == kQ4_0 ? dw[0] : *reinterpret_cast<const uint32_t *>(wrow + (blk & ~3));
+                const float d = half_bits((blk & 2) ? dwin >> 16 : dwin & 0xffffu);
+                // codes: bytes start + 2 + 4k .. +3 for k = 0..3, at byte 2 or 4
+                // of the window (blk is 0 or 2 mod 4, as start is)
+                const int sh = (blk & 3) + 2;
+                uint32_t code[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    code[k] = sh == 4 ? dw[k + 1] : __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);
+                }
+                v4i bq;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (TYPE == kQ4_0) {
+                        // per byte n in 0..15: (n + 0x78) ^ 0x80 is n - 8 as int8
+                        // (no byte carries: n + 0x78 <= 0x87)
+                        const uint32_t n4 = (kh ? code[k] >> 4 : code[k]) & 0x0f0f0f0fu;
+                        bq[k] = (int)((n4 + 0x78787878u) ^ 0x80808080u);
+                    } else {
+                        bq[k] = (int)code[k];
+                    }
+                }
+                const int slot = bb & 3;
+                v16i cc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah[slot], bq, v16i{}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    cc[r] <<= 8;
+                }
+                cc = __builtin_amdgcn_mfma_i32_32x32x32_i8(al[slot], bq, cc, 0, 0, 0);
+                // lane holds column lr of rows 8 * (r / 4) + 4 * kh + r % 4
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 s4 = *reinterpret_cast<const float4 *>(&s_lds[buf][bb][wm * 32 + 8 * g + 4 * kh]);
+                    acc[4 * g + 0] = fmaf((float)cc[4 * g + 0], s4.x * d, acc[4 * g + 0]);
+                    acc[4 * g + 1] = fmaf((float)cc[4 * g + 1], s4.y * d, acc[4 * g + 1]);
+                    acc[4 * g + 2] = fmaf((float)cc[4 * g + 2], s4.z * d, acc[4 * g + 2]);
+                    acc[4 * g + 3] = fmaf((float)cc[4 * g + 3], s4.w * d, acc[4 * g + 3]);
+                }
+            }
+        }
+        if (c + 1 < n_chunks) {
+            store_chunk(c + 1, buf ^ 1);
+        }
+        __syncthreads();
+    }
+    const int col = n0 + lr;
+    if (col < N) {
+        float *dst = gridDim.z > 1 ? part + (size_t)blockIdx.z * M * N : out;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+            if (row < M) {
+                const size_t o = (size_t)row * N + col;
+                dst[o] = RESID && gridDim.z == 1 ? resid[o] + acc[r] : acc[r];
+            }
+        }
+    }
+}
+
 // out = (resid +) the splits' partial sums, added in split order.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int splits, size_t count,
                                                           const float *resid, float *out) {
@@ -319,12 +507,26 @@ te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act
            splits * 2 * rows * n * sizeof(float) <= partial_bytes) {
         splits *= 2;
     }
-    const int per = (int)((nb + splits - 1) / splits);
+    // the LDS-staged kernel where a row's chunks are 16-byte aligned; its
+    // split boundaries fall on whole chunks
+    const bool staged = ((size_t)weights & 15u) == 0 && row_bytes % 16 == 0 && getenv("TE_HIP_GEMM_V1") == nullptr;
+    int per = (int)((nb + splits - 1) / splits);
+    if (staged) {
+        per = (per + kWChunk - 1) / kWChunk * kWChunk;
+        splits = (nb + (size_t)per - 1) / (size_t)per;
+    }
     const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)splits);
     const unsigned char *w = static_cast<const unsigned char *>(weights);
-#define TE_GEMM(T, R)                                                                                             \
-    gemm_q_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n, (int)k, per, \
-                                                  out, resid, partials)
+#define TE_GEMM(T, R)                                                                                              \
+    do {                                                                                                           \
+        if (staged) {                                                                                              \
+            gemm_q2_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n,       \
+                                                           (int)k, per, out, resid, partials);                     \
+        } else {                                                                                                   \
+            gemm_q_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n, (int)k, \
+                                                          per, out, resid, partials);                              \
+        }                                                                                                          \
+    } while (0)
     if (ggml_type == kQ4_0) {
         if (resid != nullptr) {
             TE_GEMM(kQ4_0, true);
