@@ -92,6 +92,7 @@ struct PrefillArgs {
     int kv_heads;
     int group;
     int n_qtiles;
+    int paired;      // 1: unit = tile pair (n-1-i, i); 0: unit = one tile (a launch that fits one round)
     float qscale;  // log2(e)/sqrt(D), applied to the fp32 scores
     int splits;      // key splits: blockIdx.z = (seq*layers + layer) * splits + split
     float *part_o;   // splits > 1: unnormalised O per (split, seq*layer, row, head), else null
@@ -238,8 +239,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     const int half = wave >> 2;  // key half: blocks 2*step + half
     const int g = lane >> 4;
     const int c = lane & 15;
-    const int long_tile = a.n_qtiles - 1 - pair;
-    const int n_tiles_wg = pair == long_tile ? 1 : 2;  // odd tile count: the middle tile has no partner
+    const int long_tile = a.paired ? a.n_qtiles - 1 - pair : pair;
+    // odd tile count: the middle tile has no partner; unpaired units are one tile
+    const int n_tiles_wg = !a.paired || pair == long_tile ? 1 : 2;
 
     const size_t row_stride = (size_t)a.kv_heads * D;
     const f16 *kbase = a.key_cache + (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
@@ -829,6 +831,16 @@ te_status launch_value_transpose(const f16 *v, f16 *vt, size_t sl_count, size_t 
     return te_hip::launch_status();
 }
 
+// Tile pairs (n-1-i, i) give every workgroup the same causal work, which
+// balances launches of several rounds; a launch whose single tiles fit one
+// round (one workgroup per CU) takes them unpaired instead: its time is the
+// longest tile's, not a pair's (3B at L = 2048: 256 single tiles; a 2K chunk
+// after a long prefix, whose tiles all have nearly the same length).
+bool prefill_paired(size_t seqs, size_t layers, size_t tokens, size_t heads, int splits) {
+    const size_t n_qtiles = (tokens + BM - 1) / BM;
+    return n_qtiles * heads * seqs * layers * (size_t)splits > (size_t)te_hip::device_compute_units();
+}
+
 te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t tokens, size_t base_position,
                          size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim, hipStream_t strm) {
     a.layers = (int)layers;
@@ -844,8 +856,9 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
     if (a.splits < 1) {
         a.splits = 1;
     }
-    const int n_pairs = (a.n_qtiles + 1) / 2;
-    const dim3 grid((unsigned)n_pairs, (unsigned)heads, (unsigned)(seqs * layers * a.splits));
+    a.paired = prefill_paired(seqs, layers, tokens, heads, a.splits) ? 1 : 0;
+    const int n_units_x = a.paired ? (a.n_qtiles + 1) / 2 : a.n_qtiles;
+    const dim3 grid((unsigned)n_units_x, (unsigned)heads, (unsigned)(seqs * layers * a.splits));
     if (head_dim == 128) {
         prefill_causal_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
     } else {
@@ -867,13 +880,11 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
 int prefill_splits(size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t heads,
                    size_t head_dim) {
     const size_t n_qtiles = (tokens + BM - 1) / BM;
-    const size_t w0 = (n_qtiles + 1) / 2 * heads * seqs * layers;
     const size_t cus = (size_t)te_hip::device_compute_units();
     auto tile_steps = [&](size_t qt) {
         const size_t kmax = base_position + std::min(qt * BM + BM, tokens) - 1;
         return (kmax / BN + 2) / 2;
     };
-    const size_t steps = tile_steps(n_qtiles - 1) + (n_qtiles > 1 ? tile_steps(0) : 0);
     const char *env = getenv("TE_HIP_PREFILL_SPLITS");
     if (env != nullptr) {
         const long v = strtol(env, nullptr, 10);
@@ -881,14 +892,23 @@ int prefill_splits(size_t seqs, size_t layers, size_t tokens, size_t base_positi
             return (int)v;
         }
     }
+    // A unit's time in step times: its steps split S ways, plus ~2.5 steps of
+    // prologue and merge per tile it holds; units run in ceil(S*W / CUs) rounds.
+    auto launch_steps = [&](int sp) {
+        const bool paired = prefill_paired(seqs, layers, tokens, heads, sp);
+        const size_t units = (paired ? (n_qtiles + 1) / 2 : n_qtiles) * heads * seqs * layers;
+        const size_t tiles = paired && n_qtiles > 1 ? 2 : 1;
+        const size_t steps = tile_steps(n_qtiles - 1) + (tiles > 1 ? tile_steps(0) : 0);
+        return (double)((sp * units + cus - 1) / cus) * ((double)((steps + sp - 1) / sp) + 2.5 * (double)tiles);
+    };
     // partial bytes of one split, written then read, in step times
     const double split_steps = (double)(seqs * layers * tokens * heads * (head_dim + 2) * sizeof(float)) * 2.0 /
                                (8.0e12 * 2.5e-6);
+    const size_t max_steps = tile_steps(n_qtiles - 1) + (n_qtiles > 1 ? tile_steps(0) : 0);
     int best = 1;
-    double best_t = (double)((w0 + cus - 1) / cus * steps);
-    for (int sp = 2; sp <= kMaxPrefillSplits && (size_t)sp <= steps; ++sp) {
-        const double t =
-            (double)((sp * w0 + cus - 1) / cus * ((steps + sp - 1) / sp)) + 2.0 + split_steps * (double)sp;
+    double best_t = launch_steps(1);
+    for (int sp = 2; sp <= kMaxPrefillSplits && (size_t)sp <= max_steps; ++sp) {
+        const double t = launch_steps(sp) + 2.0 + split_steps * (double)sp;
         if (t < best_t && (size_t)sp * seqs * layers <= 65535) {
             best_t = t;
             best = sp;
