@@ -203,10 +203,13 @@ __global__ __launch_bounds__(64 * kMatvecWaves) void matvec_kernel(const unsigne
 // element costs 6 / 8 (Q4_0) or 3 / 4 (Q8_0) integer dot instructions.
 
 // Input pre-operations applied while staging (the decode layer fuses them
-// into its projections): kPreNone stages x; kPreRmsNorm stages x * scale * w
-// with scale = 1 / sqrtf(mean(x^2) + eps) as the reference te_rmsnorm_f32
-// (ops.c:272-293; squares summed in fp64, here per workgroup over the whole
-// vector); kPreSwiGLU stages silu(x) * x2 as te_swiglu_f32 (ops.c:397-406).
+// into its projections): kPreNone stages x; kPreRmsNorm is the reference
+// te_rmsnorm_f32 (ops.c:272-293), x * scale * w with scale = 1 / sqrtf(mean(x^2)
+// + eps), squares summed in fp64 (here per workgroup over the whole vector):
+// it stages x * w and multiplies each row's sum by the scale, which is then
+// known, at the end (the scale is common to every element, and the staging
+// does not wait for the workgroup's reduction); kPreSwiGLU stages silu(x) * x2
+// as te_swiglu_f32 (ops.c:397-406).
 enum : int { kPreNone = 0, kPreRmsNorm = 1, kPreSwiGLU = 2 };
 
 struct StageInput {
@@ -216,30 +219,100 @@ struct StageInput {
     float eps;            // kPreRmsNorm
 };
 
-// The RMSNorm scale of in.x[0, n) (n % 4 == 0) for the whole workgroup.
-__device__ __forceinline__ float workgroup_rms_scale(const StageInput &in, int n) {
-    __shared__ double part[kPairWaves];
+// The first kStageBatch float4 slices of a thread's input, loaded before the
+// kernel issues its weight loads: loads complete in issue order, so slices
+// loaded after a tile's weights would wait for all of them.  Slice u is float4
+// u * blockDim.x + threadIdx.x of x and of the operand its pre-operation needs
+// (the norm weight or the up projection); zero past the input.
+struct StagePrefetch {
+    float4 x[kStageBatch];
+    float4 y[kStageBatch];
+};
+
+template <int PRE>
+__device__ __forceinline__ void stage_prefetch(const StageInput &in, int n4, StagePrefetch &pf) {
+    const float4 *y4 = reinterpret_cast<const float4 *>(PRE == kPreRmsNorm ? in.norm_w : in.x2);
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+        const int i = u * (int)blockDim.x + (int)threadIdx.x;
+        const bool in_range = i < n4;
+        pf.x[u] = in_range ? reinterpret_cast<const float4 *>(in.x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        pf.y[u] = PRE != kPreNone && in_range ? y4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+
+// One lane's value DPP-moved (a 64-bit value as its two halves).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// The wave's sum of v, in every lane: within each 16-lane row by quad
+// exchanges 1 and 2, the half-row mirror and the row mirror, then the four row
+// sums in row order.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<0xB1>(v);
+    v += dpp_f64<0x4E>(v);
+    v += dpp_f64<0x141>(v);
+    v += dpp_f64<0x140>(v);
+    auto row = [&](int lane) {
+        return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                                __builtin_amdgcn_readlane(__double2loint(v), lane));
+    };
+    return ((row(0) + row(16)) + row(32)) + row(48);
+}
+
+// RMSNorm's scale 1 / sqrtf(mean(x^2) + eps) of in.x[0, n) (n % 4 == 0), in
+// two halves around the workgroup barrier that ends the staging, so that the
+// staging itself does not wait for it: rms_partial sums the squares of each
+// thread's slices i = threadIdx.x + k * blockDim.x in fp64 (the first
+// kStageBatch from the prefetched registers) and stores each wave's sum to
+// LDS; rms_scale, after the barrier, adds the waves' sums in wave order.
+__shared__ double rms_part[kPairWaves];
+
+__device__ __forceinline__ void rms_partial(const StageInput &in, int n, const StagePrefetch &pf) {
     double ss = 0.0;
-    for (int i = threadIdx.x; i < n / 4; i += blockDim.x) {
-        const float4 v = reinterpret_cast<const float4 *>(in.x)[i];
+    auto add = [&](const float4 v) {
         ss += (double)v.x * v.x;
         ss += (double)v.y * v.y;
         ss += (double)v.z * v.z;
         ss += (double)v.w * v.w;
-    }
+    };
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        ss += __shfl_xor(ss, o, 64);
+    for (int u = 0; u < kStageBatch; ++u) {
+        add(pf.x[u]);  // zero past the input
     }
+    for (int i = kStageBatch * (int)blockDim.x + (int)threadIdx.x; i < n / 4; i += blockDim.x) {
+        add(reinterpret_cast<const float4 *>(in.x)[i]);
+    }
+    ss = wave_sum_f64(ss);
     if ((threadIdx.x & 63) == 0) {
-        part[threadIdx.x >> 6] = ss;
+        rms_part[threadIdx.x >> 6] = ss;
     }
-    __syncthreads();
+}
+
+__device__ __forceinline__ float rms_scale(const StageInput &in, int n) {
     double total = 0.0;
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-        total += part[w];
+        total += rms_part[w];
     }
     return 1.0f / sqrtf((float)(total / (double)n) + in.eps);
+}
+
+// Cross-lane moves of the staging below as DPP operand modifiers (VALU, no LDS
+// round trip).  octet_max: the max over the aligned 8-lane group (quad
+// exchanges 1 and 2, then the half-row mirror, lane i <-> 7 - i).
+__device__ __forceinline__ float octet_max(float m) {
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+    return fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+}
+
+// Lane i + 4's value in lanes i with i % 16 < 12 (row shift left by 4).
+__device__ __forceinline__ uint32_t from_lane_plus4(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
 }
 
 // Stage the (pre-operated) input's digit planes and block scales (layout above)
@@ -249,29 +322,27 @@ __device__ __forceinline__ float workgroup_rms_scale(const StageInput &in, int n
 // lanes, which share its max and its digit dwords (pairs * 16 is a multiple of
 // 8, so those lanes agree on the bound).
 template <uint32_t TYPE, int PRE>
-__device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pairs, uint32_t *xs_lds) {
+__device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pairs, uint32_t *xs_lds,
+                                                   const StagePrefetch &pf) {
     const int nthreads = (int)blockDim.x;
     const int n4 = pairs * 16;
-    const float scale = PRE == kPreRmsNorm ? workgroup_rms_scale(in, n4 * 4) : 1.0f;
-    for (int base = 0; base < n4; base += kStageBatch * nthreads) {
-        float4 v[kStageBatch];
+    if (PRE == kPreRmsNorm) {
+        rms_partial(in, n4 * 4, pf);
+    }
+    auto pre_op = [&](float4 x, const float4 y) {
+        if (PRE == kPreRmsNorm) {
+            // x * w: the launch's epilogue multiplies each row's sum by the scale
+            x = make_float4(x.x * y.x, x.y * y.y, x.z * y.z, x.w * y.w);
+        } else if (PRE == kPreSwiGLU) {
+            x = make_float4(x.x / (1.0f + expf(-x.x)) * y.x, x.y / (1.0f + expf(-x.y)) * y.y,
+                            x.z / (1.0f + expf(-x.z)) * y.z, x.w / (1.0f + expf(-x.w)) * y.w);
+        }
+        return x;
+    };
+    // digit planes of one batch of slices v[u] = float4 base + u * nthreads + threadIdx.x
+    auto digitize = [&](const int base, const float4 (&v)[kStageBatch]) {
         // waves whose slice of a batch row starts past the input skip it (uniform branch)
         const int wave_first = base + (int)(threadIdx.x & ~63u);
-#pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            const int i = base + u * nthreads + (int)threadIdx.x;
-            v[u] = i < n4 ? reinterpret_cast<const float4 *>(in.x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (PRE == kPreRmsNorm && i < n4) {
-                const float4 w = reinterpret_cast<const float4 *>(in.norm_w)[i];
-                v[u] = make_float4(v[u].x * scale * w.x, v[u].y * scale * w.y, v[u].z * scale * w.z,
-                                   v[u].w * scale * w.w);
-            } else if (PRE == kPreSwiGLU && i < n4) {
-                const float4 up = reinterpret_cast<const float4 *>(in.x2)[i];
-                const float4 g = v[u];
-                v[u] = make_float4(g.x / (1.0f + expf(-g.x)) * up.x, g.y / (1.0f + expf(-g.y)) * up.y,
-                                   g.z / (1.0f + expf(-g.z)) * up.z, g.w / (1.0f + expf(-g.w)) * up.w);
-            }
-        }
 #pragma unroll
         for (int u = 0; u < kStageBatch; ++u) {
             if (wave_first + u * nthreads >= n4) {
@@ -279,13 +350,13 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
             }
             const int i = base + u * nthreads + (int)threadIdx.x;
             const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            // the block's max |x| over its lane octet, +inf when any value is not finite
             float m = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
-            int bad = !(isfinite(xv[0]) && isfinite(xv[1]) && isfinite(xv[2]) && isfinite(xv[3]));
-#pragma unroll
-            for (int o = 1; o <= 4; o <<= 1) {
-                m = fmaxf(m, __shfl_xor(m, o, 64));
-                bad |= __shfl_xor(bad, o, 64);
+            if (!(isfinite(xv[0]) && isfinite(xv[1]) && isfinite(xv[2]) && isfinite(xv[3]))) {
+                m = __builtin_inff();
             }
+            m = octet_max(m);
+            const bool bad = m == __builtin_inff();
             int ex = 0;
             frexpf(m, &ex);  // m < 2^ex <= 2 m
             // blocks whose max is below 2^-104 keep an absolute error of 2^-127
@@ -314,7 +385,7 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
                 // slices f and f + 4 fill the even and odd nibbles of dword f
 #pragma unroll
                 for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                    planes[t] = (planes[t] | __shfl_xor(planes[t], 4, 64)) ^ 0x88888888u;
+                    planes[t] = (planes[t] | from_lane_plus4(planes[t])) ^ 0x88888888u;
                 }
             } else {
 #pragma unroll
@@ -344,6 +415,31 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
                 }
             }
         }
+    };
+    // The first batch from the prefetched slices, outside the loop below: the
+    // wait for them then leaves the weight loads issued after them in flight.
+    {
+        float4 v[kStageBatch];
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            v[u] = u * nthreads + (int)threadIdx.x < n4 ? pre_op(pf.x[u], pf.y[u]) : pf.x[u];
+        }
+        digitize(0, v);
+    }
+    for (int base = kStageBatch * nthreads; base < n4; base += kStageBatch * nthreads) {
+        float4 v[kStageBatch];
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int i = base + u * nthreads + (int)threadIdx.x;
+            v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (i < n4) {
+                const float4 y = PRE == kPreNone
+                                     ? v[u]
+                                     : reinterpret_cast<const float4 *>(PRE == kPreRmsNorm ? in.norm_w : in.x2)[i];
+                v[u] = pre_op(reinterpret_cast<const float4 *>(in.x)[i], y);
+            }
+        }
+        digitize(base, v);
     }
 }
 
@@ -438,11 +534,14 @@ __global__ __launch_bounds__(kPairThreads) void matvec_pairs_kernel(const unsign
             }
         }
     };
+    const StageInput in{input, nullptr, nullptr, 0.0f};
+    StagePrefetch pf;
+    stage_prefetch<kPreNone>(in, pairs * 16, pf);
     if (gwave < tiles) {
         load(wa, gwave, 0);
     }
 
-    stage_digit_planes<TYPE, kPreNone>(StageInput{input, nullptr, nullptr, 0.0f}, pairs, xs_lds);
+    stage_digit_planes<TYPE, kPreNone>(in, pairs, xs_lds, pf);
     __syncthreads();
     if (gwave >= tiles) {
         return;
@@ -603,34 +702,43 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
 
     // A tile's loads: its weight chunks and (residual launches) the residuals of
     // its rows, issued together one tile ahead, so the wait for them at the next
-    // tile's start never waits for loads issued later.
+    // tile's start never waits for loads issued later.  Every lane issues every
+    // load (lanes past the tile re-read its last chunk, a wave with no tile
+    // reads one chunk) and
+    // nothing uses them until the tile's start: no branch or select waits on
+    // them, so the staging below never waits for the weight loads.
     u32x4 ck[CH] = {};
     float res[NR];
-    auto load = [&](int tile) {
+    auto load = [&](int tile, bool live) {
         int local;
         const StreamSeg sg = seg_of(tile, local);
         const size_t b = (size_t)local * tile_bytes;
         const size_t c0 = b >> 4;
         const size_t c1 = min((b + tile_bytes + 15) >> 4, sg.total_chunks);
+        const size_t c_last = live ? c1 - 1 : c0;
         const u32x4 *w16 = reinterpret_cast<const u32x4 *>(sg.w);
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            const size_t c = c0 + lane + 64 * i;
-            if (c < c1) {
-                ck[i] = __builtin_nontemporal_load(w16 + c);
-            }
+            ck[i] = __builtin_nontemporal_load(w16 + min(c0 + lane + 64 * i, c_last));
         }
+        // (the tile's epilogue adds res only for residual launches, in lane 0 of
+        // a group, to rows < rows; other launches read the first 4 * rows bytes
+        // of their weights, a valid range with one address per row)
+        const float *rp = sg.resid != nullptr ? sg.resid : reinterpret_cast<const float *>(sg.w);
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             const int row = (local * G + grp) * NR + r;
-            res[r] = sg.resid != nullptr && li == 0 && row < sg.rows ? sg.resid[row] : 0.0f;
+            res[r] = rp[min(row, sg.rows - 1)];
         }
     };
-    if (gwave < a.tiles) {
-        load(gwave);
-    }
-    stage_digit_planes<TYPE, PRE>(a.in, pairs, xs_lds);
+    // The input slices, then the tile's weight loads: the staging waits for
+    // the input only.
+    StagePrefetch pf;
+    stage_prefetch<PRE>(a.in, pairs * 16, pf);
+    load(min(gwave, a.tiles - 1), gwave < a.tiles);
+    stage_digit_planes<TYPE, PRE>(a.in, pairs, xs_lds, pf);
     __syncthreads();
+    const float rms = PRE == kPreRmsNorm ? rms_scale(a.in, pairs * 64) : 1.0f;
     if (gwave >= a.tiles) {
         return;
     }
@@ -672,7 +780,7 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
         const StreamSeg sg = seg_of(tile, local);
         const int tn = tile + nwaves;
         if (tn < a.tiles) {
-            load(tn);
+            load(tn, true);
         }
         const unsigned char *tb =
             reinterpret_cast<const unsigned char *>(buf) + (((size_t)local * tile_bytes) & 15);
@@ -705,6 +813,9 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
             const int row = (local * G + grp) * NR + r;
             if (li == 0 && row < sg.rows) {
                 // the residual add of the reference's te_add_f32(hidden, proj)
+                if (PRE == kPreRmsNorm) {
+                    v *= rms;
+                }
                 sg.out[row] = sg.resid != nullptr ? res_cur[r] + v : v;
             }
             acc[r] = 0.0f;
