@@ -118,6 +118,13 @@ def test_decode_all_layers_head_dim_128_in_place(oracle_mod):
          in_place=True, head_type=8)
 
 
+def test_decode_all_layers_separate_gate_up(oracle_mod, monkeypatch):
+    """TE_HIP_GEMV_GLU=0: gate and up as two projections, the SwiGLU staged by
+    the down projection (the path of shapes whose tiles cannot pair them)."""
+    monkeypatch.setenv("TE_HIP_GEMV_GLU", "0")
+    _run(oracle_mod, 2, layers=2, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=500, ctx=32, position=11)
+
+
 def test_decode_all_layers_first_position_no_head(oracle_mod):
     _run(oracle_mod, 8, layers=2, heads=4, kv_heads=4, head_dim=64, ffn=256, vocab=100, ctx=16, position=0,
          head=False)

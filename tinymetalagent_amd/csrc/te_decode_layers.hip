@@ -190,16 +190,24 @@ extern "C" te_status te_hip_decode_all_layers_f16(
             break;
         }
         prof_mark(st, te_hip::kProfO);
-        const te_hip::GemvSeg gu[2] = {{m + gate_offsets[l], b.gate, nullptr, ffn},
-                                       {m + up_offsets[l], b.up, nullptr, ffn}};
-        s = te_hip::launch_gemv(ggml_type, te_hip::kGemvRmsNorm, gu, 2, hidden, out, nullptr,
-                                ffn_norm_weights + l * hidden, epsilon, b.xtmp, b.proj, st);
+        // gate / up with the SwiGLU in their epilogue (h into b.gate) where the
+        // shapes allow it, else both projections and the SwiGLU staged by down
+        bool glu = false;
+        s = te_hip::launch_gemv_glu(ggml_type, m + gate_offsets[l], m + up_offsets[l], ffn, hidden, out,
+                                    ffn_norm_weights + l * hidden, epsilon, b.gate, st, &glu);
+        if (s == TE_STATUS_OK && !glu) {
+            const te_hip::GemvSeg gu[2] = {{m + gate_offsets[l], b.gate, nullptr, ffn},
+                                           {m + up_offsets[l], b.up, nullptr, ffn}};
+            s = te_hip::launch_gemv(ggml_type, te_hip::kGemvRmsNorm, gu, 2, hidden, out, nullptr,
+                                    ffn_norm_weights + l * hidden, epsilon, b.xtmp, b.proj, st);
+        }
         if (s != TE_STATUS_OK) {
             break;
         }
         prof_mark(st, gu_share, 2);
         const te_hip::GemvSeg d = {m + down_offsets[l], out, out, hidden};
-        s = te_hip::launch_gemv(ggml_type, te_hip::kGemvSwiGLU, &d, 1, ffn, b.gate, b.up, nullptr, 0.0f, b.xtmp, b.proj, st);
+        s = te_hip::launch_gemv(ggml_type, glu ? te_hip::kGemvPlain : te_hip::kGemvSwiGLU, &d, 1, ffn, b.gate,
+                                b.up, nullptr, 0.0f, b.xtmp, b.proj, st);
         prof_mark(st, te_hip::kProfDown);
     }
     if (s == TE_STATUS_OK && out_token_id != nullptr) {

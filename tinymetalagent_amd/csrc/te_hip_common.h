@@ -145,6 +145,14 @@ enum GemvPre { kGemvPlain = 0, kGemvRmsNorm = 1, kGemvSwiGLU = 2 };
 te_status launch_gemv(uint32_t ggml_type, GemvPre pre, const GemvSeg *segs, int nseg, size_t cols, const float *x,
                       const float *x2, const float *norm_w, float eps, float *xtmp, float *ytmp,
                       hipStream_t stream);
+// The gate and up projections of one RMSNorm input in one streamed launch
+// whose tiles hold the same rows of both, writing h[r] = silu(gate[r]) * up[r]
+// (as te_swiglu_f32) and neither projection.  *launched stays false, with OK,
+// when the shapes do not suit it (then launch_gemv and a SwiGLU pre-operation
+// on the down projection do the same work).
+te_status launch_gemv_glu(uint32_t ggml_type, const void *gate_w, const void *up_w, size_t rows, size_t cols,
+                          const float *x, const float *norm_w, float eps, float *h, hipStream_t stream,
+                          bool *launched);
 
 DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
                                size_t kv_heads);

@@ -23,6 +23,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <string.h>
 
 namespace {
 
@@ -362,35 +363,37 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
             // blocks whose max is below 2^-104 keep an absolute error of 2^-127
             const int e = bad || m == 0.0f ? 0 : min(22 - ex, 126);
             const int f = i & 7;
-            uint32_t planes[kDigitPlanes<TYPE>] = {};
             // Balanced digits from plain ones: with B = sum_t 8 * 16^t (Q4_0) or
             // sum_t 128 * 256^t (Q8_0), Y = X + B lies in [0, 2^24), and digit t of X is
             // (digit t of Y) - 8 (or - 128), whose 4- (8-) bit two's complement is
-            // digit t of Y with its top bit flipped: one field extract per digit, the
-            // flips done on whole plane dwords.
+            // digit t of Y with its top bit flipped, the flips done on whole dwords.
+            uint32_t y[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int xq = bad ? 0 : (int)rintf(ldexpf(xv[j], e));  // |xq| <= 2^22
-                const uint32_t y = (uint32_t)(xq + (TYPE == kGgmlQ4_0 ? 0x888888 : 0x808080));
-#pragma unroll
-                for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                    if (TYPE == kGgmlQ4_0) {
-                        planes[t] |= ((y >> (4 * t)) & 15u) << (8 * j + ((f & 4) ? 4 : 0));
-                    } else {
-                        planes[t] |= ((y >> (8 * t)) & 255u) << (8 * j);
-                    }
-                }
+                y[j] = (uint32_t)(xq + (TYPE == kGgmlQ4_0 ? 0x888888 : 0x808080));
             }
-            if (TYPE == kGgmlQ4_0) {
-                // slices f and f + 4 fill the even and odd nibbles of dword f
+            // Byte k of the four values into byte planes yb[k] (byte j = byte k of
+            // y[j]) by v_perm_b32: bytes 0 and 1, then byte 2, of value pairs, then
+            // the pairs' halves (selector byte 0x0c is a zero byte).
+            const uint32_t p01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
+            const uint32_t p23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+            const uint32_t q01 = __builtin_amdgcn_perm(y[1], y[0], 0x0C0C0602u);
+            const uint32_t q23 = __builtin_amdgcn_perm(y[3], y[2], 0x0C0C0602u);
+            const uint32_t yb[3] = {__builtin_amdgcn_perm(p23, p01, 0x05040100u),
+                                    __builtin_amdgcn_perm(p23, p01, 0x07060302u),
+                                    __builtin_amdgcn_perm(q23, q01, 0x05040100u)};
+            uint32_t planes[kDigitPlanes<TYPE>];
 #pragma unroll
-                for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                    planes[t] = (planes[t] | from_lane_plus4(planes[t])) ^ 0x88888888u;
-                }
-            } else {
-#pragma unroll
-                for (int t = 0; t < kDigitPlanes<TYPE>; ++t) {
-                    planes[t] ^= 0x80808080u;
+            for (int k = 0; k < 3; ++k) {
+                if (TYPE == kGgmlQ4_0) {
+                    // nibble planes 2k and 2k + 1: slice f's nibbles low, slice f + 4's high
+                    const uint32_t lo = yb[k] ^ 0x88888888u;
+                    const uint32_t hi = from_lane_plus4(lo);
+                    planes[2 * k] = (lo & 0x0F0F0F0Fu) | ((hi << 4) & 0xF0F0F0F0u);
+                    planes[2 * k + 1] = ((lo >> 4) & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
+                } else {
+                    planes[k] = yb[k] ^ 0x80808080u;
                 }
             }
             if (i < n4) {
@@ -663,10 +666,18 @@ struct StreamArgs {
     StageInput in;
 };
 
-template <uint32_t TYPE, int LPR, int NR, int CH, int PRE>
+//
+// GLU launches (the decode layer's gate and up projections, seg[0] = gate
+// with the output, seg[1] = up): a tile holds the same NR * G / 2 rows of
+// both matrices, gate rows in the first G / 2 row groups (their chunks in the
+// first CH / 2 KB of the tile buffer), up rows in the rest, and the epilogue
+// writes silu(gate) * up as te_swiglu_f32 (ops.c:397-406) instead of either.
+template <uint32_t TYPE, int LPR, int NR, int CH, int PRE, bool GLU>
 __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const StreamArgs a) {
     constexpr int PW = TYPE == kGgmlQ4_0 ? 9 : 17;  // dwords per block pair
     constexpr int G = 64 / LPR;                      // row groups per wave
+    constexpr int HG = GLU ? G / 2 : G;              // row groups per matrix of a tile
+    static_assert(!GLU || (G >= 2 && CH % 2 == 0), "GLU tiles split the row groups and chunks in two");
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     extern __shared__ uint4 lds4[];  // [pairs][13] digit planes + scales, then one CH KB tile buffer per wave
     uint32_t *const xs_lds = reinterpret_cast<uint32_t *>(lds4);
@@ -681,7 +692,7 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
     const int nwaves = gridDim.x * (int)(blockDim.x >> 6);
     const int pairs = a.cols / 64;
     const int steps = (pairs + LPR - 1) / LPR;  // pair steps per tile
-    const size_t tile_bytes = (size_t)G * NR * a.row_bytes;
+    const size_t tile_bytes = (size_t)HG * NR * a.row_bytes;  // one matrix's rows of a tile
     uint4 *const buf = lds4 + pairs * 13 + wave * CH * 64;
 
     // Segment of global tile t, as values chosen by scalar selects: indexing the
@@ -708,7 +719,7 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
     // nothing uses them until the tile's start: no branch or select waits on
     // them, so the staging below never waits for the weight loads.
     u32x4 ck[CH] = {};
-    float res[NR];
+    float res[NR] = {};
     auto load = [&](int tile, bool live) {
         int local;
         const StreamSeg sg = seg_of(tile, local);
@@ -717,6 +728,16 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
         const size_t c1 = min((b + tile_bytes + 15) >> 4, sg.total_chunks);
         const size_t c_last = live ? c1 - 1 : c0;
         const u32x4 *w16 = reinterpret_cast<const u32x4 *>(sg.w);
+        if (GLU) {
+            // the same byte range of the up matrix (equal shapes) into the second half
+            const u32x4 *u16 = reinterpret_cast<const u32x4 *>(a.seg[1].w);
+#pragma unroll
+            for (int i = 0; i < CH / 2; ++i) {
+                ck[i] = __builtin_nontemporal_load(w16 + min(c0 + lane + 64 * i, c_last));
+                ck[CH / 2 + i] = __builtin_nontemporal_load(u16 + min(c0 + lane + 64 * i, c_last));
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             ck[i] = __builtin_nontemporal_load(w16 + min(c0 + lane + 64 * i, c_last));
@@ -793,7 +814,8 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
 #pragma unroll
                 for (int r = 0; r < NR; ++r) {
                     const uint32_t *src = reinterpret_cast<const uint32_t *>(
-                        tb + (size_t)(grp * NR + r) * a.row_bytes + (size_t)p * 4 * PW);
+                        tb + (GLU && grp >= HG ? (size_t)(CH / 2) * 1024 : 0) +
+                        (size_t)((grp % HG) * NR + r) * a.row_bytes + (size_t)p * 4 * PW);
                     uint32_t w[PW];
 #pragma unroll
                     for (int k = 0; k < PW; ++k) {
@@ -809,6 +831,17 @@ __global__ __launch_bounds__(kPairThreads) void matvec_stream_kernel(const Strea
 #pragma unroll
             for (int o = LPR / 2; o >= 1; o >>= 1) {
                 v += __shfl_xor(v, o, 64);
+            }
+            if (GLU) {
+                // lanes 32 apart hold the gate and up sums of the same row
+                const float g = v * rms;
+                const float u = __shfl_xor(g, 32, 64);
+                const int row = (local * HG + grp) * NR + r;
+                if (li == 0 && grp < HG && row < sg.rows) {
+                    sg.out[row] = g / (1.0f + expf(-g)) * u;
+                }
+                acc[r] = 0.0f;
+                continue;
             }
             const int row = (local * G + grp) * NR + r;
             if (li == 0 && row < sg.rows) {
@@ -984,10 +1017,12 @@ size_t ggml_row_bytes(uint32_t ggml_type, size_t cols) {
 // weight tensor not 16-byte aligned or not a multiple of 16 bytes long, a row
 // group longer than the 10 KB tile, or staged input leaving LDS for fewer than
 // 4 waves.
-te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t stream, bool *launched) {
+te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t stream, bool *launched,
+                        bool glu = false) {
     *launched = false;
     const size_t cols = (size_t)a.cols;
-    if ((ggml_type != kGgmlQ4_0 && ggml_type != kGgmlQ8_0) || cols % 64 != 0 || a.nseg < 1 || a.nseg > 3) {
+    if ((ggml_type != kGgmlQ4_0 && ggml_type != kGgmlQ8_0) || cols % 64 != 0 || a.nseg < 1 || a.nseg > 3 ||
+        (glu && (a.nseg != 2 || pre != kPreRmsNorm || a.seg[0].rows != a.seg[1].rows))) {
         return TE_STATUS_OK;
     }
     const size_t row_bytes = ggml_row_bytes(ggml_type, cols);
@@ -1003,6 +1038,11 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
     }
     const int lpr = pairs >= 64 ? 64 : pairs >= 32 ? 32 : 16;
     const size_t groups = 64 / lpr;
+    if (glu && groups < 2) {
+        return TE_STATUS_OK;  // a GLU tile needs a row group of each matrix
+    }
+    // a GLU tile's rows of one matrix fill half its buffer
+    const size_t hgroups = glu ? groups / 2 : groups;
     const size_t cus = (size_t)device_compute_units();
     const size_t want = cus * 8;
     // tiles of at most 10 KB (larger tiles measured faster at lm_head, 4 / 8 / 12 KB: more bytes
@@ -1013,16 +1053,18 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
     }
     int nr = 1;
     for (int cand = 2; cand <= (ggml_type == kGgmlQ4_0 ? 4 : 2); cand *= 2) {
-        if (groups * cand * row_bytes + 15 <= tile_cap && rows_total >= cand * groups * want) {
+        if (hgroups * cand * row_bytes + 15 <= (glu ? tile_cap / 2 : tile_cap) &&
+            rows_total >= cand * groups * want) {
             nr = cand;
         }
     }
     // Q8_0 rows of 10-12 KB (ffn_down at 11008 columns: 11696 bytes) take
     // 12-chunk tiles, one row per tile
-    const bool wide = ggml_type == kGgmlQ8_0 && groups == 1 && row_bytes + 15 > kStreamTileBytes &&
+    const bool wide = !glu && ggml_type == kGgmlQ8_0 && groups == 1 && row_bytes + 15 > kStreamTileBytes &&
                       row_bytes + 15 <= (size_t)kWideStreamChunks * 1024;
     const size_t tile_lds = wide ? (size_t)kWideStreamChunks * 1024 : kStreamTileBytes;
-    const size_t waves_fit = groups * row_bytes + 15 <= tile_lds && plane_bytes < kMaxPairLdsBytes
+    const size_t waves_fit = hgroups * row_bytes + 15 <= (glu ? tile_lds / 2 : tile_lds) &&
+                                     plane_bytes < kMaxPairLdsBytes
                                  ? (kMaxPairLdsBytes - plane_bytes) / tile_lds
                                  : 0;
     if (waves_fit < 4) {
@@ -1034,29 +1076,39 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
     a.tiles = 0;
     for (int s = 0; s < a.nseg; ++s) {
         const size_t rows = (size_t)a.seg[s].rows;
-        a.seg[s].tiles = (int)((rows + groups * nr - 1) / (groups * nr));
+        a.seg[s].tiles = (int)((rows + hgroups * nr - 1) / (hgroups * nr));
         a.seg[s].total_chunks = rows * row_bytes / 16;
         a.tiles += a.seg[s].tiles;
     }
+    if (glu) {
+        // every tile is the gate matrix's (segment 0); the up rows ride along
+        a.tiles = a.seg[0].tiles;
+        a.seg[1].tiles = 0;
+    }
     const dim3 grid((unsigned)((size_t)a.tiles < cus ? (size_t)a.tiles : cus));
-#define TE_STREAM(T, L, N, P)                                                                                      \
-    do {                                                                                                           \
-        if (lds > 65536 &&                                                                                         \
-            hipFuncSetAttribute(reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, kStreamChunks, P>),  \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {             \
-            return TE_STATUS_RUNTIME_ERROR;                                                                        \
-        }                                                                                                          \
-        matvec_stream_kernel<T, L, N, kStreamChunks, P><<<grid, dim3(64 * wpg), lds, stream>>>(a);                 \
+#define TE_STREAM(T, L, N, P, GL)                                                                                 \
+    do {                                                                                                          \
+        if (lds > 65536 &&                                                                                        \
+            hipFuncSetAttribute(                                                                                  \
+                reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, kStreamChunks, P, GL>),             \
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {                            \
+            return TE_STATUS_RUNTIME_ERROR;                                                                       \
+        }                                                                                                         \
+        matvec_stream_kernel<T, L, N, kStreamChunks, P, GL><<<grid, dim3(64 * wpg), lds, stream>>>(a);            \
     } while (0)
-#define TE_STREAM_PRE(T, L, N)                \
-    do {                                      \
-        if (pre == kPreRmsNorm) {             \
-            TE_STREAM(T, L, N, kPreRmsNorm);  \
-        } else if (pre == kPreSwiGLU) {       \
-            TE_STREAM(T, L, N, kPreSwiGLU);   \
-        } else {                              \
-            TE_STREAM(T, L, N, kPreNone);     \
-        }                                     \
+#define TE_STREAM_PRE(T, L, N)                       \
+    do {                                             \
+        if (glu) {                                   \
+            if constexpr (L <= 32) {                 \
+                TE_STREAM(T, L, N, kPreRmsNorm, true); \
+            }                                        \
+        } else if (pre == kPreRmsNorm) {             \
+            TE_STREAM(T, L, N, kPreRmsNorm, false);  \
+        } else if (pre == kPreSwiGLU) {              \
+            TE_STREAM(T, L, N, kPreSwiGLU, false);   \
+        } else {                                     \
+            TE_STREAM(T, L, N, kPreNone, false);     \
+        }                                            \
     } while (0)
 #define TE_STREAM_NR(T, L)                                    \
     do {                                                      \
@@ -1083,11 +1135,11 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
     do {                                                                                                            \
         if (lds > 65536 &&                                                                                          \
             hipFuncSetAttribute(                                                                                    \
-                reinterpret_cast<const void *>(&matvec_stream_kernel<kGgmlQ8_0, 64, 1, kWideStreamChunks, P>),      \
+                reinterpret_cast<const void *>(&matvec_stream_kernel<kGgmlQ8_0, 64, 1, kWideStreamChunks, P, false>), \
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {                              \
             return TE_STATUS_RUNTIME_ERROR;                                                                         \
         }                                                                                                           \
-        matvec_stream_kernel<kGgmlQ8_0, 64, 1, kWideStreamChunks, P><<<grid, dim3(64 * wpg), lds, stream>>>(a);     \
+        matvec_stream_kernel<kGgmlQ8_0, 64, 1, kWideStreamChunks, P, false><<<grid, dim3(64 * wpg), lds, stream>>>(a); \
     } while (0)
         if (pre == kPreRmsNorm) {
             TE_STREAM_WIDE(kPreRmsNorm);
@@ -1252,6 +1304,23 @@ te_status launch_gemv(uint32_t ggml_type, GemvPre pre, const GemvSeg *segs, int 
         }
     }
     return st;
+}
+
+te_status launch_gemv_glu(uint32_t ggml_type, const void *gate_w, const void *up_w, size_t rows, size_t cols,
+                          const float *x, const float *norm_w, float eps, float *h, hipStream_t stream,
+                          bool *launched) {
+    *launched = false;
+    const char *glu_env = getenv("TE_HIP_GEMV_GLU");
+    if (getenv("TE_HIP_GEMV_STRIDED") != nullptr || (glu_env != nullptr && strcmp(glu_env, "0") == 0)) {
+        return TE_STATUS_OK;  // the switches that take the separate launches
+    }
+    StreamArgs a = {};
+    a.seg[0] = StreamSeg{static_cast<const unsigned char *>(gate_w), h, nullptr, 0, (int)rows, 0};
+    a.seg[1] = StreamSeg{static_cast<const unsigned char *>(up_w), nullptr, nullptr, 0, (int)rows, 0};
+    a.nseg = 2;
+    a.cols = (int)cols;
+    a.in = StageInput{x, nullptr, norm_w, eps};
+    return launch_stream(ggml_type, kPreRmsNorm, a, stream, launched, true);
 }
 
 te_status launch_dequant_row(const void *weights, uint32_t ggml_type, size_t cols, size_t row, float *out,
