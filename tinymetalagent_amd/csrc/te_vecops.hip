@@ -38,7 +38,8 @@ constexpr size_t kMaxPairLdsBytes = 160 * 1024;     // staged digit planes (gfx9
 constexpr size_t kPairLdsBytes = 13 * 16;           // LDS per block pair: 12 uint4 of digit planes + scales
 constexpr int kStreamChunks = 10;                   // streamed kernel: 16-byte chunk loads per lane per tile
 constexpr size_t kStreamTileBytes = kStreamChunks * 1024;  // its LDS tile buffer per wave
-constexpr int kWideStreamChunks = 12;                // Q8_0 rows of 10-12 KB, one row per tile
+constexpr int kWideStreamChunks = 12;
+constexpr int kShortStreamChunks = 4;               // one-row-per-group tiles of at most 4 KB                // Q8_0 rows of 10-12 KB, one row per tile
 template <uint32_t TYPE>
 constexpr int kDigitPlanes = TYPE == kGgmlQ4_0 ? 6 : 3;  // balanced base-16 / base-256 digits of 22-bit X
 
@@ -1062,7 +1063,12 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
     // 12-chunk tiles, one row per tile
     const bool wide = !glu && ggml_type == kGgmlQ8_0 && groups == 1 && row_bytes + 15 > kStreamTileBytes &&
                       row_bytes + 15 <= (size_t)kWideStreamChunks * 1024;
-    const size_t tile_lds = wide ? (size_t)kWideStreamChunks * 1024 : kStreamTileBytes;
+    // Small tiles take 4-chunk loads: every lane issues every chunk load of a
+    // tile (lanes past it re-read its last chunk), so the load count follows
+    // the tile, not the largest one.
+    const bool short_tile = !glu && !wide && nr == 1 && groups * row_bytes + 15 <= (size_t)kShortStreamChunks * 1024;
+    const size_t tile_lds = wide ? (size_t)kWideStreamChunks * 1024
+                                 : short_tile ? (size_t)kShortStreamChunks * 1024 : kStreamTileBytes;
     const size_t waves_fit = hgroups * row_bytes + 15 <= (glu ? tile_lds / 2 : tile_lds) &&
                                      plane_bytes < kMaxPairLdsBytes
                                  ? (kMaxPairLdsBytes - plane_bytes) / tile_lds
@@ -1086,39 +1092,40 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
         a.seg[1].tiles = 0;
     }
     const dim3 grid((unsigned)((size_t)a.tiles < cus ? (size_t)a.tiles : cus));
-#define TE_STREAM(T, L, N, P, GL)                                                                                 \
-    do {                                                                                                          \
-        if (lds > 65536 &&                                                                                        \
-            hipFuncSetAttribute(                                                                                  \
-                reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, kStreamChunks, P, GL>),             \
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {                            \
-            return TE_STATUS_RUNTIME_ERROR;                                                                       \
-        }                                                                                                         \
-        matvec_stream_kernel<T, L, N, kStreamChunks, P, GL><<<grid, dim3(64 * wpg), lds, stream>>>(a);            \
+#define TE_STREAM(T, L, N, C, P, GL)                                                                      \
+    do {                                                                                                  \
+        if (lds > 65536 &&                                                                                \
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&matvec_stream_kernel<T, L, N, C, P, GL>), \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {    \
+            return TE_STATUS_RUNTIME_ERROR;                                                               \
+        }                                                                                                 \
+        matvec_stream_kernel<T, L, N, C, P, GL><<<grid, dim3(64 * wpg), lds, stream>>>(a);                \
     } while (0)
-#define TE_STREAM_PRE(T, L, N)                       \
-    do {                                             \
-        if (glu) {                                   \
-            if constexpr (L <= 32) {                 \
-                TE_STREAM(T, L, N, kPreRmsNorm, true); \
-            }                                        \
-        } else if (pre == kPreRmsNorm) {             \
-            TE_STREAM(T, L, N, kPreRmsNorm, false);  \
-        } else if (pre == kPreSwiGLU) {              \
-            TE_STREAM(T, L, N, kPreSwiGLU, false);   \
-        } else {                                     \
-            TE_STREAM(T, L, N, kPreNone, false);     \
-        }                                            \
+#define TE_STREAM_PRE(T, L, N, C)                          \
+    do {                                                   \
+        if (glu) {                                         \
+            if constexpr (L <= 32 && C == kStreamChunks) { \
+                TE_STREAM(T, L, N, C, kPreRmsNorm, true);  \
+            }                                              \
+        } else if (pre == kPreRmsNorm) {                   \
+            TE_STREAM(T, L, N, C, kPreRmsNorm, false);     \
+        } else if (pre == kPreSwiGLU) {                    \
+            TE_STREAM(T, L, N, C, kPreSwiGLU, false);      \
+        } else {                                           \
+            TE_STREAM(T, L, N, C, kPreNone, false);        \
+        }                                                  \
     } while (0)
-#define TE_STREAM_NR(T, L)                                    \
-    do {                                                      \
-        if (nr == 4) {                                        \
-            TE_STREAM_PRE(T, L, (T == kGgmlQ4_0 ? 4 : 2));    \
-        } else if (nr == 2) {                                 \
-            TE_STREAM_PRE(T, L, 2);                           \
-        } else {                                              \
-            TE_STREAM_PRE(T, L, 1);                           \
-        }                                                     \
+#define TE_STREAM_NR(T, L)                                                \
+    do {                                                                  \
+        if (nr == 4) {                                                    \
+            TE_STREAM_PRE(T, L, (T == kGgmlQ4_0 ? 4 : 2), kStreamChunks); \
+        } else if (nr == 2) {                                             \
+            TE_STREAM_PRE(T, L, 2, kStreamChunks);                        \
+        } else if (short_tile) {                                          \
+            TE_STREAM_PRE(T, L, 1, kShortStreamChunks);                   \
+        } else {                                                          \
+            TE_STREAM_PRE(T, L, 1, kStreamChunks);                        \
+        }                                                                 \
     } while (0)
 #define TE_STREAM_LPR(T)          \
     do {                          \
