@@ -396,6 +396,24 @@ TE_API te_status te_hip_add_f32(const float *lhs, const float *rhs, size_t len, 
 TE_API te_status te_hip_argmax_f32(const float *values, size_t len, uint32_t *out_index, void *stream);
 
 /*
+ * Top-k temperature sampling of the next token from device logits: the
+ * reference sampler (c/src/qwen.c:1182-1250; candidate scan :1198-1225,
+ * xorshift64* :1170-1178), which te_qwen_generate_text runs on host logits.
+ * It has no Metal counterpart: the reference copies the logits back.  Here
+ * the device keeps the logits that can enter the candidate list (above a
+ * lower bound of the k-th largest logit before them) and the host runs the
+ * reference's scan and draw over those, so the token and the next *rng_state
+ * equal the reference's for the same logits (any NaN logit: the host scans
+ * them all).  top_k 0 means 1; k is capped at 1024 and at vocab.  Blocks the
+ * caller (the read-back is synchronous).  workspace: device memory of
+ * te_hip_sample_workspace_bytes(vocab) bytes.
+ */
+TE_API size_t te_hip_sample_workspace_bytes(size_t vocab);
+TE_API te_status te_hip_sample_top_k_f32(const float *logits, size_t vocab, uint32_t top_k, float temperature,
+                                         uint64_t *rng_state, uint32_t *out_token, void *workspace,
+                                         size_t workspace_bytes, void *stream);
+
+/*
  * Quantized GEMM of batched prompt prefill: out[m][n] = sum_k pre(x)[m][k] *
  * W[n][k] (+ resid[m][n]) for `rows` activation rows at once -- the per-row
  * meaning of te_model_matvec_f32 (ops.c:177-269) for the projections of

@@ -26,7 +26,7 @@ INCLUDE = ROOT / "include"
 LIBRARY = PKG / "libtinyengine.so"
 
 HIP_SOURCES = ["te_rope_append.hip", "te_decode.hip", "te_prefill.hip", "te_mma_kat.hip", "te_calibrate.hip",
-               "te_vecops.hip", "te_decode_layers.hip", "te_prefill_layers.hip", "te_gemm.hip", "te_model.hip",
+               "te_vecops.hip", "te_decode_layers.hip", "te_prefill_layers.hip", "te_gemm.hip", "te_sample.hip", "te_model.hip",
                "te_hip_runtime.hip"]
 C_SOURCES = ["te_abi.c"]
 

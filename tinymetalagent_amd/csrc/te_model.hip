@@ -11,8 +11,9 @@
 // matvec run there, and generation runs one token at a time through
 // te_hip_decode_all_layers_f16 (every layer, then the head) with the embedding
 // lookup, RoPE tables, fp16 KV cache and gathered norm / bias arrays in HBM.
-// Greedy decoding takes the fused head + argmax; temperature sampling copies
-// the logits back and samples on the host as the reference does.
+// Greedy decoding takes the fused head + argmax; temperature sampling runs the
+// head, keeps the logits that can enter the reference's top-k list on the
+// device and draws on the host (te_hip_sample_top_k_f32).
 #include "te_hip_common.h"
 
 #include <fcntl.h>
@@ -1161,6 +1162,9 @@ struct te_context {
     float *ufw = nullptr;
     void *udws = nullptr;
     size_t udws_bytes = 0;
+    // sampled decoding's candidate workspace, made on first use
+    void *sws = nullptr;
+    size_t sws_bytes = 0;
 };
 
 namespace {
@@ -1174,6 +1178,7 @@ void release_state(te_context *c) {
     c->vt_valid = 0;
     c->ufw = nullptr;
     c->udws = nullptr;
+    c->sws = nullptr;
     c->ready = false;
 }
 
@@ -1580,70 +1585,6 @@ struct Sampler {
             }
         }
     }
-    // xorshift64* to a double in [0, 1) (qwen.c:1170-1178)
-    double uniform() {
-        uint64_t x = rng;
-        x ^= x >> 12;
-        x ^= x << 25;
-        x ^= x >> 27;
-        rng = x;
-        return (double)((x * 0x2545F4914F6CDD1DULL) >> 11) / 9007199254740992.0;
-    }
-    // top-k temperature sampling over the logits, in the reference's candidate
-    // order (the first k, then each larger logit replacing the current minimum,
-    // the first one on a tie), so a given draw picks the same token
-    uint32_t sample(const float *logits, size_t vocab) {
-        size_t k = top_k == 0 ? 1 : std::min<size_t>(top_k, 1024);
-        k = std::min(k, vocab);
-        std::vector<float> v;
-        std::vector<uint32_t> idx;
-        v.reserve(k);
-        idx.reserve(k);
-        size_t min_pos = 0;
-        auto find_min = [&] {
-            min_pos = 0;
-            for (size_t j = 1; j < v.size(); ++j) {
-                if (v[j] < v[min_pos]) {
-                    min_pos = j;
-                }
-            }
-        };
-        for (size_t i = 0; i < vocab; ++i) {
-            if (v.size() < k) {
-                v.push_back(logits[i]);
-                idx.push_back((uint32_t)i);
-                if (v.size() == k) {
-                    find_min();
-                }
-            } else if (logits[i] > v[min_pos]) {
-                v[min_pos] = logits[i];
-                idx[min_pos] = (uint32_t)i;
-                find_min();
-            }
-        }
-        float mx = v[0];
-        for (size_t j = 1; j < v.size(); ++j) {
-            mx = v[j] > mx ? v[j] : mx;
-        }
-        const double t = temperature > 1e-6f ? (double)temperature : 1e-6;
-        std::vector<double> p(v.size());
-        double sum = 0.0;
-        for (size_t j = 0; j < v.size(); ++j) {
-            p[j] = exp(((double)v[j] - (double)mx) / t);
-            sum += p[j];
-        }
-        const double r = uniform() * sum;
-        size_t choice = v.size() - 1;
-        double acc = 0.0;
-        for (size_t j = 0; j < v.size(); ++j) {
-            acc += p[j];
-            if (r <= acc) {
-                choice = j;
-                break;
-            }
-        }
-        return idx[choice];
-    }
 };
 
 // The next token after the hidden state in c->hidden_buf: greedy from the fused
@@ -1660,12 +1601,16 @@ te_status next_token(te_context *c, Sampler &sm, uint32_t &id) {
         if (s != TE_STATUS_OK) {
             return s;
         }
-        std::vector<float> logits(c->vocab);
-        if (hipMemcpy(logits.data(), c->logits, c->vocab * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) {
-            return TE_STATUS_RUNTIME_ERROR;
+        if (c->sws == nullptr) {
+            c->sws_bytes = te_hip_sample_workspace_bytes(c->vocab);
+            unsigned char *p = nullptr;
+            if ((s = dev_alloc(c, &p, c->sws_bytes)) != TE_STATUS_OK) {
+                return s;
+            }
+            c->sws = p;
         }
-        id = sm.sample(logits.data(), c->vocab);
-        return TE_STATUS_OK;
+        return te_hip_sample_top_k_f32(c->logits, c->vocab, sm.top_k, sm.temperature, &sm.rng, &id, c->sws,
+                                       c->sws_bytes, nullptr);
     }
     return hipMemcpy(&id, c->token, sizeof(id), hipMemcpyDeviceToHost) == hipSuccess ? TE_STATUS_OK
                                                                                    : TE_STATUS_RUNTIME_ERROR;

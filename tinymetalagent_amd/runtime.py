@@ -225,6 +225,10 @@ def _configure_library(lib: ctypes.CDLL) -> None:
     _sig(lib, "te_hip_swiglu_f32", [_vp, _vp, _sz, _vp, _vp])
     _sig(lib, "te_hip_add_f32", [_vp, _vp, _sz, _vp, _vp])
     _sig(lib, "te_hip_argmax_f32", [_vp, _sz, _vp, _vp])
+    _sig(lib, "te_hip_sample_workspace_bytes", [_sz], _sz)
+    _sig(lib, "te_hip_sample_top_k_f32", [_vp, _sz, ctypes.c_uint32, ctypes.c_float,
+                                          ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32), _vp,
+                                          _sz, _vp])
     _u64p = ctypes.POINTER(ctypes.c_uint64)
     _sig(lib, "te_hip_gemm_act_bytes", [_sz, _sz], _sz)
     _sig(lib, "te_hip_gemm_q_f32", [_vp, ctypes.c_uint32, _vp, _vp, _vp, ctypes.c_float, _int, _sz, _sz, _sz, _vp,
