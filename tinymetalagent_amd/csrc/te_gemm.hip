@@ -260,11 +260,37 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const unsigned char *__rest
 // split boundaries fall on whole chunks.
 constexpr int kWChunk = 8;
 
+// Weight matrices of one launch (same K and type), whose 64-column tiles are
+// numbered one after another along grid.x: segment i holds tiles
+// tile_end[i-1] .. tile_end[i]-1.  Split-K partial sums are laid out
+// [split][segment][M][n] (n_off: columns before segment i).
+constexpr int kMaxGemmSegs = 3;
+struct GemmSegsArg {
+    const unsigned char *w[kMaxGemmSegs];
+    float *out[kMaxGemmSegs];
+    const float *resid[kMaxGemmSegs];
+    int n[kMaxGemmSegs];
+    int tile_end[kMaxGemmSegs];
+    int n_off[kMaxGemmSegs + 1];
+    int nseg;
+};
+
 template <uint32_t TYPE, bool RESID>
-__global__ __launch_bounds__(256) void gemm_q2_kernel(const unsigned char *__restrict__ w, size_t row_bytes,
+__global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row_bytes,
                                                       const int8_t *__restrict__ hi, const int8_t *__restrict__ lo,
-                                                      const float *__restrict__ scales, int M, int N, int K, int per,
-                                                      float *out, const float *resid, float *part) {
+                                                      const float *__restrict__ scales, int M, int K, int per,
+                                                      float *part) {
+    // this workgroup's segment (uniform)
+    int seg = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGemmSegs; ++i) {
+        seg += (i < sg.nseg && (int)blockIdx.x >= sg.tile_end[i - 1]) ? 1 : 0;
+    }
+    const unsigned char *__restrict__ w = sg.w[seg];
+    const int N = sg.n[seg];
+    float *out = sg.out[seg];
+    const float *resid = sg.resid[seg];
+    const int n_tile = (int)blockIdx.x - (seg > 0 ? sg.tile_end[seg - 1] : 0);
     constexpr int BB = TYPE == kQ4_0 ? 18 : 34;     // bytes per GGUF block
     constexpr int CB = kWChunk * BB;                // bytes of one row's chunk
     constexpr int PITCH = CB + 4;                   // LDS row pitch (CB is a multiple of 16)
@@ -278,7 +304,7 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(const unsigned char *__res
     const int wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 31, kh = lane >> 5;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m_wg = blockIdx.y * 64, n_wg = blockIdx.x * 64;
+    const int m_wg = blockIdx.y * 64, n_wg = n_tile * 64;
     const int m0 = m_wg + wm * 32, n0 = n_wg + wn * 32;
     const int nb = K / 32;
     const int kb0 = blockIdx.z * per, kb1 = min(nb, kb0 + per);
@@ -423,7 +449,7 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(const unsigned char *__res
     }
     const int col = n0 + lr;
     if (col < N) {
-        float *dst = gridDim.z > 1 ? part + (size_t)blockIdx.z * M * N : out;
+        float *dst = gridDim.z > 1 ? part + ((size_t)blockIdx.z * sg.n_off[sg.nseg] + sg.n_off[seg]) * M : out;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = m0 + 8 * (r >> 2) + 4 * kh + (r & 3);
@@ -432,6 +458,26 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(const unsigned char *__res
                 dst[o] = RESID && gridDim.z == 1 ? resid[o] + acc[r] : acc[r];
             }
         }
+    }
+}
+
+// out = (resid +) the splits' partial sums, added in split order, for every
+// segment of a segmented launch (element i of the [segment][M][n] order).
+__global__ __launch_bounds__(256) void gemm_reduce_segs_kernel(const float *__restrict__ part, int splits, int M,
+                                                               GemmSegsArg sg) {
+    const size_t count = (size_t)M * sg.n_off[sg.nseg];
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
+        int seg = 0;
+#pragma unroll
+        for (int t = 1; t < kMaxGemmSegs; ++t) {
+            seg += (t < sg.nseg && i >= (size_t)M * sg.n_off[t]) ? 1 : 0;
+        }
+        float a = part[i];
+        for (int z = 1; z < splits; ++z) {
+            a += part[(size_t)z * count + i];
+        }
+        const size_t j = i - (size_t)M * sg.n_off[seg];
+        sg.out[seg][j] = sg.resid[seg] != nullptr ? sg.resid[seg][j] + a : a;
     }
 }
 
@@ -481,18 +527,45 @@ te_status launch_quant_act(int pre, const float *x, const float *x2, const float
     return launch_status();
 }
 
-te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n, size_t k,
-                        float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream) {
-    if ((ggml_type != kQ4_0 && ggml_type != kQ8_0) || k % 32 != 0 || rows == 0 || n == 0 ||
-        rows > 0x7fffffffu || n > 0x7fffffffu || k > (1u << 24) || ((size_t)weights & 1u) != 0) {
+te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, const void *act, size_t rows,
+                             size_t k, float *partials, size_t partial_bytes, hipStream_t stream) {
+    if ((ggml_type != kQ4_0 && ggml_type != kQ8_0) || k % 32 != 0 || rows == 0 || rows > 0x7fffffffu ||
+        k > (1u << 24) || nseg < 1 || nseg > kMaxGemmSegs) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    const size_t row_bytes = k / 32 * (ggml_type == kQ4_0 ? 18 : 34);
+    // the LDS-staged kernel where a row's chunks are 16-byte aligned (its
+    // split boundaries fall on whole chunks), else one gemm_q_kernel launch
+    // per matrix
+    bool staged = row_bytes % 16 == 0 && getenv("TE_HIP_GEMM_V1") == nullptr;
+    size_t n_total = 0, tiles_n = 0;
+    for (int i = 0; i < nseg; ++i) {
+        if (segs[i].n == 0 || segs[i].n > 0x7fffffffu || ((size_t)segs[i].w & 1u) != 0 ||
+            (segs[i].resid != nullptr) != (segs[0].resid != nullptr)) {
+            return TE_STATUS_UNSUPPORTED;
+        }
+        staged = staged && ((size_t)segs[i].w & 15u) == 0;
+        n_total += segs[i].n;
+        tiles_n += (segs[i].n + 63) / 64;
+    }
+    if (n_total > 0x7fffffffu) {
         return TE_STATUS_UNSUPPORTED;
     }
     const size_t planes = plane_bytes(rows, k);
     const int8_t *hi = static_cast<const int8_t *>(act);
     const int8_t *lo = hi + planes;
     const float *scales = reinterpret_cast<const float *>(lo + planes);
-    const size_t row_bytes = k / 32 * (ggml_type == kQ4_0 ? 18 : 34);
-    const size_t tiles = (n + 63) / 64 * ((rows + 63) / 64);
+    if (!staged && nseg > 1) {
+        for (int i = 0; i < nseg; ++i) {
+            const te_status st = launch_gemm_q_segs(ggml_type, &segs[i], 1, act, rows, k, partials, partial_bytes,
+                                                    stream);
+            if (st != TE_STATUS_OK) {
+                return st;
+            }
+        }
+        return TE_STATUS_OK;
+    }
+    const size_t tiles = tiles_n * ((rows + 63) / 64);
     const size_t nb = k / 32;
     // split K until the grid covers four workgroups per CU (measured: down at 512 rows 175 -> 159 us
     // against two; eight gains nothing more), keeping >= 8 blocks per split
@@ -504,37 +577,50 @@ te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act
     }
     const size_t want = per_cu * (size_t)device_compute_units();
     while (partials != nullptr && tiles * splits < want && nb / (splits * 2) >= 8 &&
-           splits * 2 * rows * n * sizeof(float) <= partial_bytes) {
+           splits * 2 * rows * n_total * sizeof(float) <= partial_bytes) {
         splits *= 2;
     }
-    // the LDS-staged kernel where a row's chunks are 16-byte aligned; its
-    // split boundaries fall on whole chunks
-    const bool staged = ((size_t)weights & 15u) == 0 && row_bytes % 16 == 0 && getenv("TE_HIP_GEMM_V1") == nullptr;
     int per = (int)((nb + splits - 1) / splits);
     if (staged) {
         per = (per + kWChunk - 1) / kWChunk * kWChunk;
         splits = (nb + (size_t)per - 1) / (size_t)per;
     }
-    const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)splits);
-    const unsigned char *w = static_cast<const unsigned char *>(weights);
+    const dim3 grid((unsigned)tiles_n, (unsigned)((rows + 63) / 64), (unsigned)splits);
+    const bool resid = segs[0].resid != nullptr;
+    GemmSegsArg sg = {};
+    sg.nseg = nseg;
+    int tile_end = 0;
+    for (int i = 0; i < nseg; ++i) {
+        sg.w[i] = static_cast<const unsigned char *>(segs[i].w);
+        sg.out[i] = segs[i].out;
+        sg.resid[i] = segs[i].resid;
+        sg.n[i] = (int)segs[i].n;
+        tile_end += (int)((segs[i].n + 63) / 64);
+        sg.tile_end[i] = tile_end;
+        sg.n_off[i + 1] = sg.n_off[i] + (int)segs[i].n;
+    }
+    const unsigned char *w = sg.w[0];
+    const size_t n = segs[0].n;
+    float *out = segs[0].out;
+    const float *res = segs[0].resid;
 #define TE_GEMM(T, R)                                                                                              \
     do {                                                                                                           \
         if (staged) {                                                                                              \
-            gemm_q2_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n,       \
-                                                           (int)k, per, out, resid, partials);                     \
+            gemm_q2_kernel<T, R><<<grid, 256, 0, stream>>>(sg, row_bytes, hi, lo, scales, (int)rows, (int)k, per,  \
+                                                           partials);                                              \
         } else {                                                                                                   \
             gemm_q_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n, (int)k, \
-                                                          per, out, resid, partials);                              \
+                                                          per, out, res, partials);                                \
         }                                                                                                          \
     } while (0)
     if (ggml_type == kQ4_0) {
-        if (resid != nullptr) {
+        if (resid) {
             TE_GEMM(kQ4_0, true);
         } else {
             TE_GEMM(kQ4_0, false);
         }
     } else {
-        if (resid != nullptr) {
+        if (resid) {
             TE_GEMM(kQ8_0, true);
         } else {
             TE_GEMM(kQ8_0, false);
@@ -542,11 +628,21 @@ te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act
     }
 #undef TE_GEMM
     if (splits > 1) {
-        const size_t count = rows * n;
+        const size_t count = rows * n_total;
         const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
-        gemm_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, count, resid, out);
+        if (nseg == 1) {
+            gemm_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, count, res, out);
+        } else {
+            gemm_reduce_segs_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, (int)rows, sg);
+        }
     }
     return launch_status();
+}
+
+te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n, size_t k,
+                        float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream) {
+    const GemmSeg seg = {weights, out, resid, n};
+    return launch_gemm_q_segs(ggml_type, &seg, 1, act, rows, k, partials, partial_bytes, stream);
 }
 
 }  // namespace te_hip

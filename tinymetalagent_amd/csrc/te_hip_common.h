@@ -127,6 +127,19 @@ te_status launch_quant_act(int pre, const float *x, const float *x2, const float
 // `partials` (partial_bytes, may be NULL) lets small output grids split K.
 te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n, size_t k,
                         float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream);
+// Up to three weight matrices of the same K against the same activations in
+// one launch (their column tiles numbered one after another, one split-K
+// reduction for all): segs[i].out[m][r] = sum_k act[m][k] W_i[r][k]
+// (+ segs[i].resid[m][r]), r < segs[i].n.  Either every segment has a
+// residual or none.  partial_bytes bounds the splits by rows * sum(n).
+struct GemmSeg {
+    const void *w;
+    float *out;
+    const float *resid;
+    size_t n;
+};
+te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, const void *act, size_t rows,
+                             size_t k, float *partials, size_t partial_bytes, hipStream_t stream);
 
 // One weight matrix of a fused GEMV launch: out[r] = W[r] . x' (+ resid[r] when
 // resid is set; resid may equal out), r < rows.

@@ -12,8 +12,8 @@
 //   x += (silu(norm Wg^T) * (norm Wu^T)) Wd^T                     (te_swiglu_f32)
 //
 // Launches per layer (one stream, no host synchronisation): the GEMM's
-// activation digits with RMSNorm folded in, then the Q, K and V GEMMs
-// (te_gemm.hip); the fused prefill step keeping V^T (bias + RoPE + fp16
+// activation digits with RMSNorm folded in, then the Q, K and V GEMMs as one
+// segmented launch (te_gemm.hip); the fused prefill step keeping V^T (bias + RoPE + fp16
 // append into the K / V caches and V^T, then the MFMA causal attention,
 // te_prefill.hip); the digits of the attention output and the Wo GEMM with
 // the residual in its epilogue; RMSNorm digits, gate and up GEMMs; SwiGLU
@@ -147,11 +147,20 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
                                          st);
         };
         const te_hip::ProfPhase ew = te_hip::kProfElementwise;
+        // Q, K and V in one launch (one split-K reduction), profiled by rows
+        const te_hip::GemmSeg qkv[3] = {{m + q_offsets[l], b.q, nullptr, hidden},
+                                        {m + k_offsets[l], b.k, nullptr, kv},
+                                        {m + v_offsets[l], b.v, nullptr, kv}};
+        auto qkv_done = [&](te_status r) {
+            const te_hip::ProfShare share[3] = {
+                {te_hip::kProfQ, (double)hidden}, {te_hip::kProfK, (double)kv}, {te_hip::kProfV, (double)kv}};
+            te_hip::prof_mark(st, share, 3);
+            return r == TE_STATUS_OK;
+        };
         if (!done(s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights + l * hidden, epsilon, batch,
                                                hidden, b.act, st), ew) ||
-            !done(s = gemm(q_offsets, hidden, hidden, b.q, nullptr), te_hip::kProfQ) ||
-            !done(s = gemm(k_offsets, kv, hidden, b.k, nullptr), te_hip::kProfK) ||
-            !done(s = gemm(v_offsets, kv, hidden, b.v, nullptr), te_hip::kProfV) ||
+            !qkv_done(s = te_hip::launch_gemm_q_segs(ggml_type, qkv, 3, b.act, batch, hidden, b.part, b.part_bytes,
+                                                     st)) ||
             !done(s = te_hip_attention_prefill_step_vt_f16(
                       b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
                       key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
