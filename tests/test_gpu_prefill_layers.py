@@ -96,6 +96,7 @@ def _run(oracle_mod, ggml_type, layers, heads, kv_heads, head_dim, ffn, ctx, bas
     n = base + batch
     vt_want = vc16.permute(0, 1, 3, 4, 2)[..., :n]
     assert torch.equal(vt[..., :n].view(torch.int16), vt_want.contiguous().view(torch.int16))
+    return got
 
 
 @pytest.mark.parametrize("ggml_type", [2, 8])
@@ -106,6 +107,44 @@ def test_prefill_all_layers_vs_oracle(oracle_mod, ggml_type):
 def test_prefill_all_layers_after_cached_prefix_head_dim_128(oracle_mod):
     """A chunk at base 37 after a cached prefix, head_dim 128, 7:1 grouping."""
     _run(oracle_mod, 2, layers=2, heads=14, kv_heads=2, head_dim=128, ffn=1024, ctx=80, base=37, batch=21)
+
+
+@pytest.mark.parametrize("ggml_type", [2, 8])
+def test_prefill_paired_gate_up_gemm(oracle_mod, ggml_type, monkeypatch):
+    """Gate and up as one GEMM launch whose epilogue writes the SwiGLU digits
+    (TE_HIP_GEMM_GLU=1 takes it at this small grid; the library takes it by
+    itself once the grid covers the GPU): the oracle's bar."""
+    monkeypatch.setenv("TE_HIP_GEMM_GLU", "1")
+    _run(oracle_mod, ggml_type, layers=2, heads=14, kv_heads=2, head_dim=128, ffn=1024, ctx=80, base=5, batch=70)
+
+
+@pytest.mark.parametrize("ggml_type", [2, 8])
+def test_prefill_paired_gate_up_gemm_bits(ggml_type, monkeypatch):
+    """At a chunk whose two-GEMM path splits no K range (512 rows, ffn 8192:
+    1024 output tiles), the paired launch gives the same output bits as the
+    two GEMMs plus the SwiGLU digits kernel: the same products, summed in the
+    same order, and the same digits."""
+    layers, heads, kv_heads, head_dim, ffn, batch, base = 1, 4, 2, 64, 8192, 512, 3
+    ctx = base + batch
+    m = S.synthetic_model(93, ggml_type, layers, heads, kv_heads, head_dim, ffn, 64, ctx, base)
+    hidden = m["hidden"]
+    cos, sin = A.rope_table(ctx, head_dim, 1.0e6)
+    x_in = _dev(S.normal(93, "rows", (batch, hidden)))
+    outs = []
+    for mode in ("1", "0"):
+        monkeypatch.setenv("TE_HIP_GEMM_GLU", mode)
+        kc, vc = _dev(m["key_cache"]), _dev(m["value_cache"])
+        vt = A.value_t_buffer(1, layers, ctx, kv_heads, head_dim)
+        A.value_transpose(vc.view(torch.float16).reshape(1, layers, ctx, kv_heads, head_dim), vt,
+                          first_position=0, count=base)
+        got = LY.prefill_all_layers(_dev(m["mapping"]), m["offsets"], layers, ggml_type, x_in.clone(),
+                                    _dev(m["attn_norm"]), _dev(m["ffn_norm"]), _dev(m["q_bias"]), _dev(m["k_bias"]),
+                                    _dev(m["v_bias"]), cos.contiguous(), sin.contiguous(), kc, vc, vt, base, ctx,
+                                    heads, kv_heads, head_dim, ffn, 1e-6)
+        torch.cuda.synchronize()
+        outs.append(got.cpu().numpy())
+    print(f"type {ggml_type}: paired vs two GEMMs max |diff| {np.abs(outs[0] - outs[1]).max():.3g}")
+    assert np.isfinite(outs[0]).all() and np.array_equal(outs[0], outs[1])
 
 
 def test_prefill_layer_by_layer(oracle_mod):

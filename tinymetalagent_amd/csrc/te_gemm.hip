@@ -275,11 +275,25 @@ struct GemmSegsArg {
     int nseg;
 };
 
-template <uint32_t TYPE, bool RESID>
+// GLU form's output: the SwiGLU of the paired gate / up products as the next
+// GEMM's activation digits (quant_act_kernel's planes and scales, K = n).
+struct GluDigits {
+    int8_t *hi;
+    int8_t *lo;
+    float *scales;
+};
+
+// GLU = true: sg.w[0] / sg.w[1] are the gate / up matrices (n rows each) and
+// a workgroup's 64 weight rows pair the same 32 rows of both (wave wn = 0 the
+// gate products, wn = 1 the up products of the same 32 columns); the epilogue
+// forms silu(gate) * up with te_swiglu_f32's operations and writes its digits
+// (one 32-value block per row and workgroup), exactly as quant_act_kernel
+// would from the two products.  One K split.
+template <uint32_t TYPE, bool RESID, bool GLU>
 __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row_bytes,
                                                       const int8_t *__restrict__ hi, const int8_t *__restrict__ lo,
                                                       const float *__restrict__ scales, int M, int K, int per,
-                                                      float *part) {
+                                                      float *part, GluDigits glu) {
     // this workgroup's segment (uniform)
     int seg = 0;
 #pragma unroll
@@ -304,8 +318,8 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
     const int wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 31, kh = lane >> 5;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m_wg = blockIdx.y * 64, n_wg = n_tile * 64;
-    const int m0 = m_wg + wm * 32, n0 = n_wg + wn * 32;
+    const int m_wg = blockIdx.y * 64, n_wg = n_tile * (GLU ? 32 : 64);
+    const int m0 = m_wg + wm * 32, n0 = GLU ? n_wg : n_wg + wn * 32;
     const int nb = K / 32;
     const int kb0 = blockIdx.z * per, kb1 = min(nb, kb0 + per);
     const size_t a_tile = (size_t)(min(m0, (M - 1) & ~31) >> 5) * nb;
@@ -333,8 +347,10 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
             const size_t off = cbyte + 16 * (size_t)j;
             wreg[i] = make_uint4(0u, 0u, 0u, 0u);
             if (item < PIECES && off < row_bytes) {  // a piece is wholly in its row or wholly past it
-                const int row = min(n_wg + r, N - 1);
-                wreg[i] = *reinterpret_cast<const uint4 *>(w + (size_t)row * row_bytes + off);
+                // GLU: rows 0..31 of the tile from the gate matrix, 32..63 from up
+                const unsigned char *wm_base = GLU ? sg.w[r >> 5] : w;
+                const int row = min(n_wg + (GLU ? (r & 31) : r), N - 1);
+                wreg[i] = *reinterpret_cast<const uint4 *>(wm_base + (size_t)row * row_bytes + off);
             }
         }
     };
@@ -448,6 +464,58 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
         __syncthreads();
     }
     const int col = n0 + lr;
+    if constexpr (GLU) {
+        // up products -> LDS (the weight stages are free after the last
+        // barrier); the gate wave forms h and its digits
+        float *xch = reinterpret_cast<float *>(&w_lds[0][0]);
+        static_assert(sizeof(w_lds) >= 2 * 16 * 64 * sizeof(float), "exchange fits the weight stages");
+        if (wn == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                xch[(wm * 16 + r) * 64 + lane] = acc[r];
+            }
+        }
+        __syncthreads();
+        if (wn == 0) {
+            const int b = n_wg >> 5;
+            const int nbo = N >> 5;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+                const float g = acc[r];
+                const float u = xch[(wm * 16 + r) * 64 + lane];
+                const float v = g / (1.0f + expf(-g)) * u;  // te_swiglu_f32 (ops.c:397-405)
+                float mx = fabsf(v);
+#pragma unroll
+                for (int off = 16; off > 0; off >>= 1) {
+                    mx = fmaxf(mx, __shfl_xor(mx, off, 32));
+                }
+                int q = 0;
+                float sc;
+                if (!(mx <= FLT_MAX)) {
+                    sc = __builtin_nanf("");
+                } else if (mx == 0.0f) {
+                    sc = 0.0f;
+                } else {
+                    int E;
+                    (void)frexpf(mx, &E);
+                    const int e = min(14 - E, 126);
+                    q = (int)rintf(ldexpf(v, e));
+                    sc = ldexpf(1.0f, -e);
+                }
+                if (row < M) {
+                    const int l8 = ((q + 128) & 255) - 128;
+                    const size_t t = (((size_t)(row >> 5) * nbo + b) << 10) + ((row & 31) << 5) + lr;
+                    glu.hi[t] = (int8_t)((q - l8) >> 8);
+                    glu.lo[t] = (int8_t)l8;
+                    if (lr == 0) {
+                        glu.scales[(size_t)row * nbo + b] = sc;
+                    }
+                }
+            }
+        }
+        return;
+    }
     if (col < N) {
         float *dst = gridDim.z > 1 ? part + ((size_t)blockIdx.z * sg.n_off[sg.nseg] + sg.n_off[seg]) * M : out;
 #pragma unroll
@@ -606,8 +674,8 @@ te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, 
 #define TE_GEMM(T, R)                                                                                              \
     do {                                                                                                           \
         if (staged) {                                                                                              \
-            gemm_q2_kernel<T, R><<<grid, 256, 0, stream>>>(sg, row_bytes, hi, lo, scales, (int)rows, (int)k, per,  \
-                                                           partials);                                              \
+            gemm_q2_kernel<T, R, false><<<grid, 256, 0, stream>>>(sg, row_bytes, hi, lo, scales, (int)rows,       \
+                                                                  (int)k, per, partials, GluDigits{});             \
         } else {                                                                                                   \
             gemm_q_kernel<T, R><<<grid, 256, 0, stream>>>(w, row_bytes, hi, lo, scales, (int)rows, (int)n, (int)k, \
                                                           per, out, res, partials);                                \
@@ -643,6 +711,48 @@ te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act
                         float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream) {
     const GemmSeg seg = {weights, out, resid, n};
     return launch_gemm_q_segs(ggml_type, &seg, 1, act, rows, k, partials, partial_bytes, stream);
+}
+
+te_status launch_gemm_glu_q(uint32_t ggml_type, const void *gate_w, const void *up_w, const void *act, size_t rows,
+                            size_t n, size_t k, void *act_out, hipStream_t stream, bool *launched) {
+    *launched = false;
+    const size_t row_bytes = k / 32 * (ggml_type == kQ4_0 ? 18 : 34);
+    const size_t tiles = n / 32 * ((rows + 63) / 64);
+    const char *env = getenv("TE_HIP_GEMM_GLU");
+    if ((ggml_type != kQ4_0 && ggml_type != kQ8_0) || k % 32 != 0 || n % 32 != 0 || rows == 0 ||
+        rows > 0x7fffffffu || n > 0x7fffffffu || k > (1u << 24) || row_bytes % 16 != 0 ||
+        ((size_t)gate_w & 15u) != 0 || ((size_t)up_w & 15u) != 0 || getenv("TE_HIP_GEMM_V1") != nullptr ||
+        (env != nullptr && env[0] == '0') ||
+        (tiles < (size_t)device_compute_units() && !(env != nullptr && env[0] == '1'))) {
+        return TE_STATUS_OK;  // not launched: the caller runs the two GEMMs and the SwiGLU digits
+    }
+    const size_t planes = plane_bytes(rows, k);
+    const int8_t *hi = static_cast<const int8_t *>(act);
+    const int8_t *lo = hi + planes;
+    const float *scales = reinterpret_cast<const float *>(lo + planes);
+    const size_t out_planes = plane_bytes(rows, n);
+    GluDigits d;
+    d.hi = static_cast<int8_t *>(act_out);
+    d.lo = d.hi + out_planes;
+    d.scales = reinterpret_cast<float *>(d.lo + out_planes);
+    GemmSegsArg sg = {};
+    sg.nseg = 1;
+    sg.w[0] = static_cast<const unsigned char *>(gate_w);
+    sg.w[1] = static_cast<const unsigned char *>(up_w);
+    sg.n[0] = (int)n;
+    sg.tile_end[0] = (int)(n / 32);
+    sg.n_off[1] = (int)n;
+    const dim3 grid((unsigned)(n / 32), (unsigned)((rows + 63) / 64), 1);
+    const int per = (int)(k / 32);
+    if (ggml_type == kQ4_0) {
+        gemm_q2_kernel<kQ4_0, false, true><<<grid, 256, 0, stream>>>(sg, row_bytes, hi, lo, scales, (int)rows, (int)k,
+                                                                     per, nullptr, d);
+    } else {
+        gemm_q2_kernel<kQ8_0, false, true><<<grid, 256, 0, stream>>>(sg, row_bytes, hi, lo, scales, (int)rows, (int)k,
+                                                                     per, nullptr, d);
+    }
+    *launched = true;
+    return launch_status();
 }
 
 }  // namespace te_hip

@@ -140,6 +140,16 @@ struct GemmSeg {
 };
 te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, const void *act, size_t rows,
                              size_t k, float *partials, size_t partial_bytes, hipStream_t stream);
+// Gate and up [n][k] against the same activation digits in one launch whose
+// tiles pair the same rows of both, writing silu(gate) * up as the down
+// projection's digits into act_out (act_buffer_bytes(rows, n) bytes, the same
+// digits launch_quant_act(2, gate, up) gives).  *launched = false (and
+// nothing queued) where the shapes or alignment do not allow it, n % 32 != 0,
+// or the grid would not cover the GPU: the caller then runs the two GEMMs and
+// launch_quant_act.  TE_HIP_GEMM_GLU=0 turns it off, =1 takes it for grids of
+// any size.
+te_status launch_gemm_glu_q(uint32_t ggml_type, const void *gate_w, const void *up_w, const void *act, size_t rows,
+                            size_t n, size_t k, void *act_out, hipStream_t stream, bool *launched);
 
 // One weight matrix of a fused GEMV launch: out[r] = W[r] . x' (+ resid[r] when
 // resid is set; resid may equal out), r < rows.

@@ -16,8 +16,9 @@
 // segmented launch (te_gemm.hip); the fused prefill step keeping V^T (bias + RoPE + fp16
 // append into the K / V caches and V^T, then the MFMA causal attention,
 // te_prefill.hip); the digits of the attention output and the Wo GEMM with
-// the residual in its epilogue; RMSNorm digits, gate and up GEMMs; SwiGLU
-// digits and the down GEMM with the residual.
+// the residual in its epilogue; RMSNorm digits; gate and up as one launch
+// whose epilogue writes the SwiGLU digits (else two GEMMs and the SwiGLU
+// digits); the down GEMM with the residual.
 //
 // Differences from the Metal slot, all device-resident: the K / V caches are
 // the HIP path's fp16 caches [layers][context_tokens][kv] plus the transposed
@@ -37,13 +38,13 @@ size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
 struct ChunkBuffers {
     float *q, *k, *v, *attn, *gate, *up, *part;
-    void *act;
+    void *act, *act_ffn;  // digits of the hidden-wide inputs; of the SwiGLU output (down's input)
     size_t part_bytes;
 };
 
 // Byte layout of the workspace, in carve-up order: the GEMM outputs, the
 // split-K partial sums (up to 8 splits of a hidden-wide output), the
-// activation digits.
+// activation digits of the hidden-wide GEMM inputs, then of down's input.
 size_t carve(size_t batch, size_t hidden, size_t kv, size_t ffn, unsigned char *base, ChunkBuffers *b) {
     const size_t floats[7] = {batch * hidden, batch * kv, batch * kv, batch * hidden, batch * ffn, batch * ffn,
                               8 * batch * hidden};
@@ -55,11 +56,13 @@ size_t carve(size_t batch, size_t hidden, size_t kv, size_t ffn, unsigned char *
         }
         off += align_up(floats[i] * sizeof(float));
     }
+    const size_t act_hidden = align_up(te_hip::act_buffer_bytes(batch, hidden));
     if (base != nullptr) {
         b->act = base + off;
+        b->act_ffn = base + off + act_hidden;
         b->part_bytes = floats[6] * sizeof(float);
     }
-    return off + align_up(te_hip::act_buffer_bytes(batch, std::max(hidden, ffn)));
+    return off + act_hidden + align_up(te_hip::act_buffer_bytes(batch, ffn));
 }
 
 bool tensor_fits(uint64_t offset, size_t rows, size_t row_bytes, size_t mapping_len) {
@@ -151,6 +154,16 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
         const te_hip::GemmSeg qkv[3] = {{m + q_offsets[l], b.q, nullptr, hidden},
                                         {m + k_offsets[l], b.k, nullptr, kv},
                                         {m + v_offsets[l], b.v, nullptr, kv}};
+        // gate and up with the SwiGLU digits in their epilogue where the
+        // shapes allow it, else both GEMMs and the SwiGLU digits
+        bool glu = false;
+        auto glu_done = [&](te_status r) {
+            if (glu) {
+                const te_hip::ProfShare share[2] = {{te_hip::kProfGate, 1.0}, {te_hip::kProfUp, 1.0}};
+                te_hip::prof_mark(st, share, 2);
+            }
+            return r == TE_STATUS_OK;
+        };
         auto qkv_done = [&](te_status r) {
             const te_hip::ProfShare share[3] = {
                 {te_hip::kProfQ, (double)hidden}, {te_hip::kProfK, (double)kv}, {te_hip::kProfV, (double)kv}};
@@ -170,10 +183,19 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
             !done(s = gemm(output_offsets, hidden, hidden, out, out), te_hip::kProfO) ||
             !done(s = te_hip::launch_quant_act(1, out, nullptr, ffn_norm_weights + l * hidden, epsilon, batch,
                                                hidden, b.act, st), ew) ||
-            !done(s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr), te_hip::kProfGate) ||
-            !done(s = gemm(up_offsets, ffn, hidden, b.up, nullptr), te_hip::kProfUp) ||
-            !done(s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act, st), ew) ||
-            !done(s = gemm(down_offsets, hidden, ffn, out, out), te_hip::kProfDown)) {
+            !glu_done(s = te_hip::launch_gemm_glu_q(ggml_type, m + gate_offsets[l], m + up_offsets[l], b.act, batch,
+                                                    ffn, hidden, b.act_ffn, st, &glu))) {
+            break;
+        }
+        if (!glu && (!done(s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr), te_hip::kProfGate) ||
+                     !done(s = gemm(up_offsets, ffn, hidden, b.up, nullptr), te_hip::kProfUp) ||
+                     !done(s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act_ffn, st),
+                           ew))) {
+            break;
+        }
+        if (!done(s = te_hip::launch_gemm_q(m + down_offsets[l], ggml_type, b.act_ffn, batch, hidden, ffn, out, out,
+                                            b.part, b.part_bytes, st),
+                  te_hip::kProfDown)) {
             break;
         }
     }
