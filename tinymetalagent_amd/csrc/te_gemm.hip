@@ -50,8 +50,42 @@ __device__ __forceinline__ float half_bits(uint32_t bits) {
 
 enum ActPre { kActPlain = 0, kActRmsNorm = 1, kActSwiGLU = 2 };
 
+// One 32-value block of digits: lane j of a half wave holds value j (every
+// lane of the half takes part; only `store` lanes write).
+__device__ __forceinline__ void quant_block(float v, size_t row, int K, int b, int lane, int8_t *__restrict__ hi,
+                                            int8_t *__restrict__ lo, float *__restrict__ scales, bool store = true) {
+    float m = fabsf(v);
+    for (int off = 16; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off, 32));
+    }
+    int q = 0;
+    float s;
+    if (!(m <= FLT_MAX)) {  // inf or NaN in the block: its products are NaN
+        s = __builtin_nanf("");
+    } else if (m == 0.0f) {
+        s = 0.0f;
+    } else {
+        int E;
+        (void)frexpf(m, &E);
+        const int e = min(14 - E, 126);  // blocks below 2^-112 round towards 0
+        q = (int)rintf(ldexpf(v, e));
+        s = ldexpf(1.0f, -e);
+    }
+    if (store) {
+        const int l8 = ((q + 128) & 255) - 128;
+        const size_t t = (((row >> 5) * (size_t)(K >> 5) + b) << 10) + ((row & 31) << 5) + lane;
+        hi[t] = (int8_t)((q - l8) >> 8);
+        lo[t] = (int8_t)l8;
+        if (lane == 0) {
+            scales[row * (size_t)(K / 32) + b] = s;
+        }
+    }
+}
+
 // One workgroup per row: x' = pre(x), then digits and block scales.
 // planes: hi and lo, int8 in 32 x 32 tiles [M/32][K/32][32][32]; scales [M][K/32] fp32.
+// The kernel is bound by load latency, not bandwidth: loads are issued
+// together ahead of their use.
 template <int PRE>
 __global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__restrict__ x,
                                                                 const float *__restrict__ x2,
@@ -63,12 +97,26 @@ __global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__r
     const float *xr = x + row * (size_t)K;
     float rms = 1.0f;
     if (PRE == kActRmsNorm) {
-        // te_rmsnorm_f32 (ops.c:272-293): fp64 sum of squares, 1 / sqrtf(mean + eps)
+        // te_rmsnorm_f32 (ops.c:272-293): fp64 sum of squares, 1 / sqrtf(mean + eps);
+        // each thread sums its values in index order, eight loads in flight
         __shared__ double part[kActThreads / 64];
         double ss = 0.0;
-        for (int i = threadIdx.x; i < K; i += kActThreads) {
-            const double v = (double)xr[i];
-            ss += v * v;
+        int i = threadIdx.x;
+        for (; i + 7 * kActThreads < K; i += 8 * kActThreads) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                v[u] = xr[i + u * kActThreads];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const double d = (double)v[u];
+                ss += d * d;
+            }
+        }
+        for (; i < K; i += kActThreads) {
+            const double d = (double)xr[i];
+            ss += d * d;
         }
         for (int off = 32; off > 0; off >>= 1) {
             ss += __shfl_xor(ss, off);
@@ -84,41 +132,40 @@ __global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__r
         rms = 1.0f / sqrtf((float)(t / (double)K) + eps);
     }
     // one 32-value block per half wave: lane j of the half takes value j;
-    // workgroup blockIdx.y of gridDim.y takes every gridDim.y-th group of blocks
+    // workgroup blockIdx.y of gridDim.y takes every gridDim.y-th group of
+    // blocks, four blocks' loads at a time
     const int lane = threadIdx.x & 31;
     const int halves = kActThreads / 32 * gridDim.y;
-    for (int b = (threadIdx.x >> 5) + blockIdx.y * (kActThreads / 32); b < K / 32; b += halves) {
-        const int i = b * 32 + lane;
-        float v = xr[i];
-        if (PRE == kActRmsNorm) {
-            v = v * rms * norm_w[i];
-        } else if (PRE == kActSwiGLU) {
-            const float u = x2[row * (size_t)K + i];
-            v = v / (1.0f + expf(-v)) * u;  // te_swiglu_f32 (ops.c:397-405)
+    const int nblk = K / 32;
+    for (int b = (threadIdx.x >> 5) + blockIdx.y * (kActThreads / 32); b < nblk; b += 4 * halves) {
+        float v[4], w2[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int bb = b + u * halves;
+            v[u] = 0.0f;
+            w2[u] = 0.0f;
+            if (bb < nblk) {  // uniform per half wave
+                const int i = bb * 32 + lane;
+                v[u] = xr[i];
+                if (PRE == kActRmsNorm) {
+                    w2[u] = norm_w[i];
+                } else if (PRE == kActSwiGLU) {
+                    w2[u] = x2[row * (size_t)K + i];
+                }
+            }
         }
-        float m = fabsf(v);
-        for (int off = 16; off > 0; off >>= 1) {
-            m = fmaxf(m, __shfl_xor(m, off, 32));
-        }
-        int q = 0;
-        float s;
-        if (!(m <= FLT_MAX)) {  // inf or NaN in the block: its products are NaN
-            s = __builtin_nanf("");
-        } else if (m == 0.0f) {
-            s = 0.0f;
-        } else {
-            int E;
-            (void)frexpf(m, &E);
-            const int e = min(14 - E, 126);  // blocks below 2^-112 round towards 0
-            q = (int)rintf(ldexpf(v, e));
-            s = ldexpf(1.0f, -e);
-        }
-        const int l8 = ((q + 128) & 255) - 128;
-        const size_t t = (((row >> 5) * (size_t)(K >> 5) + b) << 10) + ((row & 31) << 5) + lane;
-        hi[t] = (int8_t)((q - l8) >> 8);
-        lo[t] = (int8_t)l8;
-        if (lane == 0) {
-            scales[row * (size_t)(K / 32) + b] = s;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int bb = b + u * halves;
+            if (bb < nblk) {
+                float y = v[u];
+                if (PRE == kActRmsNorm) {
+                    y = y * rms * w2[u];
+                } else if (PRE == kActSwiGLU) {
+                    y = y / (1.0f + expf(-y)) * w2[u];  // te_swiglu_f32 (ops.c:397-405)
+                }
+                quant_block(y, row, K, bb, lane, hi, lo, scales);
+            }
         }
     }
 }
@@ -305,6 +352,7 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
     float *out = sg.out[seg];
     const float *resid = sg.resid[seg];
     const int n_tile = (int)blockIdx.x - (seg > 0 ? sg.tile_end[seg - 1] : 0);
+    const uintptr_t up_delta = GLU ? (uintptr_t)sg.w[1] - (uintptr_t)sg.w[0] : 0;  // modulo 2^64
     constexpr int BB = TYPE == kQ4_0 ? 18 : 34;     // bytes per GGUF block
     constexpr int CB = kWChunk * BB;                // bytes of one row's chunk
     constexpr int PITCH = CB + 4;                   // LDS row pitch (CB is a multiple of 16)
@@ -347,10 +395,12 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
             const size_t off = cbyte + 16 * (size_t)j;
             wreg[i] = make_uint4(0u, 0u, 0u, 0u);
             if (item < PIECES && off < row_bytes) {  // a piece is wholly in its row or wholly past it
-                // GLU: rows 0..31 of the tile from the gate matrix, 32..63 from up
-                const unsigned char *wm_base = GLU ? sg.w[r >> 5] : w;
+                // GLU: rows 0..31 of the tile from the gate matrix, 32..63 from
+                // up (a byte offset from gate: a per-piece pointer select
+                // costs registers that lower occupancy)
                 const int row = min(n_wg + (GLU ? (r & 31) : r), N - 1);
-                wreg[i] = *reinterpret_cast<const uint4 *>(wm_base + (size_t)row * row_bytes + off);
+                const uintptr_t base = (uintptr_t)w + (GLU ? (uintptr_t)(r >> 5) * up_delta : 0);
+                wreg[i] = *reinterpret_cast<const uint4 *>(base + (size_t)row * row_bytes + off);
             }
         }
     };
@@ -478,40 +528,13 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
         __syncthreads();
         if (wn == 0) {
             const int b = n_wg >> 5;
-            const int nbo = N >> 5;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + 8 * (r >> 2) + 4 * kh + (r & 3);
                 const float g = acc[r];
                 const float u = xch[(wm * 16 + r) * 64 + lane];
                 const float v = g / (1.0f + expf(-g)) * u;  // te_swiglu_f32 (ops.c:397-405)
-                float mx = fabsf(v);
-#pragma unroll
-                for (int off = 16; off > 0; off >>= 1) {
-                    mx = fmaxf(mx, __shfl_xor(mx, off, 32));
-                }
-                int q = 0;
-                float sc;
-                if (!(mx <= FLT_MAX)) {
-                    sc = __builtin_nanf("");
-                } else if (mx == 0.0f) {
-                    sc = 0.0f;
-                } else {
-                    int E;
-                    (void)frexpf(mx, &E);
-                    const int e = min(14 - E, 126);
-                    q = (int)rintf(ldexpf(v, e));
-                    sc = ldexpf(1.0f, -e);
-                }
-                if (row < M) {
-                    const int l8 = ((q + 128) & 255) - 128;
-                    const size_t t = (((size_t)(row >> 5) * nbo + b) << 10) + ((row & 31) << 5) + lr;
-                    glu.hi[t] = (int8_t)((q - l8) >> 8);
-                    glu.lo[t] = (int8_t)l8;
-                    if (lr == 0) {
-                        glu.scales[(size_t)row * nbo + b] = sc;
-                    }
-                }
+                quant_block(v, (size_t)row, N, b, lr, glu.hi, glu.lo, glu.scales, row < M);
             }
         }
         return;
