@@ -123,16 +123,19 @@ def test_prefill_paired_gate_up_gemm_bits(ggml_type, monkeypatch):
     """At a chunk whose two-GEMM path splits no K range (512 rows, ffn 8192:
     1024 output tiles), the paired launch gives the same output bits as the
     two GEMMs plus the SwiGLU digits kernel: the same products, summed in the
-    same order, and the same digits."""
-    layers, heads, kv_heads, head_dim, ffn, batch, base = 1, 4, 2, 64, 8192, 512, 3
+    same order, and the same digits.  The same holds for the next layer's
+    RMSNorm digits formed inside down's split-K sums against the separate
+    sums and digits launches (TE_HIP_GEMM_REDUCE_RMS=0)."""
+    layers, heads, kv_heads, head_dim, ffn, batch, base = 2, 4, 2, 64, 8192, 512, 3
     ctx = base + batch
     m = S.synthetic_model(93, ggml_type, layers, heads, kv_heads, head_dim, ffn, 64, ctx, base)
     hidden = m["hidden"]
     cos, sin = A.rope_table(ctx, head_dim, 1.0e6)
     x_in = _dev(S.normal(93, "rows", (batch, hidden)))
     outs = []
-    for mode in ("1", "0"):
+    for mode, fused in (("1", "1"), ("0", "1"), ("1", "0")):
         monkeypatch.setenv("TE_HIP_GEMM_GLU", mode)
+        monkeypatch.setenv("TE_HIP_GEMM_REDUCE_RMS", fused)
         kc, vc = _dev(m["key_cache"]), _dev(m["value_cache"])
         vt = A.value_t_buffer(1, layers, ctx, kv_heads, head_dim)
         A.value_transpose(vc.view(torch.float16).reshape(1, layers, ctx, kv_heads, head_dim), vt,
@@ -143,8 +146,9 @@ def test_prefill_paired_gate_up_gemm_bits(ggml_type, monkeypatch):
                                     heads, kv_heads, head_dim, ffn, 1e-6)
         torch.cuda.synchronize()
         outs.append(got.cpu().numpy())
-    print(f"type {ggml_type}: paired vs two GEMMs max |diff| {np.abs(outs[0] - outs[1]).max():.3g}")
-    assert np.isfinite(outs[0]).all() and np.array_equal(outs[0], outs[1])
+    print(f"type {ggml_type}: paired vs two GEMMs max |diff| {np.abs(outs[0] - outs[1]).max():.3g}, "
+          f"fused vs separate RMSNorm digits {np.abs(outs[0] - outs[2]).max():.3g}")
+    assert np.isfinite(outs[0]).all() and np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
 def test_prefill_layer_by_layer(oracle_mod):

@@ -572,6 +572,82 @@ __global__ __launch_bounds__(256) void gemm_reduce_segs_kernel(const float *__re
     }
 }
 
+// gemm_reduce_kernel's sums for one row (resid + the splits' partial sums in
+// split order -> out), then that row's RMSNorm digits into hi / lo / scales,
+// exactly as quant_act_kernel<kActRmsNorm> computes them from out: thread t
+// holds columns t + 256 u, summed into the fp64 sum of squares in that order,
+// which are the values lane t % 32 of half wave t / 32 quantizes for blocks
+// t / 32 + 8 u.  One workgroup per row, N <= kRmsCache * 256, N % 32 == 0,
+// splits <= kRmsSplits.  Every load is issued before the first store (out may
+// be resid), so all of a thread's loads are in flight together.
+constexpr int kRmsCache = 8;
+constexpr int kRmsSplits = 8;
+__global__ __launch_bounds__(kActThreads) void gemm_reduce_rms_kernel(const float *__restrict__ part, int splits,
+                                                                      size_t count, const float *resid, float *out,
+                                                                      int N, const float *__restrict__ norm_w,
+                                                                      float eps, int8_t *__restrict__ hi,
+                                                                      int8_t *__restrict__ lo,
+                                                                      float *__restrict__ scales) {
+    const size_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    float pv[kRmsCache][kRmsSplits];
+    float rv[kRmsCache];
+#pragma unroll
+    for (int u = 0; u < kRmsCache; ++u) {
+        const int i = tid + kActThreads * u;
+        const size_t o = row * (size_t)N + i;
+        rv[u] = 0.0f;
+#pragma unroll
+        for (int z = 0; z < kRmsSplits; ++z) {
+            pv[u][z] = i < N && z < splits ? part[(size_t)z * count + o] : 0.0f;
+        }
+        if (i < N && resid != nullptr) {
+            rv[u] = resid[o];
+        }
+    }
+    float xv[kRmsCache];
+    double ss = 0.0;
+#pragma unroll
+    for (int u = 0; u < kRmsCache; ++u) {
+        const int i = tid + kActThreads * u;
+        float a = pv[u][0];
+#pragma unroll
+        for (int z = 1; z < kRmsSplits; ++z) {
+            if (z < splits) {
+                a += pv[u][z];
+            }
+        }
+        const float x = resid != nullptr ? rv[u] + a : a;
+        xv[u] = x;
+        if (i < N) {
+            out[row * (size_t)N + i] = x;
+            const double d = (double)x;
+            ss += d * d;
+        }
+    }
+    __shared__ double sum_part[kActThreads / 64];
+    for (int off = 32; off > 0; off >>= 1) {
+        ss += __shfl_xor(ss, off);
+    }
+    if ((tid & 63) == 0) {
+        sum_part[tid >> 6] = ss;
+    }
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < kActThreads / 64; ++w) {
+        t += sum_part[w];
+    }
+    const float rms = 1.0f / sqrtf((float)(t / (double)N) + eps);
+    const int lane = tid & 31;
+#pragma unroll
+    for (int u = 0; u < kRmsCache; ++u) {
+        const int bb = (tid >> 5) + (kActThreads / 32) * u;
+        if (bb < N / 32) {  // uniform per half wave
+            quant_block(xv[u] * rms * norm_w[bb * 32 + lane], row, N, bb, lane, hi, lo, scales);
+        }
+    }
+}
+
 // out = (resid +) the splits' partial sums, added in split order.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int splits, size_t count,
                                                           const float *resid, float *out) {
@@ -619,7 +695,8 @@ te_status launch_quant_act(int pre, const float *x, const float *x2, const float
 }
 
 te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, const void *act, size_t rows,
-                             size_t k, float *partials, size_t partial_bytes, hipStream_t stream) {
+                             size_t k, float *partials, size_t partial_bytes, hipStream_t stream,
+                             const GemmRmsDigits *post) {
     if ((ggml_type != kQ4_0 && ggml_type != kQ8_0) || k % 32 != 0 || rows == 0 || rows > 0x7fffffffu ||
         k > (1u << 24) || nseg < 1 || nseg > kMaxGemmSegs) {
         return TE_STATUS_UNSUPPORTED;
@@ -649,7 +726,7 @@ te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, 
     if (!staged && nseg > 1) {
         for (int i = 0; i < nseg; ++i) {
             const te_status st = launch_gemm_q_segs(ggml_type, &segs[i], 1, act, rows, k, partials, partial_bytes,
-                                                    stream);
+                                                    stream, nullptr);
             if (st != TE_STATUS_OK) {
                 return st;
             }
@@ -718,22 +795,48 @@ te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, 
         }
     }
 #undef TE_GEMM
+    // the RMSNorm digits of a single output: fused into the split-K sums
+    // where the row fits the fused kernel, else from out afterwards
+    const bool rms = post != nullptr && nseg == 1 && n % 32 == 0;
+    bool digits_done = false;
     if (splits > 1) {
         const size_t count = rows * n_total;
         const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
-        if (nseg == 1) {
+        const char *env = getenv("TE_HIP_GEMM_REDUCE_RMS");
+        if (rms && n <= (size_t)kRmsCache * kActThreads && splits <= (size_t)kRmsSplits &&
+            !(env != nullptr && env[0] == '0')) {
+            const size_t planes_out = plane_bytes(rows, n);
+            int8_t *ohi = static_cast<int8_t *>(post->act_out);
+            int8_t *olo = ohi + planes_out;
+            float *osc = reinterpret_cast<float *>(olo + planes_out);
+            gemm_reduce_rms_kernel<<<(unsigned)rows, kActThreads, 0, stream>>>(
+                partials, (int)splits, count, res, out, (int)n, post->norm_w, post->eps, ohi, olo, osc);
+            digits_done = true;
+        } else if (nseg == 1) {
             gemm_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, count, res, out);
         } else {
             gemm_reduce_segs_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, (int)rows, sg);
         }
     }
-    return launch_status();
+    te_status st = launch_status();
+    if (st == TE_STATUS_OK && post != nullptr && !digits_done) {
+        st = launch_quant_act(kActRmsNorm, out, nullptr, post->norm_w, post->eps, rows, n, post->act_out, stream);
+    }
+    return st;
 }
 
 te_status launch_gemm_q(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n, size_t k,
                         float *out, const float *resid, float *partials, size_t partial_bytes, hipStream_t stream) {
     const GemmSeg seg = {weights, out, resid, n};
-    return launch_gemm_q_segs(ggml_type, &seg, 1, act, rows, k, partials, partial_bytes, stream);
+    return launch_gemm_q_segs(ggml_type, &seg, 1, act, rows, k, partials, partial_bytes, stream, nullptr);
+}
+
+te_status launch_gemm_q_rms(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n,
+                            size_t k, float *out, const float *resid, float *partials, size_t partial_bytes,
+                            const float *norm_w, float eps, void *act_out, hipStream_t stream) {
+    const GemmSeg seg = {weights, out, resid, n};
+    const GemmRmsDigits post = {norm_w, eps, act_out};
+    return launch_gemm_q_segs(ggml_type, &seg, 1, act, rows, k, partials, partial_bytes, stream, &post);
 }
 
 te_status launch_gemm_glu_q(uint32_t ggml_type, const void *gate_w, const void *up_w, const void *act, size_t rows,

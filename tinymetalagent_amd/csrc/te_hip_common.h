@@ -138,8 +138,22 @@ struct GemmSeg {
     const float *resid;
     size_t n;
 };
+// With `post` (one segment): afterwards also the RMSNorm digits of out
+// (launch_quant_act(1, out, nullptr, norm_w, eps) into act_out, the same
+// bits), fused into the split-K sums where they run (TE_HIP_GEMM_REDUCE_RMS=0:
+// separate launches).  act_out may be act.
+struct GemmRmsDigits {
+    const float *norm_w;
+    float eps;
+    void *act_out;
+};
 te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, const void *act, size_t rows,
-                             size_t k, float *partials, size_t partial_bytes, hipStream_t stream);
+                             size_t k, float *partials, size_t partial_bytes, hipStream_t stream,
+                             const GemmRmsDigits *post = nullptr);
+// launch_gemm_q, then the RMSNorm digits of out (see GemmRmsDigits).
+te_status launch_gemm_q_rms(const void *weights, uint32_t ggml_type, const void *act, size_t rows, size_t n,
+                            size_t k, float *out, const float *resid, float *partials, size_t partial_bytes,
+                            const float *norm_w, float eps, void *act_out, hipStream_t stream);
 // Gate and up [n][k] against the same activation digits in one launch whose
 // tiles pair the same rows of both, writing silu(gate) * up as the down
 // projection's digits into act_out (act_buffer_bytes(rows, n) bytes, the same

@@ -16,9 +16,11 @@
 // segmented launch (te_gemm.hip); the fused prefill step keeping V^T (bias + RoPE + fp16
 // append into the K / V caches and V^T, then the MFMA causal attention,
 // te_prefill.hip); the digits of the attention output and the Wo GEMM with
-// the residual in its epilogue; RMSNorm digits; gate and up as one launch
+// the residual (and the next RMSNorm's digits in its split-K sums); gate and
+// up as one launch
 // whose epilogue writes the SwiGLU digits (else two GEMMs and the SwiGLU
-// digits); the down GEMM with the residual.
+// digits); the down GEMM with the residual and the next layer's attention
+// RMSNorm digits.
 //
 // Differences from the Metal slot, all device-resident: the K / V caches are
 // the HIP path's fp16 caches [layers][context_tokens][kv] plus the transposed
@@ -170,8 +172,11 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
             te_hip::prof_mark(st, share, 3);
             return r == TE_STATUS_OK;
         };
-        if (!done(s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights + l * hidden, epsilon, batch,
-                                               hidden, b.act, st), ew) ||
+        // the attention RMSNorm digits of layer l > 0 came with the previous
+        // layer's down projection
+        if ((l == 0 && !done(s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights, epsilon, batch, hidden,
+                                                          b.act, st),
+                             ew)) ||
             !qkv_done(s = te_hip::launch_gemm_q_segs(ggml_type, qkv, 3, b.act, batch, hidden, b.part, b.part_bytes,
                                                      st)) ||
             !done(s = te_hip_attention_prefill_step_vt_f16(
@@ -180,9 +185,10 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
                       base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream),
                   te_hip::kProfAttention) ||
             !done(s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st), ew) ||
-            !done(s = gemm(output_offsets, hidden, hidden, out, out), te_hip::kProfO) ||
-            !done(s = te_hip::launch_quant_act(1, out, nullptr, ffn_norm_weights + l * hidden, epsilon, batch,
-                                               hidden, b.act, st), ew) ||
+            !done(s = te_hip::launch_gemm_q_rms(m + output_offsets[l], ggml_type, b.act, batch, hidden, hidden, out,
+                                                out, b.part, b.part_bytes, ffn_norm_weights + l * hidden, epsilon,
+                                                b.act, st),
+                  te_hip::kProfO) ||
             !glu_done(s = te_hip::launch_gemm_glu_q(ggml_type, m + gate_offsets[l], m + up_offsets[l], b.act, batch,
                                                     ffn, hidden, b.act_ffn, st, &glu))) {
             break;
@@ -193,9 +199,14 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
                            ew))) {
             break;
         }
-        if (!done(s = te_hip::launch_gemm_q(m + down_offsets[l], ggml_type, b.act_ffn, batch, hidden, ffn, out, out,
-                                            b.part, b.part_bytes, st),
-                  te_hip::kProfDown)) {
+        // down + residual, with the next layer's attention RMSNorm digits
+        s = l + 1 < layers
+                ? te_hip::launch_gemm_q_rms(m + down_offsets[l], ggml_type, b.act_ffn, batch, hidden, ffn, out, out,
+                                            b.part, b.part_bytes, attn_norm_weights + (l + 1) * hidden, epsilon,
+                                            b.act, st)
+                : te_hip::launch_gemm_q(m + down_offsets[l], ggml_type, b.act_ffn, batch, hidden, ffn, out, out,
+                                        b.part, b.part_bytes, st);
+        if (!done(s, te_hip::kProfDown)) {
             break;
         }
     }
