@@ -302,8 +302,8 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const unsigned char *__rest
 // dword count, so the wave's 32 rows read a block without bank conflicts.  A
 // lane's block (fp16 scale + codes) is a 5-dword LDS window whose byte
 // alignment is the same for every lane (the block index's parity), unpacked by
-// byte alignment and nibble masks.  Activation digits are prefetched two
-// blocks ahead.  Needs row_bytes % 16 == 0 and a 16-byte aligned tensor;
+// byte alignment and nibble masks.  Activation digits are prefetched one
+// block ahead.  Needs row_bytes % 16 == 0 and a 16-byte aligned tensor;
 // split boundaries fall on whole chunks.
 constexpr int kWChunk = 8;
 
@@ -423,8 +423,9 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
         }
         (void)c;
     };
-    // activation digits of block b (two blocks in flight ahead of use)
-    v4i ah[4], al[4];
+    // activation digits of block b, one block ahead of use (two ahead took 8
+    // more VGPRs and measured 3-4 % slower)
+    v4i ah[2], al[2];
     auto load_a = [&](int b, int slot) {
         if (b < kb1) {
             const size_t o = ((a_tile + b) << 10) + a_lane;
@@ -441,7 +442,6 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
         load_chunk(0);
         store_chunk(0, 0);
         load_a(kb0, 0);
-        load_a(kb0 + 1, 1);
     }
     __syncthreads();
     for (int c = 0; c < n_chunks; ++c) {
@@ -453,7 +453,7 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
 #pragma unroll
         for (int bb = 0; bb < kWChunk; ++bb) {
             const int b = kb0 + c * kWChunk + bb;
-            load_a(b + 2, (bb + 2) & 3);
+            load_a(b + 1, (bb + 1) & 1);
             if (b < kb1) {
                 // the block's fp16 scale and 16 codes of this lane's k half: a
                 // 5-dword window starting at the block's dword (Q8_0: the half's)
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
                         bq[k] = (int)code[k];
                     }
                 }
-                const int slot = bb & 3;
+                const int slot = bb & 1;
                 v16i cc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah[slot], bq, v16i{}, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
