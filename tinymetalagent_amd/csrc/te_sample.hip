@@ -65,40 +65,11 @@ SampleLayout sample_layout(size_t n) {
     return l;
 }
 
-// Workgroup w < blocks: the k-th largest of 1024-block w; w >= blocks: of
-// 8192-block w - blocks.  Exact, by a 4-pass radix select (8 bits a pass) on
-// the order-preserving keys; -inf for a block shorter than k.
-__global__ __launch_bounds__(kThreads) void kth_largest_kernel(const float *x, uint32_t n, uint32_t k, int blocks,
-                                                               unsigned char *ws, SampleLayout l) {
-    constexpr int PER = kBigBlock / kThreads;
-    const int w = blockIdx.x;
-    const bool big = w >= blocks;
-    const uint32_t len = big ? kBigBlock : kBlock;
-    const uint32_t start = big ? (uint32_t)(w - blocks) * kBigBlock : (uint32_t)w * kBlock;
-    const uint32_t cnt = min(len, n - start);
-    float *out = reinterpret_cast<float *>(ws + (big ? l.kth_big : l.kth)) + (big ? w - blocks : w);
-    uint32_t *hdr = reinterpret_cast<uint32_t *>(ws);
-    if (w == 0 && threadIdx.x == 0) {
-        hdr[0] = 0;  // the candidate pass's counter (it runs after this launch)
-    }
-    uint32_t key[PER];
-    bool nan = false;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const uint32_t i = (uint32_t)j * kThreads + threadIdx.x;
-        const float v = i < cnt ? x[start + i] : -INFINITY;
-        nan |= v != v;
-        key[j] = i < cnt ? float_key(v) : 0u;
-    }
-    if (nan) {
-        hdr[1] = 1u;
-    }
-    if (cnt < k) {
-        if (threadIdx.x == 0) {
-            *out = -INFINITY;
-        }
-        return;
-    }
+// The k-th largest of the `cnt` keys held PER per thread (thread t, slot j:
+// key j * 256 + t), by a 4-pass radix select (8 bits a pass) over LDS
+// histograms; exact.
+template <int PER>
+__device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[PER], uint32_t cnt, uint32_t k) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t sel[2];  // chosen digit, the rank left within it
     uint32_t prefix = 0, mask = 0, rank = k;  // the rank-th largest among keys matching prefix under mask
@@ -151,8 +122,46 @@ __global__ __launch_bounds__(kThreads) void kth_largest_kernel(const float *x, u
         rank = sel[1];
         __syncthreads();
     }
+    return prefix;
+}
+
+template <int LEN>
+__device__ __forceinline__ void kth_block(const float *x, uint32_t n, uint32_t k, uint32_t start, float *out) {
+    constexpr int PER = LEN / kThreads;
+    const uint32_t cnt = min((uint32_t)LEN, n - start);
+    if (cnt < k) {  // uniform
+        if (threadIdx.x == 0) {
+            *out = -INFINITY;
+        }
+        return;
+    }
+    uint32_t key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const uint32_t i = (uint32_t)j * kThreads + threadIdx.x;
+        key[j] = i < cnt ? float_key(x[start + i]) : 0u;
+    }
+    const uint32_t kk = kth_key<PER>(key, cnt, k);
     if (threadIdx.x == 0) {
-        *out = key_float(prefix);
+        *out = key_float(kk);
+    }
+}
+
+// Workgroup w < blocks: the k-th largest of 1024-block w; w >= blocks: of
+// 8192-block w - blocks; -inf for a block shorter than k.  Workgroup 0 also
+// clears the header (candidate counter, NaN flag) for the candidate pass,
+// which runs after this launch.
+__global__ __launch_bounds__(kThreads) void kth_largest_kernel(const float *x, uint32_t n, uint32_t k, int blocks,
+                                                               unsigned char *ws, SampleLayout l) {
+    const int w = blockIdx.x;
+    if (w == 0 && threadIdx.x < 2) {
+        reinterpret_cast<uint32_t *>(ws)[threadIdx.x] = 0u;
+    }
+    if (w < blocks) {
+        kth_block<kBlock>(x, n, k, (uint32_t)w * kBlock, reinterpret_cast<float *>(ws + l.kth) + w);
+    } else {
+        kth_block<kBigBlock>(x, n, k, (uint32_t)(w - blocks) * kBigBlock,
+                             reinterpret_cast<float *>(ws + l.kth_big) + (w - blocks));
     }
 }
 
@@ -186,13 +195,18 @@ __global__ __launch_bounds__(kThreads) void candidates_kernel(const float *x, ui
     t = red[0];
     float v[4];
     uint32_t take = 0;
+    bool nan = false;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t i = start + 4 * threadIdx.x + j;
         v[j] = i < n ? x[i] : -INFINITY;
+        nan |= v[j] != v[j];
         if (i < n && (c == 0 || v[j] > t)) {
             take |= 1u << j;
         }
+    }
+    if (nan) {
+        reinterpret_cast<uint32_t *>(ws)[1] = 1u;  // the host then scans every logit
     }
     // exclusive scan of the per-thread counts (Hillis-Steele)
     const uint32_t mine = __popc(take);
@@ -327,9 +341,6 @@ extern "C" te_status te_hip_sample_top_k_f32(const float *logits, size_t vocab, 
     const uint32_t k = (uint32_t)std::min<size_t>(top_k == 0 ? 1 : std::min(top_k, kMaxTopK), vocab);
     const hipStream_t st = te_hip::as_stream(stream);
     unsigned char *ws = static_cast<unsigned char *>(workspace);
-    if (hipMemsetAsync(ws + 4, 0, 4, st) != hipSuccess) {  // the NaN flag
-        return TE_STATUS_RUNTIME_ERROR;
-    }
     kth_largest_kernel<<<l.blocks + l.big_blocks, kThreads, 0, st>>>(logits, (uint32_t)vocab, k, l.blocks, ws, l);
     candidates_kernel<<<l.blocks, kThreads, 0, st>>>(logits, (uint32_t)vocab, ws, l);
     te_status s = te_hip::launch_status();
