@@ -63,6 +63,20 @@ def test_sample_ties_and_orders():
     _check(late, 40, 0.3, 95, "late winners")
 
 
+def test_sample_few_distinct_values():
+    """Four distinct logit values over the whole vocabulary: every replacement
+    meets ties, so the list's minimum slot (the first slot of the smallest
+    value) decides which slot each new logit takes, and the draw walks the
+    slots in that order."""
+    rng = np.random.default_rng(13)
+    few = np.floor(rng.uniform(0.0, 4.0, VOCAB)).astype(np.float32)
+    for k, state in ((40, 31), (300, 32), (1024, 33)):
+        _check(few, k, 0.7, state, f"four values, k {k}")
+    signed_zeros = np.where(rng.uniform(size=20000) < 0.5, -0.0, 0.0).astype(np.float32)
+    signed_zeros[[5, 777, 19000]] = [1.0, 2.0, 1.0]
+    _check(signed_zeros, 40, 0.3, 34, "signed zeros")
+
+
 def test_sample_small_and_edge_cases():
     rng = np.random.default_rng(11)
     _check(rng.normal(size=700), 40, 0.3, 5, "vocab 700")

@@ -25,6 +25,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 namespace {
@@ -239,13 +240,41 @@ __global__ __launch_bounds__(kThreads) void candidates_kernel(const float *x, ui
 }
 
 // The reference's scan and draw over a stream of (index, value) in index
-// order; next(j) gives element j of `count`.
+// order; next(j) gives element j of `count`.  The reference's list: slots
+// filled in order, then each value strictly above the list's minimum replaces
+// it, the minimum being the first (lowest) slot holding the smallest value.
+// Without NaN the slots sit in a binary heap ordered by (value, slot), whose
+// top is exactly that slot, so a replacement costs O(log k) instead of a pass
+// over the k slots; with a NaN (`reference_min`) the minimum is searched the
+// reference's way, whose comparisons then decide the list.
 template <typename Next>
-uint32_t scan_and_draw(size_t count, uint32_t k, float temperature, uint64_t *rng, Next next) {
-    std::vector<float> v;
-    std::vector<uint32_t> idx;
-    v.reserve(k);
-    idx.reserve(k);
+uint32_t scan_and_draw(size_t count, uint32_t k, float temperature, uint64_t *rng, Next next,
+                       bool reference_min = false) {
+    thread_local std::vector<float> v;
+    thread_local std::vector<uint32_t> idx;
+    thread_local std::vector<uint32_t> heap;  // slots
+    v.clear();
+    idx.clear();
+    heap.clear();
+    auto below = [&](uint32_t a, uint32_t b) { return v[a] < v[b] || (!(v[b] < v[a]) && a < b); };
+    auto sift_down = [&](size_t i) {
+        const size_t n = heap.size();
+        for (;;) {
+            const size_t l = 2 * i + 1, r = l + 1;
+            size_t m = i;
+            if (l < n && below(heap[l], heap[m])) {
+                m = l;
+            }
+            if (r < n && below(heap[r], heap[m])) {
+                m = r;
+            }
+            if (m == i) {
+                return;
+            }
+            std::swap(heap[i], heap[m]);
+            i = m;
+        }
+    };
     size_t min_pos = 0;
     auto find_min = [&] {
         min_pos = 0;
@@ -259,16 +288,36 @@ uint32_t scan_and_draw(size_t count, uint32_t k, float temperature, uint64_t *rn
         uint32_t i;
         float x;
         next(j, i, x);
+        if (reference_min) {
+            if (v.size() < k) {
+                v.push_back(x);
+                idx.push_back(i);
+                if (v.size() == k) {
+                    find_min();
+                }
+            } else if (x > v[min_pos]) {
+                v[min_pos] = x;
+                idx[min_pos] = i;
+                find_min();
+            }
+            continue;
+        }
         if (v.size() < k) {
             v.push_back(x);
             idx.push_back(i);
             if (v.size() == k) {
-                find_min();
+                heap.resize(k);
+                for (uint32_t t = 0; t < k; ++t) {
+                    heap[t] = t;
+                }
+                for (size_t t = k / 2; t-- > 0;) {
+                    sift_down(t);
+                }
             }
-        } else if (x > v[min_pos]) {
-            v[min_pos] = x;
-            idx[min_pos] = i;
-            find_min();
+        } else if (x > v[heap[0]]) {
+            v[heap[0]] = x;
+            idx[heap[0]] = i;
+            sift_down(0);
         }
     }
     float mx = v[0];
@@ -276,7 +325,8 @@ uint32_t scan_and_draw(size_t count, uint32_t k, float temperature, uint64_t *rn
         mx = v[j] > mx ? v[j] : mx;
     }
     const double t = temperature > 1e-6f ? (double)temperature : 1e-6;
-    std::vector<double> p(v.size());
+    thread_local std::vector<double> p;
+    p.resize(v.size());
     double sum = 0.0;
     for (size_t j = 0; j < v.size(); ++j) {
         p[j] = exp(((double)v[j] - (double)mx) / t);
@@ -364,10 +414,13 @@ extern "C" te_status te_hip_sample_top_k_f32(const float *logits, size_t vocab, 
         if (hipMemcpy(all.data(), logits, vocab * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) {
             return TE_STATUS_RUNTIME_ERROR;
         }
-        *out_token = scan_and_draw(vocab, k, temperature, rng_state, [&](size_t j, uint32_t &i, float &x) {
-            i = (uint32_t)j;
-            x = all[j];
-        });
+        *out_token = scan_and_draw(
+            vocab, k, temperature, rng_state,
+            [&](size_t j, uint32_t &i, float &x) {
+                i = (uint32_t)j;
+                x = all[j];
+            },
+            true);
         return TE_STATUS_OK;
     }
     const size_t total = hdr[0];
@@ -376,7 +429,8 @@ extern "C" te_status te_hip_sample_top_k_f32(const float *logits, size_t vocab, 
         return TE_STATUS_RUNTIME_ERROR;
     }
     // the candidates in block order (blocks took their bases in any order)
-    std::vector<size_t> order;
+    thread_local std::vector<size_t> order;
+    order.clear();
     order.reserve(total);
     const uint32_t *slots = reinterpret_cast<const uint32_t *>(h + l.hdr);
     for (int c = 0; c < l.blocks; ++c) {
