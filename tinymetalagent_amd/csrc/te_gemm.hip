@@ -701,6 +701,9 @@ te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, 
         k > (1u << 24) || nseg < 1 || nseg > kMaxGemmSegs) {
         return TE_STATUS_UNSUPPORTED;
     }
+    if (post != nullptr && nseg != 1) {
+        return TE_STATUS_INVALID_ARGUMENT;  // the digits are of one output
+    }
     const size_t row_bytes = k / 32 * (ggml_type == kQ4_0 ? 18 : 34);
     // the LDS-staged kernel where a row's chunks are 16-byte aligned (its
     // split boundaries fall on whole chunks), else one gemm_q_kernel launch
