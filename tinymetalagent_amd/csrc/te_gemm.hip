@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace {
 
@@ -375,11 +376,21 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
     const int n_chunks = (kb1 - kb0 + kWChunk - 1) / kWChunk;
 
     // chunk c's pieces and activation scales: global -> registers (a chunk
-    // ahead), then registers -> LDS buffer
+    // ahead), then registers -> LDS buffer. Q8_0 stages its 5 pieces per
+    // thread in two halves (the first stored and the second loaded at the
+    // chunk's midpoint): only 3 pieces are held in registers, which keeps the
+    // kernel at <= 128 VGPRs (4 waves per SIMD instead of 3). Q4_0 (3 pieces)
+    // stages the chunk at once: halves measured slower there.
     constexpr int SPT = kWChunk * 64 / 256;  // scales per thread
-    uint4 wreg[PPT];
+    constexpr bool HALVES = TYPE == kQ8_0;
+    constexpr int PA = HALVES ? (PPT + 1) / 2 : PPT;  // pieces of the first half
+    using P0 = std::integral_constant<int, 0>;
+    using PMid = std::integral_constant<int, PA>;
+    using PEnd = std::integral_constant<int, PPT>;
+    using PLast = std::integral_constant<int, HALVES ? PA : 0>;  // first piece stored at the chunk's end
+    uint4 wreg[PA];
     float sreg[SPT];
-    auto load_chunk = [&](int c) {
+    auto load_scales = [&](int c) {
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const int t = tid + 256 * i;
@@ -387,41 +398,47 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
             const int row = min(m_wg + rr, M - 1);
             sreg[i] = cb < kb1 ? scales[(size_t)row * nb + cb] : 0.0f;
         }
+    };
+    // pieces I0 .. I1 - 1 of chunk c into wreg[0 ..]
+    auto load_pieces = [&](int c, auto i0, auto i1) {
+        constexpr int I0 = decltype(i0)::value, I1 = decltype(i1)::value;
         const size_t cbyte = (size_t)(kb0 + c * kWChunk) * BB;
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
+        for (int i = I0; i < I1; ++i) {
             const int item = tid + 256 * i;
             const int r = item / RC, j = item % RC;
             const size_t off = cbyte + 16 * (size_t)j;
-            wreg[i] = make_uint4(0u, 0u, 0u, 0u);
+            wreg[i - I0] = make_uint4(0u, 0u, 0u, 0u);
             if (item < PIECES && off < row_bytes) {  // a piece is wholly in its row or wholly past it
                 // GLU: rows 0..31 of the tile from the gate matrix, 32..63 from
                 // up (a byte offset from gate: a per-piece pointer select
                 // costs registers that lower occupancy)
                 const int row = min(n_wg + (GLU ? (r & 31) : r), N - 1);
                 const uintptr_t base = (uintptr_t)w + (GLU ? (uintptr_t)(r >> 5) * up_delta : 0);
-                wreg[i] = *reinterpret_cast<const uint4 *>(base + (size_t)row * row_bytes + off);
+                wreg[i - I0] = *reinterpret_cast<const uint4 *>(base + (size_t)row * row_bytes + off);
             }
         }
     };
-    auto store_chunk = [&](int c, int buf) {
+    auto store_pieces = [&](int buf, auto i0, auto i1) {
+        constexpr int I0 = decltype(i0)::value, I1 = decltype(i1)::value;
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
+        for (int i = I0; i < I1; ++i) {
             const int item = tid + 256 * i;
             if (item < PIECES) {
                 uint32_t *dst = reinterpret_cast<uint32_t *>(&w_lds[buf][(item / RC) * PITCH + 16 * (item % RC)]);
-                dst[0] = wreg[i].x;
-                dst[1] = wreg[i].y;
-                dst[2] = wreg[i].z;
-                dst[3] = wreg[i].w;
+                dst[0] = wreg[i - I0].x;
+                dst[1] = wreg[i - I0].y;
+                dst[2] = wreg[i - I0].z;
+                dst[3] = wreg[i - I0].w;
             }
         }
+    };
+    auto store_scales = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const int t = tid + 256 * i;
             s_lds[buf][t >> 6][t & 63] = sreg[i];
         }
-        (void)c;
     };
     // activation digits of block b, one block ahead of use (two ahead took 8
     // more VGPRs and measured 3-4 % slower)
@@ -439,21 +456,31 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
         acc[r] = 0.0f;
     }
     if (n_chunks > 0) {
-        load_chunk(0);
-        store_chunk(0, 0);
+        load_scales(0);
+        load_pieces(0, P0{}, PMid{});
+        store_pieces(0, P0{}, PMid{});
+        load_pieces(0, PMid{}, PEnd{});
+        store_pieces(0, PMid{}, PEnd{});
+        store_scales(0);
         load_a(kb0, 0);
     }
     __syncthreads();
     for (int c = 0; c < n_chunks; ++c) {
         const int buf = c & 1;
         if (c + 1 < n_chunks) {
-            load_chunk(c + 1);
+            load_scales(c + 1);
+            load_pieces(c + 1, P0{}, PMid{});
         }
         const unsigned char *wrow = &w_lds[buf][(wn * 32 + lr) * PITCH];
 #pragma unroll
         for (int bb = 0; bb < kWChunk; ++bb) {
             const int b = kb0 + c * kWChunk + bb;
             load_a(b + 1, (bb + 1) & 1);
+            if (HALVES && bb == kWChunk / 2 && c + 1 < n_chunks) {
+                // buffer buf ^ 1 was last read before the previous chunk's barrier
+                store_pieces(buf ^ 1, P0{}, PMid{});
+                load_pieces(c + 1, PMid{}, PEnd{});
+            }
             if (b < kb1) {
                 // the block's fp16 scale and 16 codes of this lane's k half: a
                 // 5-dword window starting at the block's dword (Q8_0: the half's)
@@ -509,7 +536,8 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
             }
         }
         if (c + 1 < n_chunks) {
-            store_chunk(c + 1, buf ^ 1);
+            store_pieces(buf ^ 1, PLast{}, PEnd{});
+            store_scales(buf ^ 1);
         }
         __syncthreads();
     }
