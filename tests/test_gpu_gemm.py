@@ -70,7 +70,10 @@ def _run(oracle_mod, ggml_type, rows, n, k, pre=0, resid=False, seed=3, scale=1.
 
 
 @pytest.mark.parametrize("ggml_type,rows,n,k", [
-    (2, 1, 64, 64), (2, 7, 100, 96), (8, 64, 64, 2048), (2, 130, 257, 256), (8, 65, 33, 512), (2, 256, 512, 2048)])
+    (2, 1, 64, 64), (2, 7, 100, 96), (8, 64, 64, 2048), (2, 130, 257, 256), (8, 65, 33, 512), (2, 256, 512, 2048),
+    # Q8_0 stages a weight chunk of 8 blocks in two halves: one partial chunk
+    # (no second half staged ahead), and a full chunk then a partial one
+    (8, 7, 100, 96), (8, 130, 257, 288)])
 def test_gemm_vs_fp64(oracle_mod, ggml_type, rows, n, k):
     _run(oracle_mod, ggml_type, rows, n, k)
 
