@@ -212,6 +212,14 @@ te_status launch_kv_append(const float *k, const float *v, const float *k_bias, 
                            const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
                            uint16_t *value_cache, size_t seqs, size_t layers, size_t tokens, size_t base_position,
                            size_t context_tokens, size_t kv_heads, size_t head_dim, hipStream_t stream);
+// The fused prefill step's k / v append (launch_kv_append's arithmetic) and
+// the V^T rows of the chunk's positions (launch_value_transpose's layout,
+// row pitch ctx_pad) in one launch; head_dim 64 or 128.
+te_status launch_kv_append_vt(const float *k, const float *v, const float *k_bias, const float *v_bias,
+                              const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+                              uint16_t *value_cache, uint16_t *value_t, size_t sl_count, size_t layers,
+                              size_t tokens, size_t base_position, size_t context_tokens, size_t ctx_pad,
+                              size_t kv_heads, size_t head_dim, hipStream_t stream);
 te_status launch_rope_rows(float *values, size_t heads, size_t head_dim, const float *cos_row,
                            const float *sin_row, hipStream_t stream);
 te_status launch_mma_kat(int mode, const float *query, const float *key_t, const float *value, int k_cols,

@@ -1076,12 +1076,10 @@ extern "C" te_status te_hip_attention_prefill_step_vt_f16(
         return st;
     }
     hipStream_t strm = te_hip::as_stream(stream);
-    st = te_hip::launch_kv_append(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache, seqs,
-                                  layers, tokens, base_position, context_tokens, kv_heads, head_dim, strm);
-    if (st == TE_STATUS_OK) {
-        st = launch_value_transpose(reinterpret_cast<const f16 *>(value_cache), reinterpret_cast<f16 *>(value_cache_t),
-                                    seqs * layers, base_position, tokens, context_tokens, kv_heads, head_dim, strm);
-    }
+    // bias + RoPE + fp16 append of k / v and the chunk's V^T rows: one launch
+    st = te_hip::launch_kv_append_vt(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache,
+                                     value_cache_t, seqs * layers, layers, tokens, base_position, context_tokens,
+                                     vt_pitch(context_tokens), kv_heads, head_dim, strm);
     if (st != TE_STATUS_OK) {
         return st;
     }

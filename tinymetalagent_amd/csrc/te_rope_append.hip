@@ -16,6 +16,8 @@
 // HBM-bound at prefill.
 #include "te_hip_common.h"
 
+#include <algorithm>
+
 #pragma clang fp contract(off)
 
 namespace {
@@ -116,6 +118,134 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
     }
 }
 
+// Fused prefill step's append and V^T in one launch: for the chunk's
+// positions [base, base + tokens) of every (seq*layer), bias + RoPE of k and
+// bias of v with rope_kv_append_kernel's operations (so the fp16 cache rows
+// are the same bits), and the V^T rows of those positions as
+// value_transpose_kernel writes them (zeros at [end, end8), end8 = end
+// rounded up to 8 within the row pitch).  One workgroup per 64 aligned
+// positions, KV head and seq*layer; the tile's v rows meet in LDS and leave
+// as 16-byte chunks of 8 positions per dim row.
+struct KvAppendVtArgs {
+    const float *k;  // [sl][tokens][kv_heads][D]
+    const float *v;
+    const float *k_bias;  // [layers][kv_heads*D] or null
+    const float *v_bias;
+    const float *cos_t;
+    const float *sin_t;
+    f16 *key_cache;    // [sl][ctx][kv_heads][D]
+    f16 *value_cache;
+    f16 *value_t;      // [sl][kv_heads][D][ctx_pad]
+    int layers;
+    int tokens;
+    int base;
+    int end8;
+    int ctx;
+    int ctx_pad;
+    int kv_heads;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void kv_append_vt_kernel(KvAppendVtArgs a) {
+    constexpr int P = 64;
+    constexpr int HALF = D / 2;
+    __shared__ __attribute__((aligned(16))) f16 tile[P][D + 8];
+    const int first = a.base;
+    const int end = a.base + a.tokens;
+    const int p0 = (first & ~(P - 1)) + P * (int)blockIdx.x;
+    const int h = blockIdx.y;
+    const int sl = blockIdx.z;
+    const int layer = sl % a.layers;
+    const int kv_dim = a.kv_heads * D;
+    const float *kb = a.k_bias != nullptr ? a.k_bias + (size_t)layer * kv_dim + h * D : nullptr;
+    const float *vb = a.v_bias != nullptr ? a.v_bias + (size_t)layer * kv_dim + h * D : nullptr;
+    // k: pairs (i, i + D/2), four per item
+    for (int idx = threadIdx.x; idx < P * (HALF / 4); idx += 256) {
+        const int r = idx / (HALF / 4);
+        const int i = 4 * (idx % (HALF / 4));
+        const int p = p0 + r;
+        if (p < first || p >= end) {
+            continue;
+        }
+        const float *krow = a.k + ((size_t)sl * a.tokens + (p - first)) * kv_dim + h * D;
+        const float4 a0 = *reinterpret_cast<const float4 *>(krow + i);
+        const float4 a1 = *reinterpret_cast<const float4 *>(krow + i + HALF);
+        float x0[4] = {a0.x, a0.y, a0.z, a0.w};
+        float x1[4] = {a1.x, a1.y, a1.z, a1.w};
+        if (kb != nullptr) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x0[j] = x0[j] + kb[i + j];
+                x1[j] = x1[j] + kb[i + j + HALF];
+            }
+        }
+        const float4 c4 = *reinterpret_cast<const float4 *>(a.cos_t + (size_t)p * HALF + i);
+        const float4 s4 = *reinterpret_cast<const float4 *>(a.sin_t + (size_t)p * HALF + i);
+        const float cs[4] = {c4.x, c4.y, c4.z, c4.w};
+        const float sn[4] = {s4.x, s4.y, s4.z, s4.w};
+        f16x4 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            lo[j] = (f16)(x0[j] * cs[j] - x1[j] * sn[j]);
+            hi[j] = (f16)(x1[j] * cs[j] + x0[j] * sn[j]);
+        }
+        f16 *dst = a.key_cache + ((size_t)sl * a.ctx + p) * kv_dim + h * D;
+        *reinterpret_cast<f16x4 *>(dst + i) = lo;
+        *reinterpret_cast<f16x4 *>(dst + i + HALF) = hi;
+    }
+    // v: 8 values per item, into the cache and the LDS tile (zeros outside the chunk)
+    for (int idx = threadIdx.x; idx < P * (D / 8); idx += 256) {
+        const int r = idx / (D / 8);
+        const int cq = idx % (D / 8);
+        const int p = p0 + r;
+        f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (p >= first && p < end) {
+            const float *vrow = a.v + ((size_t)sl * a.tokens + (p - first)) * kv_dim + h * D + 8 * cq;
+            const float4 b0 = *reinterpret_cast<const float4 *>(vrow);
+            const float4 b1 = *reinterpret_cast<const float4 *>(vrow + 4);
+            float x[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            if (vb != nullptr) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    x[j] = x[j] + vb[8 * cq + j];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                val[j] = (f16)x[j];
+            }
+            *reinterpret_cast<f16x8 *>(a.value_cache + ((size_t)sl * a.ctx + p) * kv_dim + h * D + 8 * cq) = val;
+        }
+        *reinterpret_cast<f16x8 *>(&tile[r][8 * cq]) = val;
+    }
+    __syncthreads();
+    f16 *dst = a.value_t + ((size_t)sl * a.kv_heads + h) * (size_t)D * a.ctx_pad;
+    for (int idx = threadIdx.x; idx < D * (P / 8); idx += 256) {
+        const int i = idx / (P / 8);
+        const int pc = idx % (P / 8);
+        const int pa = p0 + 8 * pc;
+        if (pa >= a.end8 || pa + 8 <= first) {
+            continue;
+        }
+        f16x8 val;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            val[j] = tile[8 * pc + j][i];
+        }
+        f16 *row = dst + (size_t)i * a.ctx_pad + pa;
+        if (pa >= first && pa + 8 <= a.end8) {
+            *reinterpret_cast<f16x8 *>(row) = val;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (pa + j >= first && pa + j < a.end8) {
+                    row[j] = val[j];
+                }
+            }
+        }
+    }
+}
+
 // In-place rotation of `heads` rows with one cos/sin row (te_rope_f32).
 __global__ __launch_bounds__(256) void rope_rows_kernel(float *values, int heads, int head_dim,
                                                         const float *cos_row, const float *sin_row) {
@@ -166,6 +296,43 @@ te_status launch_kv_append(const float *k, const float *v, const float *k_bias, 
     const size_t items = kv_heads * head_dim;
     const dim3 grid((unsigned)((items + 255) / 256), (unsigned)tokens, (unsigned)(seqs * layers));
     rope_kv_append_kernel<<<grid, 256, 0, stream>>>(a);
+    return launch_status();
+}
+
+te_status launch_kv_append_vt(const float *k, const float *v, const float *k_bias, const float *v_bias,
+                              const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+                              uint16_t *value_cache, uint16_t *value_t, size_t sl_count, size_t layers,
+                              size_t tokens, size_t base_position, size_t context_tokens, size_t ctx_pad,
+                              size_t kv_heads, size_t head_dim, hipStream_t stream) {
+    if ((head_dim != 64 && head_dim != 128) || tokens == 0 || ctx_pad < base_position + tokens ||
+        ctx_pad % 64 != 0 || sl_count > 65535 || kv_heads > 65535) {
+        return TE_STATUS_INVALID_ARGUMENT;
+    }
+    KvAppendVtArgs a = {};
+    a.k = k;
+    a.v = v;
+    a.k_bias = k_bias;
+    a.v_bias = v_bias;
+    a.cos_t = rope_cos;
+    a.sin_t = rope_sin;
+    a.key_cache = reinterpret_cast<f16 *>(key_cache);
+    a.value_cache = reinterpret_cast<f16 *>(value_cache);
+    a.value_t = reinterpret_cast<f16 *>(value_t);
+    a.layers = (int)layers;
+    a.tokens = (int)tokens;
+    a.base = (int)base_position;
+    const size_t end = base_position + tokens;
+    a.end8 = (int)std::min((end + 7) / 8 * 8, ctx_pad);
+    a.ctx = (int)context_tokens;
+    a.ctx_pad = (int)ctx_pad;
+    a.kv_heads = (int)kv_heads;
+    const size_t tiles = ((size_t)a.end8 - (base_position & ~(size_t)63) + 63) / 64;
+    const dim3 grid((unsigned)tiles, (unsigned)kv_heads, (unsigned)sl_count);
+    if (head_dim == 128) {
+        kv_append_vt_kernel<128><<<grid, 256, 0, stream>>>(a);
+    } else {
+        kv_append_vt_kernel<64><<<grid, 256, 0, stream>>>(a);
+    }
     return launch_status();
 }
 
