@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
 // bias of v with rope_kv_append_kernel's operations (so the fp16 cache rows
 // are the same bits), and the V^T rows of those positions as
 // value_transpose_kernel writes them (zeros at [end, end8), end8 = end
-// rounded up to 8 within the row pitch).  One workgroup per 64 aligned
+// rounded up to 8 within the row pitch).  One workgroup per 32 aligned
 // positions, KV head and seq*layer; the tile's v rows meet in LDS and leave
 // as 16-byte chunks of 8 positions per dim row.
 struct KvAppendVtArgs {
@@ -147,7 +147,7 @@ struct KvAppendVtArgs {
 
 template <int D>
 __global__ __launch_bounds__(256) void kv_append_vt_kernel(KvAppendVtArgs a) {
-    constexpr int P = 64;
+    constexpr int P = 32;  // positions per workgroup (64 measured 5 % slower at 512 tokens)
     constexpr int HALF = D / 2;
     __shared__ __attribute__((aligned(16))) f16 tile[P][D + 8];
     const int first = a.base;
@@ -326,7 +326,7 @@ te_status launch_kv_append_vt(const float *k, const float *v, const float *k_bia
     a.ctx = (int)context_tokens;
     a.ctx_pad = (int)ctx_pad;
     a.kv_heads = (int)kv_heads;
-    const size_t tiles = ((size_t)a.end8 - (base_position & ~(size_t)63) + 63) / 64;
+    const size_t tiles = ((size_t)a.end8 - (base_position & ~(size_t)31) + 31) / 32;
     const dim3 grid((unsigned)tiles, (unsigned)kv_heads, (unsigned)sl_count);
     if (head_dim == 128) {
         kv_append_vt_kernel<128><<<grid, 256, 0, stream>>>(a);
