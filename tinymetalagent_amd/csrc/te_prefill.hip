@@ -753,13 +753,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float *part_o,
 //   vt[((sl*kv + h)*D + i)*ctx_pad + p] = v[((sl*ctx + p)*kv + h)*D + i],
 // and zeros at [end, end8) (end8 = end rounded up to 8, at most ctx_pad), so
 // the 8-key chunks the attention kernel reads past a sequence's end are
-// finite.  One workgroup per 64 aligned positions, kv head and seq*layer:
+// finite.  One workgroup per 32 aligned positions, kv head and seq*layer:
 // the rows come in as whole 16-byte chunks into LDS, the dim rows go out as
 // 16-byte chunks of 8 positions (single halves at the range's edges).
 template <int D>
 __global__ __launch_bounds__(256) void value_transpose_kernel(const f16 *v, f16 *vt, int first, int end, int end8,
                                                               int ctx, int ctx_pad, int kv_heads) {
-    constexpr int P = 64;
+    constexpr int P = 32;
     constexpr int CPR = D / 8;
     __shared__ __attribute__((aligned(16))) f16 tile[P][D + 8];
     const int p0 = (first & ~(P - 1)) + P * (int)blockIdx.x;
@@ -822,7 +822,7 @@ te_status launch_value_transpose(const f16 *v, f16 *vt, size_t sl_count, size_t 
     if (end8 <= first) {
         return TE_STATUS_OK;
     }
-    const size_t tiles = (end8 - (first & ~(size_t)63) + 63) / 64;
+    const size_t tiles = (end8 - (first & ~(size_t)31) + 31) / 32;
     const dim3 grid((unsigned)tiles, (unsigned)kv_heads, (unsigned)sl_count);
     if (head_dim == 128) {
         value_transpose_kernel<128><<<grid, 256, 0, stream>>>(v, vt, (int)first, (int)end, (int)end8,
