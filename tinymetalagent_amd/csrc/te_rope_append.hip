@@ -44,6 +44,50 @@ struct RopeAppendArgs {
     int base[TE_HIP_MAX_SEQS];
 };
 
+// VEC consecutive values of a row: one 16-byte access for VEC = 4.
+template <int VEC>
+__device__ __forceinline__ void load_vec(const float *p, float (&x)[VEC]) {
+    if constexpr (VEC == 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(p);
+        x[0] = t.x;
+        x[1] = t.y;
+        x[2] = t.z;
+        x[3] = t.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            x[j] = p[j];
+        }
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_vec(float *p, const float (&x)[VEC]) {
+    if constexpr (VEC == 4) {
+        *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            p[j] = x[j];
+        }
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_vec_f16(f16 *p, const float (&x)[VEC]) {
+    if constexpr (VEC == 4) {
+        *reinterpret_cast<f16x4 *>(p) = f16x4{(f16)x[0], (f16)x[1], (f16)x[2], (f16)x[3]};
+    } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            p[j] = (f16)x[j];
+        }
+    }
+}
+
+// Item = VEC consecutive rotation pairs (q, k) or VEC consecutive values (v)
+// of one token; the operations per element are the same for every VEC.
+template <int VEC>
 __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
     const int item = blockIdx.x * blockDim.x + threadIdx.x;
     const int b = blockIdx.y;
@@ -51,6 +95,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
     const int s = sl / a.layers;
     const int layer = sl - s * a.layers;
     const int half = a.head_dim >> 1;
+    const int hq = half / VEC;  // items per head
     const int pos = a.base[s] + b;
     const int hidden = a.heads * a.head_dim;
     const int kv_dim = a.kv_heads * a.head_dim;
@@ -58,64 +103,103 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeAppendArgs a) {
     const float *sin_row = a.sin_t + (size_t)pos * half;
     const size_t tok = (size_t)sl * a.tokens + b;
 
-    if (a.q != nullptr && item < a.heads * half) {
-        const int head = item / half;
-        const int i = item - head * half;
+    // one rotation of VEC pairs (x0 + bias, x1 + bias) at dims i .. and i + half ..
+    auto rotate = [&](const float *row, const float *bias, int off, int i, float (&lo)[VEC], float (&hi)[VEC]) {
+        float x0[VEC], x1[VEC], cs[VEC], sn[VEC];
+        load_vec<VEC>(row + off, x0);
+        load_vec<VEC>(row + off + half, x1);
+        if (bias != nullptr) {
+            float b0[VEC], b1[VEC];
+            load_vec<VEC>(bias + off, b0);
+            load_vec<VEC>(bias + off + half, b1);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                x0[j] = x0[j] + b0[j];
+                x1[j] = x1[j] + b1[j];
+            }
+        }
+        load_vec<VEC>(cos_row + i, cs);
+        load_vec<VEC>(sin_row + i, sn);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            lo[j] = x0[j] * cs[j] - x1[j] * sn[j];
+            hi[j] = x1[j] * cs[j] + x0[j] * sn[j];
+        }
+    };
+
+    if (a.q != nullptr && item < a.heads * hq) {
+        const int head = item / hq;
+        const int i = VEC * (item - head * hq);
         const int off = head * a.head_dim + i;
         float *qrow = a.q + tok * hidden;
-        float x0 = qrow[off];
-        float x1 = qrow[off + half];
-        if (a.q_bias != nullptr) {
-            x0 = x0 + a.q_bias[(size_t)layer * hidden + off];
-            x1 = x1 + a.q_bias[(size_t)layer * hidden + off + half];
-        }
-        const float c = cos_row[i];
-        const float sn = sin_row[i];
-        const float lo = x0 * c - x1 * sn;
-        const float hi = x1 * c + x0 * sn;
-        qrow[off] = lo;
-        qrow[off + half] = hi;
+        float lo[VEC], hi[VEC];
+        rotate(qrow, a.q_bias != nullptr ? a.q_bias + (size_t)layer * hidden : nullptr, off, i, lo, hi);
+        store_vec<VEC>(qrow + off, lo);
+        store_vec<VEC>(qrow + off + half, hi);
         if (a.q_half != nullptr) {
-            a.q_half[tok * hidden + off] = (f16)lo;
-            a.q_half[tok * hidden + off + half] = (f16)hi;
+            store_vec_f16<VEC>(a.q_half + tok * hidden + off, lo);
+            store_vec_f16<VEC>(a.q_half + tok * hidden + off + half, hi);
         }
     }
 
     const size_t slot = ((size_t)sl * a.ctx + pos) * kv_dim;
-    if (item < a.kv_heads * half) {
-        const int head = item / half;
-        const int i = item - head * half;
+    if (item < a.kv_heads * hq) {
+        const int head = item / hq;
+        const int i = VEC * (item - head * hq);
         const int off = head * a.head_dim + i;
         float *krow = a.k + tok * kv_dim;
-        float x0 = krow[off];
-        float x1 = krow[off + half];
-        if (a.k_bias != nullptr) {
-            x0 = x0 + a.k_bias[(size_t)layer * kv_dim + off];
-            x1 = x1 + a.k_bias[(size_t)layer * kv_dim + off + half];
-        }
-        const float c = cos_row[i];
-        const float sn = sin_row[i];
-        const float lo = x0 * c - x1 * sn;
-        const float hi = x1 * c + x0 * sn;
+        float lo[VEC], hi[VEC];
+        rotate(krow, a.k_bias != nullptr ? a.k_bias + (size_t)layer * kv_dim : nullptr, off, i, lo, hi);
         if (a.write_back) {
-            krow[off] = lo;
-            krow[off + half] = hi;
+            store_vec<VEC>(krow + off, lo);
+            store_vec<VEC>(krow + off + half, hi);
         }
-        a.key_cache[slot + off] = (f16)lo;
-        a.key_cache[slot + off + half] = (f16)hi;
+        store_vec_f16<VEC>(a.key_cache + slot + off, lo);
+        store_vec_f16<VEC>(a.key_cache + slot + off + half, hi);
     }
 
-    if (item < kv_dim) {
+    if (item < kv_dim / VEC) {
+        const int off = VEC * item;
         float *vrow = a.v + tok * kv_dim;
-        float x = vrow[item];
+        float x[VEC];
+        load_vec<VEC>(vrow + off, x);
         if (a.v_bias != nullptr) {
-            x = x + a.v_bias[(size_t)layer * kv_dim + item];
+            float bv[VEC];
+            load_vec<VEC>(a.v_bias + (size_t)layer * kv_dim + off, bv);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                x[j] = x[j] + bv[j];
+            }
             if (a.write_back) {
-                vrow[item] = x;
+                store_vec<VEC>(vrow + off, x);
             }
         }
-        a.value_cache[slot + item] = (f16)x;
+        store_vec_f16<VEC>(a.value_cache + slot + off, x);
     }
+}
+
+// The kernel's vector width: 4 when every row piece it touches is 16-byte
+// aligned (fp32) / 8-byte aligned (fp16), else 1.
+int rope_append_vec(const RopeAppendArgs &a) {
+    auto al = [](const void *p, uintptr_t n) { return p == nullptr || ((uintptr_t)p % n) == 0; };
+    const bool ok = a.head_dim % 8 == 0 && al(a.q, 16) && al(a.k, 16) && al(a.v, 16) && al(a.q_bias, 16) &&
+                    al(a.k_bias, 16) && al(a.v_bias, 16) && al(a.cos_t, 16) && al(a.sin_t, 16) &&
+                    al(a.key_cache, 8) && al(a.value_cache, 8) && al(a.q_half, 8);
+    return ok ? 4 : 1;
+}
+
+te_status launch_rope_append(const RopeAppendArgs &a, size_t seqs, size_t layers, size_t tokens, hipStream_t st) {
+    const int vec = rope_append_vec(a);
+    const size_t half = (size_t)a.head_dim / 2;
+    size_t items = (a.q != nullptr ? (size_t)a.heads : 0) * half;
+    items = std::max(items, (size_t)a.kv_heads * a.head_dim) / (size_t)vec;
+    const dim3 grid((unsigned)((items + 255) / 256), (unsigned)tokens, (unsigned)(seqs * layers));
+    if (vec == 4) {
+        rope_kv_append_kernel<4><<<grid, 256, 0, st>>>(a);
+    } else {
+        rope_kv_append_kernel<1><<<grid, 256, 0, st>>>(a);
+    }
+    return te_hip::launch_status();
 }
 
 // Fused prefill step's append and V^T in one launch: for the chunk's
@@ -293,10 +377,7 @@ te_status launch_kv_append(const float *k, const float *v, const float *k_bias, 
     for (size_t s = 0; s < seqs; ++s) {
         a.base[s] = (int)base_position;
     }
-    const size_t items = kv_heads * head_dim;
-    const dim3 grid((unsigned)((items + 255) / 256), (unsigned)tokens, (unsigned)(seqs * layers));
-    rope_kv_append_kernel<<<grid, 256, 0, stream>>>(a);
-    return launch_status();
+    return launch_rope_append(a, seqs, layers, tokens, stream);
 }
 
 te_status launch_kv_append_vt(const float *k, const float *v, const float *k_bias, const float *v_bias,
@@ -390,12 +471,5 @@ extern "C" te_status te_hip_rope_kv_append_f16(
     a.heads = (int)heads;
     a.kv_heads = (int)kv_heads;
     a.head_dim = (int)head_dim;
-    const size_t half = head_dim / 2;
-    size_t items = heads * half;
-    if (kv_heads * head_dim > items) {
-        items = kv_heads * head_dim;
-    }
-    const dim3 grid((unsigned)((items + 255) / 256), (unsigned)tokens, (unsigned)(seqs * layers));
-    rope_kv_append_kernel<<<grid, 256, 0, te_hip::as_stream(stream)>>>(a);
-    return te_hip::launch_status();
+    return launch_rope_append(a, seqs, layers, tokens, te_hip::as_stream(stream));
 }
