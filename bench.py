@@ -84,6 +84,11 @@ def parse_args():
                         "and exit")
     p.add_argument("--prefill-gemm", action="store_true",
                    help="only the prefill GEMM cases (3B gate and down, 512 rows, Q4_0); print their JSON and exit")
+    p.add_argument("--phases", action="store_true",
+                   help="only the prefill phase table: load the phase-instrumented library "
+                        "(python -m tinymetalagent_amd.build --phases), run the causal prefill at 3B L=4096 and "
+                        "L=2048 and a 1.5B 2K chunk after 128K, print per-step shader-clock cycles per phase as "
+                        "JSON and exit")
     p.add_argument("--generate", action="store_true",
                    help="only the end-to-end te_generate_raw case on a 3B-shaped GGUF (Q4_0 and Q8_0); print its "
                         "JSON and exit")
@@ -877,8 +882,72 @@ def measured_traffic(ctx_len: int):
     return int(m.group(1)) if m else None
 
 
+PHASE_NAMES = ["step start (DMA plan, clamped loads)", "QK^T (with the next step's DMA pieces)", "softmax",
+               "PV", "-", "DMA wait", "barrier", "merge (per tile)", "steps", "prologue"]
+
+
+def phase_table() -> dict:
+    """Per-phase shader-clock cycles of prefill_causal_f16_kernel<128>, from the
+    -DTE_PREFILL_PHASES build: every wave sums s_memtime deltas per phase of
+    its step loop; reported as the mean over waves, per step (the merge and
+    the prologue as totals per wave)."""
+    import ctypes
+
+    import torch
+
+    from tinymetalagent_amd import attention as A
+    from tinymetalagent_amd import build as B
+    from tinymetalagent_amd import runtime as R
+
+    lib = R.load_library()
+    if not hasattr(lib, "te_hip_prefill_phase_log_set"):
+        raise SystemExit("bench.py --phases: set TINYENGINE_LIBRARY to the phases build "
+                         f"({B.PHASE_LIBRARY}; python -m tinymetalagent_amd.build --phases)")
+    waves, nph = 8, len(PHASE_NAMES)
+    out = {}
+    for (h, kv, d, L, base) in [(16, 2, 128, 4096, 0), (16, 2, 128, 2048, 0), (12, 2, 128, 2048, 131072)]:
+        ctx = base + L
+        g = torch.Generator(device="cuda").manual_seed(1)
+        kc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+        vc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+        qh = torch.randn((1, 1, L, h, d), generator=g, device="cuda").half()
+        vt = A.value_t_buffer(1, 1, ctx, kv, d)
+        A.value_transpose(vc, vt)
+        o = torch.empty((1, 1, L, h, d), device="cuda")
+        log = torch.zeros(4096 * waves * nph, dtype=torch.int32, device="cuda")
+        for _ in range(3):
+            A.attention_prefill_vt(qh, kc, vt, base_position=base, out=o)
+        torch.cuda.synchronize()
+        lib.te_hip_prefill_phase_log_set(ctypes.c_void_p(log.data_ptr()))
+        A.attention_prefill_vt(qh, kc, vt, base_position=base, out=o)
+        torch.cuda.synchronize()
+        lib.te_hip_prefill_phase_log_set(ctypes.c_void_p(0))
+        x = log.view(-1, waves, nph).cpu().numpy().astype("float64")
+        x = x[x[:, :, 8].sum(axis=1) > 0]
+        steps = float(x[:, :, 8].mean())
+        case = {"workgroups": int(x.shape[0]), "steps_per_wave": round(steps, 1),
+                "cycles_per_wave": round(float(x[:, :, [0, 1, 2, 3, 5, 6, 7, 9]].sum(axis=2).mean()))}
+        for i, nm in enumerate(PHASE_NAMES):
+            if i in (4, 8):
+                continue
+            if i in (7, 9):
+                case[nm + " (per wave, total)"] = round(float(x[:, :, i].mean()))
+            else:
+                case[nm] = round(float(x[:, :, i].mean()) / max(steps, 1.0))
+        out[f"H{h}_L{L}_base{base}"] = case
+        del kc, vc, qh, vt, o
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse_args()
+    if args.phases:
+        from tinymetalagent_amd import build as B
+
+        os.environ["TINYENGINE_LIBRARY"] = str(B.PHASE_LIBRARY)
+        print(json.dumps({"prefill_phases_cycles": phase_table()}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "Run with --gpus 1.", file=sys.stderr)

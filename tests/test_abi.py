@@ -83,6 +83,52 @@ def test_defaults_and_capabilities():
     assert lib.te_make_kernel_plan(ctypes.byref(o), ctypes.byref(plan)) == runtime.TE_STATUS_UNSUPPORTED
 
 
+# Reference c/src/tinyengine.c:36-83 (te_quant_name) and :85-118 (te_vector_op_name),
+# in enum order (c/include/tinyengine.h:46-87); out-of-range values print the default.
+REFERENCE_QUANT_NAMES = [
+    "UNKNOWN", "F32", "F16", "BF16", "GGUF_Q4_0", "GGUF_Q4_1", "GGUF_Q5_0", "GGUF_Q5_1", "GGUF_Q8_0",
+    "GGUF_Q2_K", "GGUF_Q3_K", "GGUF_Q4_K", "GGUF_Q5_K", "GGUF_Q6_K", "GGUF_Q8_K", "GGUF_IQ2_XXS",
+    "GGUF_IQ2_XS", "GGUF_IQ3_XXS", "GGUF_IQ3_S", "GGUF_IQ4_NL", "GGUF_IQ4_XS", "MXFP4",
+]
+REFERENCE_OP_NAMES = [
+    "matvec", "matmul", "batched-prefill", "decode-token", "rmsnorm", "rope", "causal-attention",
+    "swiglu", "residual-add", "argmax", "sampling", "kv-cache", "tokenize",
+]
+
+
+def test_quant_and_op_names_match_reference(lib):
+    lib.te_quant_name.restype = ctypes.c_char_p
+    lib.te_quant_name.argtypes = [ctypes.c_int]
+    lib.te_vector_op_name.restype = ctypes.c_char_p
+    lib.te_vector_op_name.argtypes = [ctypes.c_int]
+    assert [lib.te_quant_name(i).decode() for i in range(22)] == REFERENCE_QUANT_NAMES
+    for bad in (22, 99, -1):  # TE_QUANT_COUNT and out of range: the reference's default
+        assert lib.te_quant_name(bad).decode() == "UNKNOWN"
+    assert [lib.te_vector_op_name(i).decode() for i in range(13)] == REFERENCE_OP_NAMES
+    for bad in (13, 99, -1):
+        assert lib.te_vector_op_name(bad).decode() == "unknown"
+
+
+def test_kernel_plan_defaults_match_reference(lib):
+    """Reference tinyengine.c:201-235: NULL options mean te_default_options(),
+    ABI version 0 is accepted, a NULL plan is an invalid argument."""
+    from tinymetalagent_amd import runtime
+
+    plan = runtime._KernelPlan()
+    assert lib.te_make_kernel_plan(None, ctypes.byref(plan)) == runtime.TE_STATUS_OK
+    assert plan.abi_version == 3 and plan.max_context_tokens == 512  # the default options' context
+    o = runtime._RuntimeOptions(abi_version=0, context_tokens=4096)
+    assert lib.te_make_kernel_plan(ctypes.byref(o), ctypes.byref(plan)) == runtime.TE_STATUS_OK
+    assert plan.abi_version == 3 and plan.max_context_tokens == 4096
+    assert lib.te_make_kernel_plan(ctypes.byref(o), None) == runtime.TE_STATUS_INVALID_ARGUMENT
+    # te_compile_kernels (reference :237-246): the plan is required, the options are not
+    assert lib.te_compile_kernels(None, None) == runtime.TE_STATUS_INVALID_ARGUMENT
+    bad = runtime._KernelPlan()
+    ctypes.memmove(ctypes.byref(bad), ctypes.byref(plan), ctypes.sizeof(plan))
+    bad.abi_version = 2
+    assert lib.te_compile_kernels(None, ctypes.byref(bad)) == runtime.TE_STATUS_UNSUPPORTED
+
+
 def test_public_attention_argument_checks(lib):
     f = np.ones(64, np.float32)
     p = f.ctypes.data_as(ctypes.POINTER(ctypes.c_float))

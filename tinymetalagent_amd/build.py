@@ -91,7 +91,9 @@ def build(verbose: bool = False) -> Path:
     if failed:
         raise RuntimeError(f"compilation failed: {', '.join(failed)}")
     tmp = LIBRARY.with_suffix(".so.tmp")
-    link = [hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", *map(str, objs), "-o", str(tmp)]
+    # -z defs: an unresolved symbol (e.g. a kernel stub the host pass did not
+    # emit) fails the link here instead of the first dlopen.
+    link = [hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", "-Wl,-z,defs", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(link), flush=True)
     subprocess.run(link, check=True)
@@ -156,8 +158,44 @@ def build_sanitized(verbose: bool = False) -> Path:
     return SAN_LIBRARY
 
 
+# Phase-instrumented build (profiling only): te_prefill.hip with
+# -DTE_PREFILL_PHASES (the causal prefill kernel sums shader-clock cycles per
+# phase of its step loop into a log set by te_hip_prefill_phase_log_set),
+# linked with the other objects of the normal build.  bench.py --phases runs
+# it and prints the phase table.
+PHASE_BUILD = PKG / "_build_phases"
+PHASE_LIBRARY = PHASE_BUILD / "libtinyengine_phases.so"
+
+
+def build_phases(verbose: bool = False) -> Path:
+    """Build libtinyengine_phases.so (needs the objects of build() for the rest)."""
+    hipcc = _hipcc()
+    PHASE_BUILD.mkdir(exist_ok=True)
+    objs = []
+    for src in HIP_SOURCES:
+        if src == "te_prefill.hip":
+            obj = PHASE_BUILD / "te_prefill.o"
+            cmd = [hipcc, *HIP_FLAGS, *HIP_SOURCE_FLAGS.get(src, []), "-DTE_PREFILL_PHASES", f"-I{INCLUDE}",
+                   f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        else:
+            obj = BUILD / (Path(src).stem + ".o")
+            if not obj.is_file():
+                raise RuntimeError(f"{obj} missing: run build() first")
+        objs.append(obj)
+    objs += [BUILD / (Path(src).stem + ".o") for src in C_SOURCES]
+    link = [hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", "-Wl,-z,defs", *map(str, objs), "-o",
+            str(PHASE_LIBRARY)]
+    subprocess.run(link, check=True)
+    return PHASE_LIBRARY
+
+
 if __name__ == "__main__":
-    if "--sanitize" in sys.argv:
+    if "--phases" in sys.argv:
+        print(build_phases(verbose="-v" in sys.argv))
+    elif "--sanitize" in sys.argv:
         print(build_sanitized(verbose="-v" in sys.argv))
     else:
         print(build(verbose="-v" in sys.argv))

@@ -44,16 +44,20 @@ const char *te_strerror(te_status status) {
     }
 }
 
+/* Names as the reference prints them (tinyengine.c:36-83): the GGUF block
+ * formats carry their "GGUF_" prefix, anything else is "UNKNOWN". */
 const char *te_quant_name(te_quant_kind quant) {
     static const char *const names[TE_QUANT_COUNT] = {
-        "unknown", "F32", "F16", "BF16", "Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q2_K", "Q3_K",
-        "Q4_K", "Q5_K", "Q6_K", "Q8_K", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS", "MXFP4"};
+        "UNKNOWN", "F32", "F16", "BF16", "GGUF_Q4_0", "GGUF_Q4_1", "GGUF_Q5_0", "GGUF_Q5_1", "GGUF_Q8_0",
+        "GGUF_Q2_K", "GGUF_Q3_K", "GGUF_Q4_K", "GGUF_Q5_K", "GGUF_Q6_K", "GGUF_Q8_K", "GGUF_IQ2_XXS",
+        "GGUF_IQ2_XS", "GGUF_IQ3_XXS", "GGUF_IQ3_S", "GGUF_IQ4_NL", "GGUF_IQ4_XS", "MXFP4"};
     if ((int)quant < 0 || quant >= TE_QUANT_COUNT) {
-        return "unknown";
+        return "UNKNOWN";
     }
     return names[quant];
 }
 
+/* Names as the reference prints them (tinyengine.c:85-118). */
 const char *te_vector_op_name(te_vector_op op) {
     static const char *const names[TE_OP_COUNT] = {
         "matvec", "matmul", "batched-prefill", "decode-token", "rmsnorm", "rope", "causal-attention",
@@ -128,31 +132,49 @@ te_status te_get_capabilities(te_capabilities *out_capabilities) {
     return TE_STATUS_OK;
 }
 
+/* Reference tinyengine.c:201-235: NULL options mean te_default_options(),
+ * ABI version 0 is accepted as "current", TE_ARCH_AUTO resolves through
+ * te_detect_arch.  The masks and sizes describe this library's kernels. */
 te_status te_make_kernel_plan(const te_runtime_options *options, te_kernel_plan *out_plan) {
-    if (options == NULL || out_plan == NULL) {
+    const te_runtime_options effective = options != NULL ? *options : te_default_options();
+    if (out_plan == NULL) {
         return TE_STATUS_INVALID_ARGUMENT;
     }
-    if (options->abi_version != TE_ABI_VERSION) {
+    if (effective.abi_version != 0u && effective.abi_version != TE_ABI_VERSION) {
         return TE_STATUS_UNSUPPORTED;
+    }
+    te_arch_kind arch = effective.target_arch;
+    if (arch == TE_ARCH_AUTO) {
+        te_arch_info info;
+        const te_status status = te_detect_arch(&info);
+        if (status != TE_STATUS_OK) {
+            return status;
+        }
+        arch = info.kind;
     }
     memset(out_plan, 0, sizeof(*out_plan));
     out_plan->abi_version = TE_ABI_VERSION;
-    out_plan->target_arch = TE_ARCH_AMD_GFX950;
+    out_plan->target_arch = arch;
     out_plan->quant_mask[0] = te_hip_quant_mask();
     out_plan->optimized_quant_mask[0] = te_hip_quant_mask();
     out_plan->vector_op_mask = te_hip_op_mask();
     out_plan->optimization_flags = TE_OPT_ARCH_SPECIALIZED | TE_OPT_GPU_RESIDENT_KV | TE_OPT_BATCHED_PREFILL;
     out_plan->dot_threads = 64u; /* wavefront width */
     out_plan->preferred_alignment_bytes = 256u;
-    out_plan->max_context_tokens = options->context_tokens != 0u ? options->context_tokens : 512u;
-    out_plan->memory_budget_bytes = options->memory_limit_bytes;
+    out_plan->max_context_tokens = effective.context_tokens != 0u ? effective.context_tokens : 512u;
+    out_plan->memory_budget_bytes = effective.memory_limit_bytes;
     snprintf(out_plan->metal_function_suffix, sizeof(out_plan->metal_function_suffix), "%s", "_gfx950");
     return TE_STATUS_OK;
 }
 
+/* Reference tinyengine.c:237-246: the plan is required, the options are not. */
 te_status te_compile_kernels(const te_runtime_options *options, const te_kernel_plan *plan) {
-    if (options == NULL || plan == NULL) {
+    (void)options;
+    if (plan == NULL) {
         return TE_STATUS_INVALID_ARGUMENT;
+    }
+    if (plan->abi_version != TE_ABI_VERSION) {
+        return TE_STATUS_UNSUPPORTED;
     }
     /* Kernels are compiled ahead of time for gfx950. */
     return te_hip_available() ? TE_STATUS_OK : TE_STATUS_UNSUPPORTED;

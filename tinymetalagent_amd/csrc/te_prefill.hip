@@ -97,7 +97,27 @@ struct PrefillArgs {
     int splits;      // key splits: blockIdx.z = (seq*layers + layer) * splits + split
     float *part_o;   // splits > 1: unnormalised O per (split, seq*layer, row, head), else null
     float *part_ml;  // splits > 1: (m, l) per (split, seq*layer, row, head)
+#ifdef TE_PREFILL_PHASES
+    unsigned *phase_log;  // [workgroup][wave][kPhases]: shader-clock cycles per phase, summed
+#endif
 };
+
+// Phase instrumentation (a build with -DTE_PREFILL_PHASES only, see
+// build.py --phases and bench.py --phases): each wave sums s_memtime deltas
+// per phase of the step loop and writes them when it ends.
+#ifdef TE_PREFILL_PHASES
+constexpr int kPhases = 10;  // step start, QK^T, softmax, PV, -, DMA wait, barrier, merge, steps, prologue
+#define TE_PHASE(i)                                                 \
+    do {                                                            \
+        const unsigned t_ = (unsigned)__builtin_amdgcn_s_memtime(); \
+        ph[i] += t_ - t_last;                                       \
+        t_last = t_;                                                \
+    } while (0)
+#else
+#define TE_PHASE(i) \
+    do {            \
+    } while (0)
+#endif
 
 // Fused prefill step: query row `row` of (sl, layer) for head h, bias + RoPE at
 // its position, rounded to the fp16 Q^T operand -- the operation order of
@@ -192,6 +212,14 @@ struct VtHalf {
     static constexpr int LOADS = BYTES / 1024;
 };
 
+// Where a step issues the next step's DMA pieces (see dma_piece in the kernel).
+struct DmaPlan {
+    unsigned char *stage;  // the next step's staging buffer
+    bool live;             // false: every piece goes to the sink
+    int ksoff;             // scalar source offsets of the K and V^T pieces
+    int vsoff;
+};
+
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
     typedef KHalf<D> KH;
@@ -211,6 +239,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     // make those reads wait for the DMA (vmcnt).
     __shared__ __attribute__((aligned(1024))) unsigned char st0[STAGE];
     __shared__ __attribute__((aligned(1024))) unsigned char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) unsigned char dma_sink[1024];  // target of idle DMA slots
 
     // Work unit of this workgroup.  Units are ordered pair-fastest, then the
     // heads of one KV group, then KV head, then (seq*layer, split); the
@@ -239,6 +268,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     const int half = wave >> 2;  // key half: blocks 2*step + half
     const int g = lane >> 4;
     const int c = lane & 15;
+#ifdef TE_PREFILL_PHASES
+    unsigned ph[kPhases] = {};
+    unsigned t_last = (unsigned)__builtin_amdgcn_s_memtime();
+#endif
     const int long_tile = a.paired ? a.n_qtiles - 1 - pair : pair;
     // odd tile count: the middle tile has no partner; unpaired units are one tile
     const int n_tiles_wg = !a.paired || pair == long_tile ? 1 : 2;
@@ -330,6 +363,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                                                      (__attribute__((address_space(3))) void *)stage_dst(stage, i),
                                                      16, off, 0, 0, 0);
         }
+    };
+    // The fast-path DMA of the next step, one piece per QK^T batch of the
+    // current one: the CU's vector memory path takes ~16 cycles per 1 KB
+    // piece, and the 64 pieces of a step issued back to back at its start
+    // held every wave until the last was accepted.  A plan that is not
+    // `live` (no next step, or one staged by the clamping path) sends every
+    // slot to dma_sink with zero offsets, so the instruction stream is the
+    // same for every step.
+    auto dma_piece = [&](const DmaPlan &d, int i) __attribute__((always_inline)) {
+        unsigned char *dst = d.live ? stage_dst(d.stage, i) : dma_sink;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(i < NKL ? krsrc : vrsrc, (__attribute__((address_space(3))) void *)dst,
+                                                 16, (int)ld_off[i], i < NKL ? d.ksoff : d.vsoff, 0, 0);
     };
     auto stage_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0): this wave's loads are in LDS
 
@@ -442,8 +487,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         // MASK: a diagonal block (some key beyond some row's position); the
         // interior variant carries no mask code, so nothing splits the QK^T
         // MFMAs from the softmax into separate scheduling regions.
-        auto compute = [&](auto mask_tag, int kb0, const unsigned char *lk, const unsigned char *lv)
-                           __attribute__((always_inline)) {
+        auto compute = [&](auto mask_tag, int kb0, const unsigned char *lk, const unsigned char *lv,
+                           const DmaPlan &dma) __attribute__((always_inline)) {
             constexpr bool MASK = decltype(mask_tag)::value;
             // ---- S^T = K Q^T, tiles 0-1 (keys 0-31) then 2-3 (keys 32-63):
             // batch b = (key half b / KK, k-step b % KK) is two K operand reads
@@ -466,10 +511,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             for (int b = 0; b < kQkAhead; ++b) {
                 kread(b);
             }
+            static_assert(QB == LOADS, "one DMA piece per QK^T batch");
 #pragma unroll
             for (int b = 0; b < QB; ++b) {
                 const int hk = b / KK;
                 const int kk = b % KK;
+                dma_piece(dma, b);
                 if (b + kQkAhead < QB) {
                     kread(b + kQkAhead);
                 }
@@ -519,6 +566,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                     mxh[hk][nb] = m;
                 }
             }
+            TE_PHASE(1);
             f16x8 vbuf[2 * NT];
             auto vread = [&](int b) __attribute__((always_inline)) {
                 vbuf[b] = *reinterpret_cast<const f16x8 *>(lv + v_off[b / NT] + (b % NT) * 16 * VH::ROWB);
@@ -573,6 +621,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                 }
                 l[nb] = psum;
             }
+            TE_PHASE(2);
             // ---- O^T += V^T P^T: tile t (dims 16t .. 16t+15), k-step ks: lane
             // (c, g) reads dim 16t + c, keys 32 ks + 8g .. +7; the first
             // kPvAhead reads are issued before the softmax above and each
@@ -596,21 +645,47 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             constexpr int B = decltype(tag)::value;
             const unsigned char *cur = B == 0 ? st0 : st1;
             unsigned char *nxt = B == 0 ? st1 : st0;
+            // The step staged during this one: the tile's next step, or (on
+            // st1's last step) the next tile's first, in flight across the
+            // merge.  One that reaches past its tile's last key goes through
+            // the clamping path here; a full one is issued piece by piece
+            // inside compute (or here, when this wave has nothing to compute).
+            int next = -1, next_kmax = 0;
             if (j + 1 < cnt) {
-                stage_load(lo + j + 1, kmax, nxt);
+                next = lo + j + 1;
+                next_kmax = kmax;
             } else if (B == 1 && cnt_next > 0) {
-                stage_load(lo_next, tile_kmax(pair), nxt);  // the next tile's first step, in flight across the merge
+                next = lo_next;
+                next_kmax = tile_kmax(pair);
             }
+            const bool next_fast = next >= 0 && next * 2 * BN + 2 * BN - 1 <= next_kmax;
+            if (next >= 0 && !next_fast) {
+                stage_load(next, next_kmax, nxt);
+            }
+            DmaPlan dma;
+            dma.stage = nxt;
+            dma.live = next_fast;
+            dma.ksoff = next_fast ? next * 2 * BN * (int)row_stride * 2 : 0;
+            dma.vsoff = next_fast ? next * 2 * BN * 2 : 0;
+            TE_PHASE(0);
             const int kb0 = (2 * (lo + j) + half) * BN;
             if (j < cnt && wave_active && kb0 <= wave_max_pos) {
                 if (kb0 + BN - 1 > wave_min_pos) {
-                    compute(std::true_type(), kb0, cur + half * KB, cur + 2 * KB + half * VB);  // diagonal block
+                    compute(std::true_type(), kb0, cur + half * KB, cur + 2 * KB + half * VB, dma);  // diagonal block
                 } else {
-                    compute(std::false_type(), kb0, cur + half * KB, cur + 2 * KB + half * VB);
+                    compute(std::false_type(), kb0, cur + half * KB, cur + 2 * KB + half * VB, dma);
                 }
+            } else if (next_fast) {
+                stage_load(next, next_kmax, nxt);
             }
+            TE_PHASE(3);
             stage_wait();
+            TE_PHASE(5);
             __syncthreads();
+            TE_PHASE(6);
+#ifdef TE_PREFILL_PHASES
+            ph[8] += 1;
+#endif
         };
         if (ti == 0 || !first_staged) {
             // The kernel's first step (and a step staged after an empty key
@@ -620,6 +695,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             // stay in flight.
             stage_wait();
             __syncthreads();
+        }
+        if (ti == 0) {
+            TE_PHASE(9);
         }
         for (int j = 0; j < cnt; j += 2) {
             body(std::integral_constant<int, 0>(), j);
@@ -703,6 +781,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             finish(o[1], mref[1], l[1], 1);
         }
         lds_barrier();  // exchange reads finish before st1 is staged again
+        TE_PHASE(7);
         if (cnt == 0 && cnt_next > 0) {
             // Nothing of this tile was staged (an empty key range of the
             // split), so st0 is free; staged after the merge, so no LDS DMA
@@ -710,6 +789,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             stage_load(lo_next, tile_kmax(pair), st0);
         }
     }
+#ifdef TE_PREFILL_PHASES
+    if (a.phase_log != nullptr && lane == 0) {
+        const unsigned wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        for (int i = 0; i < kPhases; ++i) {
+            a.phase_log[(wg * kWaves + wave) * kPhases + i] = ph[i];
+        }
+    }
+#endif
 }
 
 // Key-split merge: out[row][h] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s
@@ -844,6 +931,10 @@ bool prefill_paired(size_t seqs, size_t layers, size_t tokens, size_t heads, int
     return n_qtiles * heads * seqs * layers * (size_t)splits > (size_t)te_hip::device_compute_units();
 }
 
+#ifdef TE_PREFILL_PHASES
+unsigned *g_phase_log = nullptr;
+#endif
+
 te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t tokens, size_t base_position,
                          size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim, hipStream_t strm) {
     a.layers = (int)layers;
@@ -860,6 +951,9 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
         a.splits = 1;
     }
     a.paired = prefill_paired(seqs, layers, tokens, heads, a.splits) ? 1 : 0;
+#ifdef TE_PREFILL_PHASES
+    a.phase_log = g_phase_log;
+#endif
     const int n_units_x = a.paired ? (a.n_qtiles + 1) / 2 : a.n_qtiles;
     const dim3 grid((unsigned)n_units_x, (unsigned)heads, (unsigned)(seqs * layers * a.splits));
     if (head_dim == 128) {
@@ -985,6 +1079,12 @@ int splits_for(void *workspace, size_t workspace_bytes, size_t seqs, size_t laye
 }
 
 }  // namespace
+
+#ifdef TE_PREFILL_PHASES
+// Phase log of the next prefill launches ([workgroup][wave][10] unsigned, see
+// kPhases); a build with -DTE_PREFILL_PHASES only.
+extern "C" void te_hip_prefill_phase_log_set(unsigned *device_log) { g_phase_log = device_log; }
+#endif
 
 extern "C" size_t te_hip_value_t_bytes(size_t seqs, size_t layers, size_t context_tokens, size_t kv_heads,
                                        size_t head_dim) {
