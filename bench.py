@@ -787,8 +787,10 @@ def write_3b_gguf(path: str, ggml_type: int, *, layers=36, heads=16, kv_heads=2,
 def generate_case(ggml_type: int, prompt_tokens: int = 512, new_tokens: int = 128, ctx: int = 1024) -> dict:
     """End-to-end te_generate_raw on a 3B-shaped GGUF through the public C ABI
     (the reference's own entry point, qwen.c:261-400): load, a prompt of
-    `prompt_tokens` byte tokens processed token by token, then greedy decode
-    with every token streamed to the callback.  Times: load (parse + upload of
+    `prompt_tokens` byte tokens through the batched prefill (int8-MFMA prompt
+    GEMMs and causal attention over 512-row chunks,
+    te_hip_prefill_all_layers_f16), then greedy decode with every token
+    streamed to the callback.  Times: load (parse + upload of
     the file to HBM on first use), prompt (to the first generated token) and
     decode (tokens after the first, per second)."""
     import ctypes
@@ -882,8 +884,8 @@ def measured_traffic(ctx_len: int):
     return int(m.group(1)) if m else None
 
 
-PHASE_NAMES = ["step start (DMA plan, clamped loads)", "QK^T (with the next step's DMA pieces)", "softmax",
-               "PV", "-", "DMA wait", "barrier", "merge (per tile)", "steps", "prologue"]
+PHASE_NAMES = ["step start (DMA plan, clamped loads)", "QK^T + weights (with the next step's DMA pieces)", "-",
+               "reference checks + PV", "-", "DMA wait", "barrier", "merge", "steps", "prologue"]
 
 
 def phase_table() -> dict:
@@ -926,9 +928,10 @@ def phase_table() -> dict:
         x = x[x[:, :, 8].sum(axis=1) > 0]
         steps = float(x[:, :, 8].mean())
         case = {"workgroups": int(x.shape[0]), "steps_per_wave": round(steps, 1),
-                "cycles_per_wave": round(float(x[:, :, [0, 1, 2, 3, 5, 6, 7, 9]].sum(axis=2).mean()))}
+                "cycles_per_wave": round(float(x[:, :, [i for i, nm in enumerate(PHASE_NAMES) if nm not in ("-", "steps")]]
+                                         .sum(axis=2).mean()))}
         for i, nm in enumerate(PHASE_NAMES):
-            if i in (4, 8):
+            if nm in ("-", "steps"):
                 continue
             if i in (7, 9):
                 case[nm + " (per wave, total)"] = round(float(x[:, :, i].mean()))
@@ -1118,7 +1121,8 @@ def main():
         # generation through the public C ABI on a 3B-shaped GGUF
         line["generate"] = {
             "workload": "te_generate_raw on a Qwen2.5-3B-shaped GGUF (random weights, 151936-token byte-level "
-                        "vocabulary): 512 prompt tokens token by token, then 128 greedy tokens; ctx 1024",
+                        "vocabulary): 512 prompt tokens through the batched int8-MFMA prefill (512-row chunks), "
+                        "then 128 greedy tokens; ctx 1024",
             "q4_0": generate_case(2),
             "prefill_gemm_gate_q4_0": gemm_case(torch, 2, 512, 11008, 2048, pre=1),
             "prefill_gemm_down_q4_0": gemm_case(torch, 2, 512, 2048, 11008, pre=2),

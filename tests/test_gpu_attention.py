@@ -782,6 +782,120 @@ def test_prefill_step_vt_matches_plain_step(seqs, layers, h, kv, d, tokens, base
     assert err <= TOL
 
 
+def _off16(t):
+    """A contiguous copy of t whose data pointer is one element past 16-byte alignment."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    view = buf[1:].view(t.shape)
+    view.copy_(t)
+    assert view.data_ptr() % 16 != 0
+    return view
+
+
+def test_prefill_step_vt_misaligned_kv_rows():
+    """k_new / v_new one float off 16-byte alignment: the fused V^T step takes
+    the element-wise append and the chunk's transpose instead of the 16-byte
+    kernel, with the same cache, V^T and output bits as aligned rows.  A query,
+    cache, V^T or output off alignment is refused (UNSUPPORTED), as is a
+    misaligned value cache in te_hip_value_transpose_f16."""
+    seqs, layers, h, kv, d, tokens, base = 1, 2, 16, 2, 128, 200, 37
+    ctx = base + tokens + 3
+    g = torch.Generator(device=DEV).manual_seed(11)
+    q = torch.randn((seqs, layers, tokens, h, d), generator=g, device=DEV) / math.sqrt(d)
+    k = torch.randn((seqs, layers, tokens, kv, d), generator=g, device=DEV)
+    v = torch.randn((seqs, layers, tokens, kv, d), generator=g, device=DEV)
+    qb = torch.randn((layers, h * d), generator=g, device=DEV) * 0.1
+    kb = torch.randn((layers, kv * d), generator=g, device=DEV) * 0.1
+    vb = torch.randn((layers, kv * d), generator=g, device=DEV) * 0.1
+    kc0 = torch.randn((seqs, layers, ctx, kv, d), generator=g, device=DEV).half()
+    vc0 = torch.randn((seqs, layers, ctx, kv, d), generator=g, device=DEV).half()
+    cos, sin = A.rope_table(ctx, d, 1e6)
+
+    def run(kk, vv):
+        kc, vc = kc0.clone(), vc0.clone()
+        vt = A.value_t_buffer(seqs, layers, ctx, kv, d)
+        A.value_transpose(vc, vt, first_position=0, count=base)
+        out = A.prefill_step_vt(q, kk, vv, cos, sin, kc, vc, vt, base_position=base, q_bias=qb, k_bias=kb,
+                                v_bias=vb)
+        torch.cuda.synchronize()
+        return kc, vc, vt, out
+
+    ref = run(k, v)
+    got = run(_off16(k), _off16(v))
+    for x, y in zip(ref[:3], got[:3]):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    assert torch.equal(ref[3], got[3])
+
+    kc, vc = kc0.clone(), vc0.clone()
+    vt = A.value_t_buffer(seqs, layers, ctx, kv, d)
+    with pytest.raises(R.TinyEngineError, match="unsupported"):
+        A.prefill_step_vt(_off16(q), k, v, cos, sin, kc, vc, vt, base_position=base)
+    with pytest.raises(R.TinyEngineError, match="unsupported"):
+        A.prefill_step_vt(q, k, v, cos, sin, kc, vc, vt, base_position=base, out=_off16(torch.empty_like(q)))
+    qh = q.half()
+    with pytest.raises(R.TinyEngineError, match="unsupported"):
+        A.attention_prefill_vt(qh, _off16(kc), vt, base_position=base)
+    with pytest.raises(R.TinyEngineError, match="unsupported"):
+        A.attention_prefill(_off16(qh), kc, vc, base_position=base)
+    with pytest.raises(R.TinyEngineError, match="unsupported"):
+        A.value_transpose(_off16(vc), vt, first_position=0, count=base)
+
+
+@pytest.mark.parametrize("tokens,base", [(300, 0), (130, 203), (1, 5)])
+def test_prefill_vt_ignores_positions_past_rounded_end(oracle_mod, tokens, base):
+    """V^T positions at and past base + tokens rounded up to 8 are never read
+    as values.  V^T is filled with fp16 NaN (0x7E00) before the writers run
+    (te_hip_value_transpose_f16 and the fused step write the positions up to
+    the end and zeros up to the next multiple of 8); the outputs, with one
+    split and with the key split, are finite, match the oracle and equal the
+    outputs over a zero-filled V^T."""
+    h, kv, d = 16, 2, 128
+    end = base + tokens
+    ctx = end + 40
+    tag = f"nanvt{tokens}{base}"
+    kc = S.to_f16_bits(S.normal(47, tag + "k", (1, 1, ctx, kv, d)))
+    vc = S.to_f16_bits(S.normal(47, tag + "v", (1, 1, ctx, kv, d)))
+    q16 = S.to_f16_bits(S.normal(47, tag + "q", (1, 1, tokens, h, d)))
+    qd, kd, vd = f16_dev(q16), f16_dev(kc), f16_dev(vc)
+    vt_nan = A.value_t_buffer(1, 1, ctx, kv, d)
+    vt_nan.view(torch.int16).fill_(0x7E00)
+    A.value_transpose(vd, vt_nan, first_position=0, count=end)
+    end8 = (end + 7) // 8 * 8
+    assert torch.isnan(vt_nan[..., end8:]).all() and not torch.isnan(vt_nan[..., :end8]).any()
+    vt_zero = A.value_t_buffer(1, 1, ctx, kv, d)
+    A.value_transpose(vd, vt_zero, first_position=0, count=end)
+    ws = A.prefill_vt_workspace(1, 1, tokens, h, kv, d, base_position=base, context_tokens=ctx)
+    want = oracle_mod.attention_prefill(S.f16_bits_to_f32(q16[0, 0]).reshape(tokens, h, d), kc[0, 0].copy(),
+                                        vc[0, 0].copy(), tokens, base, ctx, h, kv, d).reshape(tokens, h, d)
+    one = A.attention_prefill_vt(qd, kd, vt_nan, base_position=base)
+    split = A.attention_prefill_vt(qd, kd, vt_nan, base_position=base, workspace=ws)
+    zero = A.attention_prefill_vt(qd, kd, vt_zero, base_position=base)
+    torch.cuda.synchronize()
+    assert torch.isfinite(one).all() and torch.isfinite(split).all()
+    assert torch.equal(one, zero)
+    err = max(maxabs(one.cpu().numpy()[0, 0], want), maxabs(split.cpu().numpy()[0, 0], want))
+
+    # the fused step over a NaN-filled V^T holding only the cached prefix
+    g = torch.Generator(device=DEV).manual_seed(tokens + base)
+    qf = torch.randn((1, 1, tokens, h, d), generator=g, device=DEV) / math.sqrt(d)
+    kf = torch.randn((1, 1, tokens, kv, d), generator=g, device=DEV)
+    vf = torch.randn((1, 1, tokens, kv, d), generator=g, device=DEV)
+    cos, sin = A.rope_table(ctx, d, 1e6)
+    outs = []
+    for fill, work in ((0x7E00, None), (0x7E00, ws), (0, None)):
+        kc2, vc2 = kd.clone(), vd.clone()
+        vt2 = A.value_t_buffer(1, 1, ctx, kv, d)
+        vt2.view(torch.int16).fill_(fill)
+        A.value_transpose(vc2, vt2, first_position=0, count=base)
+        outs.append(A.prefill_step_vt(qf, kf, vf, cos, sin, kc2, vc2, vt2, base_position=base, workspace=work))
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(o).all() for o in outs)
+    assert torch.equal(outs[0], outs[2])
+    err_step = float((outs[1] - outs[2]).abs().max())
+    print(f"NaN past the rounded V^T end, L{tokens} base{base}: max abs err {err:.3e} (oracle), "
+          f"fused step split vs one split {err_step:.3e}")
+    assert err <= TOL and err_step <= TOL
+
+
 @pytest.mark.parametrize("growth", [0.0, 0.02, 0.1, 0.2])
 def test_prefill_rising_scores_rescale(oracle_mod, growth):
     """Scores that keep rising along the keys (key p scaled by 1 + growth * p /

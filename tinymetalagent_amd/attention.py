@@ -276,10 +276,15 @@ def prefill_step_vt(query, k_new, v_new, rope_cos, rope_sin, key_cache, value_ca
 
 def prefill_workspace(seqs: int, layers: int, tokens: int, heads: int, kv_heads: int, head_dim: int, *,
                       base_position: int = 0, context_tokens: int, device="cuda") -> torch.Tensor | None:
-    """Workspace for attention_prefill_split (None when the launch does not split)."""
+    """Workspace for attention_prefill_split: the key-split partials (none when
+    the launch does not split) plus a V^T of the whole prefix, which the split
+    entry rebuilds on every call -- so it is never None.  Chunked prefill over
+    a long cache should keep a V^T buffer and use the *_vt entries instead."""
     n = load_library().te_hip_attention_prefill_workspace_bytes(seqs, layers, tokens, base_position, context_tokens,
                                                                 heads, kv_heads, head_dim)
-    return None if n == 0 else torch.empty(n, dtype=torch.uint8, device=device)
+    if n == 0:
+        raise TinyEngineError("invalid argument")
+    return torch.empty(n, dtype=torch.uint8, device=device)
 
 
 def attention_prefill_split(q_half, key_cache, value_cache, *, base_position: int = 0, out: torch.Tensor | None = None,

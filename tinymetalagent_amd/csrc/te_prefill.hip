@@ -43,12 +43,18 @@
 // The DMA writes 1 KB per wave instruction with lane l at +16 l; each lane's
 // global source is the chunk its slot holds.
 //
-// Softmax: fp32, base 2.  The row maximum is taken on raw scores; p =
-// exp2(s*qscale - m_ref) with one FMA.  m_ref is only raised (and O, l
-// rescaled) when a row's maximum exceeds it by more than 2^kLazyLog2, so the
-// rescale is skipped in almost every block; O/l is exact for any m_ref >= the
-// true maximum minus kLazyLog2 (P stays <= 2^kLazyLog2, fine for fp16).
-// Q and P are single fp16 operands (the rotated q is already fp16 here).
+// Softmax: fp32, base 2, per 32-key half of a block.  The weights are
+// p = exp2(fma(s, qscale, -m_ref)) with qscale = log2(e)/sqrt(D) applied in
+// fp32 to the raw score (the fp16 query is the operand as given, rounded
+// once), against a per-row reference m_ref that is only raised (and O, l
+// rescaled) when a row's maximum exceeds it by more than kLazyLog2 (log2
+// units).  No row maximum is taken in the common case: a lane's fp16 weights
+// are summed for l anyway, and while that sum stays <= 2^kLazyLog2 no weight
+// exceeds 2^kLazyLog2, so m_ref is within kLazyLog2 of the maximum and O/l is
+// exact.  A larger (or non-finite: the row's first keys, m_ref = -inf) sum
+// sends the wave through the exact path: the half's row maxima, the new
+// reference, the rescale and the weights again.  Q and P are single fp16
+// operands.
 //
 // Work per (seq, layer): 2*heads*D*sum_t(base+t+1) MACs (QK^T + PV); the
 // roofline unit is that count x2 FLOP.
@@ -68,6 +74,7 @@ constexpr int BN = 64;    // keys per block
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr float kLazyLog2 = 8.0f;
+constexpr float kLazyMax = 256.0f;  // 2^kLazyLog2: the largest lane sum of one half's weights taken as is
 constexpr int kMaxPrefillSplits = 32;
 constexpr int kVtAlign = 64;  // V^T rows are padded to a multiple of this many positions
 constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dispatched to them round-robin
@@ -106,7 +113,7 @@ struct PrefillArgs {
 // build.py --phases and bench.py --phases): each wave sums s_memtime deltas
 // per phase of the step loop and writes them when it ends.
 #ifdef TE_PREFILL_PHASES
-constexpr int kPhases = 10;  // step start, QK^T, softmax, PV, -, DMA wait, barrier, merge, steps, prologue
+constexpr int kPhases = 10;  // step start, QK^T + weights, -, checks + PV, -, DMA wait, barrier, merge, steps, prologue
 #define TE_PHASE(i)                                                 \
     do {                                                            \
         const unsigned t_ = (unsigned)__builtin_amdgcn_s_memtime(); \
@@ -403,8 +410,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     // Q^T operand for the wave's two 16-row blocks.  fp16 queries are loaded
     // raw (load_q16) before they are needed: the first tile's with its first
     // K/V step, the second tile's right after the first tile's last step, so
-    // that load overlaps the merge; prep_q then scales them (and the fused
-    // step loads, rotates and scales its fp32 queries there).
+    // that load overlaps the merge; prep_q then zeroes rows past the end (and
+    // the fused step loads and rotates its fp32 queries there).
     f16x8 qop[2][KK];
     auto load_q16 = [&](int qt) __attribute__((always_inline)) {
 #pragma unroll
@@ -425,14 +432,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             if (a.q32 != nullptr) {
                 load_q_rope<D>(a, sl, sl % a.layers, h, ok ? row : 0, g, qop[nb]);
             }
-            // The softmax scale log2(e)/sqrt(D) rides in the operand: q' =
-            // fp16(q * qscale), so S^T comes out in log2 units and p =
-            // exp2(s - m_ref) needs no multiply.
+            // rows past the end: zero operands (finite scores, never stored)
+            if (!ok) {
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    qop[nb][kk][j] = ok ? (f16)((float)qop[nb][kk][j] * qs) : (f16)0.0f;
+                for (int kk = 0; kk < KK; ++kk) {
+                    qop[nb][kk] = f16x8{};
                 }
             }
         }
@@ -465,10 +469,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         prep_q(qt);
 
         float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
-        // QK^T accumulators start at -m_ref (0 while m_ref is -inf), so the
-        // MFMA results are already s - m_ref: one tile per row block, the
-        // lane's row in all four elements.
-        f32x4 negm[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
         float l[2] = {0.0f, 0.0f};               // per-lane partial row sums
         f32x4 o[2][NT];
 #pragma unroll
@@ -494,11 +494,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             // batch b = (key half b / KK, k-step b % KK) is two K operand reads
             // (tiles 2hk, 2hk+1) and four MFMAs; the reads run kQkAhead batches
             // ahead of their MFMAs so LDS latency hides under the MFMAs, and
-            // the row maximum of the first half is taken while the second
-            // half's MFMAs run ----
+            // the first half's weights are computed while the second half's
+            // MFMAs run ----
             constexpr int QB = 2 * KK;
             f32x4 s[4][2];
-            float mxh[2][2];  // [key half][row block]
+            f16x8 pb[2][2];     // [key half = PV k-step][row block]: keys 32 hk + 8 g + j
+            float psum[2][2];   // [key half][row block]: the lane's sum of those weights
             f16x8 kbuf[QB][2];
             auto kread = [&](int b) __attribute__((always_inline)) {
 #pragma unroll
@@ -506,6 +507,41 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                     kbuf[b][i] = *reinterpret_cast<const f16x8 *>(lk + k_off[b % KK] +
                                                                   (2 * (b / KK) + i) * 16 * KH::ROWB);
                 }
+            };
+            // fp16 weights of key half hk, row block nb, against the current
+            // reference (0 for every key while a row has none: m_ref = -inf
+            // only reaches here from the exact path), and their lane sum
+            auto weights = [&](int hk, int nb) __attribute__((always_inline)) {
+                const float nm = -mref[nb];
+                const bool none = mref[nb] == -INFINITY;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = fast_exp2(fmaf(s[2 * hk + (e >> 2)][nb][e & 3], qs, nm));
+                    pb[hk][nb][e] = none ? (f16)0.0f : (f16)x;
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const f16x2 pr = {pb[hk][nb][j], pb[hk][nb][j + 1]};
+                    sum = __builtin_amdgcn_fdot2(pr, f16x2{(f16)1.0f, (f16)1.0f}, sum, false);
+                }
+                psum[hk][nb] = sum;
+            };
+            // the common case: no reference test, m_ref = -inf gives inf / NaN
+            // weights and so a failing sum
+            auto weights_fast = [&](int hk, int nb) __attribute__((always_inline)) {
+                const float nm = -mref[nb];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    pb[hk][nb][e] = (f16)fast_exp2(fmaf(s[2 * hk + (e >> 2)][nb][e & 3], qs, nm));
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const f16x2 pr = {pb[hk][nb][j], pb[hk][nb][j + 1]};
+                    sum = __builtin_amdgcn_fdot2(pr, f16x2{(f16)1.0f, (f16)1.0f}, sum, false);
+                }
+                psum[hk][nb] = sum;
             };
 #pragma unroll
             for (int b = 0; b < kQkAhead; ++b) {
@@ -523,8 +559,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                 if (kk == 0) {
 #pragma unroll
                     for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
-                        s[i][0] = negm[0];
-                        s[i][1] = negm[1];
+                        s[i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        s[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                     }
                 }
 #pragma unroll
@@ -553,17 +589,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                         }
                     }
                 }
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    float m = -INFINITY;
-#pragma unroll
-                    for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            m = fmaxf(m, s[i][nb][r]);
-                        }
-                    }
-                    mxh[hk][nb] = m;
+                if (hk == 0) {
+                    weights_fast(0, 0);
+                    weights_fast(0, 1);
                 }
             }
             TE_PHASE(1);
@@ -575,64 +603,55 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             for (int b = 0; b < kPvAhead; ++b) {
                 vread(b);
             }
-            // ---- lazy online softmax per row ----
-            f16x8 pb[2][2];  // [k-step][row block]: keys 32 ks + 8 g + j
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                // row maximum of s - m_ref (of s itself while m_ref is -inf)
-                const float mx = xor_max_16_32(fmaxf(mxh[0][nb], mxh[1][nb]));
-                const bool first = mref[nb] == -INFINITY;
-                if (__any(mx > kLazyLog2 || (first && mx > -INFINITY))) {
-                    // A new reference: m_ref + mx (mx for a row's first
-                    // unmasked key).  A row that has seen no unmasked key keeps
-                    // m_ref = -inf (its l and O are still zero): a key half can
-                    // meet such rows.
-                    const bool move = first ? mx > -INFINITY : mx > kLazyLog2;
-                    const float shift = move ? mx : 0.0f;
-                    const float alpha = first ? 0.0f : fast_exp2(-shift);
-                    mref[nb] = first ? mx : mref[nb] + shift;
-                    negm[nb] = f32x4{-mref[nb], -mref[nb], -mref[nb], -mref[nb]};
-                    if (mref[nb] == -INFINITY) {
-                        negm[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
-                    l[nb] *= alpha;
+            for (int hk = 0; hk < 2; ++hk) {
+                // ---- the exact path, when a lane's weights of this half sum
+                // past 2^kLazyLog2 (or are not finite) ----
+                if (__any(!(psum[hk][0] <= kLazyMax) || !(psum[hk][1] <= kLazyMax))) {
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        o[nb][t] = o[nb][t] * alpha;
-                    }
+                    for (int nb = 0; nb < 2; ++nb) {
+                        float m = -INFINITY;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        s[i][nb] = s[i][nb] - shift;
-                    }
-                }
+                        for (int i = 2 * hk; i < 2 * hk + 2; ++i) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    pb[e >> 3][nb][e & 7] = (f16)fast_exp2(s[e >> 2][nb][e & 3]);
-                }
-                // row sum of the fp16 weights the PV product uses (v_dot2_f32_f16)
-                float psum = l[nb];
+                            for (int r = 0; r < 4; ++r) {
+                                m = fmaxf(m, s[i][nb][r]);
+                            }
+                        }
+                        // the half's row maximum in log2 units (-inf: no unmasked key)
+                        const float mx = xor_max_16_32(m) * qs;
+                        const bool first = mref[nb] == -INFINITY;
+                        const bool move = first ? mx > -INFINITY : mx - mref[nb] > kLazyLog2;
+                        const float alpha = !move ? 1.0f : first ? 0.0f : fast_exp2(mref[nb] - mx);
+                        mref[nb] = move ? mx : mref[nb];
+                        l[nb] *= alpha;
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        const f16x2 pr = {pb[ks][nb][j], pb[ks][nb][j + 1]};
-                        psum = __builtin_amdgcn_fdot2(pr, f16x2{(f16)1.0f, (f16)1.0f}, psum, false);
+                        for (int t = 0; t < NT; ++t) {
+                            o[nb][t] = o[nb][t] * alpha;
+                        }
+                        weights(hk, nb);
                     }
                 }
-                l[nb] = psum;
-            }
-            TE_PHASE(2);
-            // ---- O^T += V^T P^T: tile t (dims 16t .. 16t+15), k-step ks: lane
-            // (c, g) reads dim 16t + c, keys 32 ks + 8g .. +7; the first
-            // kPvAhead reads are issued before the softmax above and each
-            // later one kPvAhead MFMA pairs ahead ----
+                l[0] += psum[hk][0];
+                l[1] += psum[hk][1];
+                // ---- O^T += V^T P^T, k-step hk: tile t (dims 16t .. 16t+15):
+                // lane (c, g) reads dim 16t + c, keys 32 hk + 8g .. +7; the
+                // first kPvAhead reads are issued before the check above and
+                // each later one kPvAhead MFMA pairs ahead.  The second half's
+                // weights are computed under the first half's MFMAs. ----
 #pragma unroll
-            for (int b = 0; b < 2 * NT; ++b) {
-                if (b + kPvAhead < 2 * NT) {
-                    vread(b + kPvAhead);
+                for (int t = 0; t < NT; ++t) {
+                    const int b = hk * NT + t;
+                    if (b + kPvAhead < 2 * NT) {
+                        vread(b + kPvAhead);
+                    }
+                    o[0][t] = mfma16x16x32(vbuf[b], pb[hk][0], o[0][t]);
+                    o[1][t] = mfma16x16x32(vbuf[b], pb[hk][1], o[1][t]);
                 }
-                o[0][b % NT] = mfma16x16x32(vbuf[b], pb[b / NT][0], o[0][b % NT]);
-                o[1][b % NT] = mfma16x16x32(vbuf[b], pb[b / NT][1], o[1][b % NT]);
+                if (hk == 0) {
+                    weights_fast(1, 0);
+                    weights_fast(1, 1);
+                }
             }
         };
 
@@ -901,6 +920,11 @@ size_t vt_bytes(size_t seqs, size_t layers, size_t context_tokens, size_t kv_hea
     return seqs * layers * kv_heads * head_dim * vt_pitch(context_tokens) * sizeof(uint16_t);
 }
 
+// 16-byte alignment (null passes): the attention kernel's operand loads and
+// output stores and the V^T kernels' 16-byte chunks assume it of every base
+// pointer; the entry points return UNSUPPORTED for a base that lacks it.
+bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
 te_status launch_value_transpose(const f16 *v, f16 *vt, size_t sl_count, size_t first, size_t count,
                                  size_t context_tokens, size_t kv_heads, size_t head_dim, hipStream_t stream) {
     const size_t pad = vt_pitch(context_tokens);
@@ -1104,7 +1128,7 @@ extern "C" te_status te_hip_value_transpose_f16(const uint16_t *value_cache, uin
         return TE_STATUS_INVALID_ARGUMENT;
     }
     if ((head_dim != 64 && head_dim != 128) || context_tokens * kv_heads * head_dim * 2 >= ((size_t)1 << 31) ||
-        seqs * layers > 65535 || kv_heads > 65535) {
+        seqs * layers > 65535 || kv_heads > 65535 || !al16(value_cache) || !al16(value_cache_t)) {
         return TE_STATUS_UNSUPPORTED;
     }
     if (count == 0) {
@@ -1138,6 +1162,9 @@ extern "C" te_status te_hip_attention_prefill_vt_f16(
     if (st != TE_STATUS_OK) {
         return st;
     }
+    if (!al16(q_half) || !al16(key_cache) || !al16(value_cache_t) || !al16(out) || !al16(workspace)) {
+        return TE_STATUS_UNSUPPORTED;
+    }
     const int splits = splits_for(workspace, workspace_bytes, seqs, layers, tokens, base_position, heads, head_dim,
                                   &st);
     if (st != TE_STATUS_OK) {
@@ -1170,16 +1197,32 @@ extern "C" te_status te_hip_attention_prefill_step_vt_f16(
     if (seqs > TE_HIP_MAX_SEQS || tokens > 65535) {
         return TE_STATUS_UNSUPPORTED;
     }
+    if (!al16(query) || !al16(q_bias) || !al16(rope_cos) || !al16(rope_sin) || !al16(key_cache) ||
+        !al16(value_cache) || !al16(value_cache_t) || !al16(out) || !al16(workspace)) {
+        return TE_STATUS_UNSUPPORTED;
+    }
     const int splits = splits_for(workspace, workspace_bytes, seqs, layers, tokens, base_position, heads, head_dim,
                                   &st);
     if (st != TE_STATUS_OK) {
         return st;
     }
     hipStream_t strm = te_hip::as_stream(stream);
-    // bias + RoPE + fp16 append of k / v and the chunk's V^T rows: one launch
-    st = te_hip::launch_kv_append_vt(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache,
-                                     value_cache_t, seqs * layers, layers, tokens, base_position, context_tokens,
-                                     vt_pitch(context_tokens), kv_heads, head_dim, strm);
+    if (al16(k_new) && al16(v_new)) {
+        // bias + RoPE + fp16 append of k / v and the chunk's V^T rows: one launch
+        st = te_hip::launch_kv_append_vt(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache,
+                                         value_cache_t, seqs * layers, layers, tokens, base_position, context_tokens,
+                                         vt_pitch(context_tokens), kv_heads, head_dim, strm);
+    } else {
+        // k / v rows off 16-byte alignment: the append's element-wise form
+        // (the same bits), then the chunk's V^T rows from the value cache
+        st = te_hip::launch_kv_append(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache, seqs,
+                                      layers, tokens, base_position, context_tokens, kv_heads, head_dim, strm);
+        if (st == TE_STATUS_OK) {
+            st = launch_value_transpose(reinterpret_cast<const f16 *>(value_cache),
+                                        reinterpret_cast<f16 *>(value_cache_t), seqs * layers, base_position, tokens,
+                                        context_tokens, kv_heads, head_dim, strm);
+        }
+    }
     if (st != TE_STATUS_OK) {
         return st;
     }
@@ -1207,6 +1250,9 @@ extern "C" te_status te_hip_attention_prefill_f16(
     te_status st = check_prefill_args(seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim);
     if (st != TE_STATUS_OK) {
         return st;
+    }
+    if (!al16(q_half) || !al16(key_cache) || !al16(value_cache) || !al16(out)) {
+        return TE_STATUS_UNSUPPORTED;
     }
     // V^T of positions 0 .. base + tokens in a library-owned buffer: whole
     // calls are serialized on it (calls must share one stream).
@@ -1258,6 +1304,9 @@ extern "C" te_status te_hip_attention_prefill_split_f16(
     if (workspace == nullptr) {
         return TE_STATUS_INVALID_ARGUMENT;
     }
+    if (!al16(q_half) || !al16(key_cache) || !al16(value_cache) || !al16(out) || !al16(workspace)) {
+        return TE_STATUS_UNSUPPORTED;
+    }
     const int splits = prefill_splits(seqs, layers, tokens, base_position, heads, head_dim);
     const size_t part = prefill_workspace(splits, seqs, layers, tokens, heads, head_dim);
     if (workspace_bytes < part + vt_bytes(seqs, layers, context_tokens, kv_heads, head_dim)) {
@@ -1294,6 +1343,10 @@ extern "C" te_status te_hip_attention_prefill_step_f16(
         return st;
     }
     if (seqs > TE_HIP_MAX_SEQS || tokens > 65535) {
+        return TE_STATUS_UNSUPPORTED;
+    }
+    if (!al16(query) || !al16(q_bias) || !al16(rope_cos) || !al16(rope_sin) || !al16(key_cache) ||
+        !al16(value_cache) || !al16(out)) {
         return TE_STATUS_UNSUPPORTED;
     }
     std::lock_guard<std::mutex> lock(te_hip::library_mutex());

@@ -351,10 +351,20 @@ uint32_t scan_and_draw(size_t count, uint32_t k, float temperature, uint64_t *rn
     return idx[choice];
 }
 
-// Pinned host staging for the read-back, grown on demand, one per thread.
+// Pinned host staging for the read-back, grown on demand, one per thread and
+// released when the thread ends (a thread's thread_local objects are
+// destroyed before the process's static objects, so the runtime is still up).
 struct HostStage {
     void *p = nullptr;
     size_t bytes = 0;
+    HostStage() = default;
+    HostStage(const HostStage &) = delete;
+    HostStage &operator=(const HostStage &) = delete;
+    ~HostStage() {
+        if (p != nullptr) {
+            (void)hipHostFree(p);
+        }
+    }
     unsigned char *get(size_t need) {
         if (need > bytes) {
             if (p != nullptr) {
