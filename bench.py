@@ -572,7 +572,16 @@ def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, rep
             want = oracle.attention_decode_f16kv(qf[t].reshape(1, 1, heads, d).copy(), kb, vb, None,
                                                  bases[-1] + t, 1, 1, ctx, heads, kv, d)
             worst = max(worst, float(np.abs(got[t] - want.reshape(heads, d)).max()))
-        res["check"] = dict(max_abs_err=worst, rows=len(check_rows))
+        # every row against the split-K decode kernel at its position (the
+        # same fp16 queries; that kernel is checked against the oracle)
+        dec = torch.empty((1, 1, heads, d), dtype=torch.float32, device=dev)
+        qd = qh[chunks - 1].float()
+        worst_all = torch.zeros((), dtype=torch.float32, device=dev)
+        for t in range(tokens):
+            A.attention_decode(qd[:, :, t].contiguous(), kc, vc, position=bases[-1] + t, out=dec)
+            worst_all = torch.maximum(worst_all, (dec[0, 0] - out[0, 0, t]).abs().max())
+        res["check"] = dict(max_abs_err=worst, rows=len(check_rows),
+                            max_abs_err_all_rows_vs_decode_kernel=float(worst_all), all_rows=tokens)
     res["step_ms"] = timer(step_vt, reps, warmup=2)
     res["plain_ms"] = timer(plain, reps, warmup=1)
     res["rope_append_ms"] = timer(rope, reps, warmup=1)
@@ -1061,6 +1070,10 @@ def main():
         line["prefill"]["max_abs_err_vs_reference"] = pre["check"]["max_abs_err"]
         line["prefill"]["reference_check"] = (f"{pre['check']['rows']} rows of the L=4096 output against the "
                                               "oracle's per-token decode over the fp16 cache (row t = decode at t)")
+        line["prefill"]["max_abs_err_all_rows_vs_decode_kernel"] = pre["check"][
+            "max_abs_err_all_rows_vs_decode_kernel"]
+        line["prefill"]["all_rows_check"] = (f"all {pre['check']['all_rows']} rows x 16 heads against the split-K "
+                                             "decode kernel at position t (same fp16 queries)")
     if not args.quick:
         cfgs = {}
         reps = max(10, K // 2)

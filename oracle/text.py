@@ -14,18 +14,20 @@ Only tests/ import it.
   (tests/test_model_cpu.py::test_rng_matches_reference_source); sample is
   pinned by what fixes it (top-k 1 and a vanishing temperature are argmax,
   the candidates are the k largest logits, draw frequencies follow the
-  tempered softmax).
+  tempered softmax); the temperature is a float32, as the reference holds it.
 - generate: c/src/qwen.c:261-400 (prompt, then tokens until eos / padding /
   max_tokens), each token through oracle.decode_all_layers (qwen.c:907-1087)
   on an fp16 KV cache.
 
-ref_tokenizer() wraps the reference's own tokenizer.c (oracle/_ref, built
-where the reference tree is present) for checking this restatement.
+RefTokenizer wraps the reference's own gguf.c loader and tokenizer.c
+(oracle/_ref, built where the reference tree is present) for checking this
+restatement and the product's tokenizer on the same GGUF file.
 """
 from __future__ import annotations
 
 import ctypes
 import math
+import os
 
 import numpy as np
 
@@ -169,7 +171,10 @@ def sample(logits: np.ndarray, temperature: float, k: int, state: int) -> tuple[
     k = 1 if k == 0 else min(k, 1024, logits.size)
     vals, idx = top_k(np.asarray(logits, np.float32), k)
     mx = max(vals)
-    t = float(temperature) if temperature > 1e-6 else 1e-6
+    # the reference holds the temperature as a float (qwen.c:42) and widens
+    # it after a float comparison (qwen.c:1229)
+    t32 = np.float32(temperature)
+    t = float(t32) if t32 > np.float32(1e-6) else 1e-6
     p = [math.exp((float(v) - float(mx)) / t) for v in vals]
     s = 0.0
     for e in p:
@@ -236,14 +241,15 @@ def generate(model: dict, prompt_ids: list[int], max_tokens: int, *, eos: int, p
 
 
 class RefTokenizer:
-    """The reference's tokenizer.c over a token / merge list."""
+    """The reference's tokenizer.c over a GGUF file loaded by the reference's
+    gguf.c (te_model_parse_gguf).  The library keeps gguf.c's one reference to
+    the Metal backend unresolved, so it is loaded with lazy binding; a model is
+    never released (gguf.c's release path is that reference)."""
 
-    def __init__(self, tokens: list[str], types: list[int], merges: list[str]):
-        lib = ctypes.CDLL(str(REF_TOK_LIB))
-        lib.ref_tok_create.restype = ctypes.c_void_p
-        lib.ref_tok_create.argtypes = [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int32),
-                                       ctypes.c_uint64, ctypes.POINTER(ctypes.c_char_p), ctypes.c_uint64]
-        lib.ref_tok_free.argtypes = [ctypes.c_void_p]
+    def __init__(self, path):
+        lib = ctypes.CDLL(str(REF_TOK_LIB), mode=os.RTLD_LAZY | os.RTLD_LOCAL)
+        lib.ref_tok_load.restype = ctypes.c_void_p
+        lib.ref_tok_load.argtypes = [ctypes.c_char_p]
         lib.te_model_tokenize.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int,
                                           ctypes.POINTER(ctypes.c_uint32), ctypes.c_size_t,
                                           ctypes.POINTER(ctypes.c_size_t)]
@@ -251,11 +257,8 @@ class RefTokenizer:
                                             ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t,
                                             ctypes.POINTER(ctypes.c_size_t)]
         self._lib = lib
-        t = (ctypes.c_char_p * len(tokens))(*[s.encode() for s in tokens])
-        ty = (ctypes.c_int32 * len(types))(*types)
-        m = (ctypes.c_char_p * max(len(merges), 1))(*[s.encode() for s in merges])
-        self._h = lib.ref_tok_create(t, ty, len(tokens), m, len(merges))
-        assert self._h
+        self._h = lib.ref_tok_load(str(path).encode())
+        assert self._h, f"the reference's gguf.c rejected {path}"
 
     def tokenize(self, text: bytes, parse_special: bool = True):
         cap = len(text) + 16
@@ -271,11 +274,6 @@ class RefTokenizer:
         n = ctypes.c_size_t()
         st = self._lib.te_model_detokenize(self._h, arr, len(ids), int(skip_special), buf, cap, ctypes.byref(n))
         return st, buf.raw[:n.value] if st == 0 else None
-
-    def close(self):
-        if self._h:
-            self._lib.ref_tok_free(self._h)
-            self._h = None
 
 
 def ref_tokenizer_available() -> bool:

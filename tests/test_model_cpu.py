@@ -230,7 +230,7 @@ def _texts(seed, n, specials=True):
 def test_tokenizer_parity_random_text(qwen_file):
     q = qwen_file
     orc = OT.Tokenizer(q["tokens"], q["types"], q["merges"])
-    ref = OT.RefTokenizer(q["tokens"], q["types"], q["merges"]) if OT.ref_tokenizer_available() else None
+    ref = OT.RefTokenizer(q["path"]) if OT.ref_tokenizer_available() else None
     with Model(q["path"]) as m:
         for text in _texts(11, 200):
             for special in (True, False):
@@ -246,8 +246,6 @@ def test_tokenizer_parity_random_text(qwen_file):
                         assert ref.detokenize(got, skip) == (0, back)
                 if not special or b"<|" not in text:
                     assert m.detokenize_bytes(got, False) == text  # every byte has a token: exact round trip
-    if ref is not None:
-        ref.close()
 
 
 def test_oracle_bpe_matches_independent_bpe(qwen_file):
@@ -278,12 +276,17 @@ def test_tokenizer_duplicates_and_specials(tmp_path):
     w.kv("tokenizer.ggml.merges", G.ARR, (G.STR, merges))
     path = w.write(tmp_path / "dup.gguf")
     orc = OT.Tokenizer(tokens, types, merges)
+    ref = OT.RefTokenizer(path) if OT.ref_tokenizer_available() else None
     with Model(path) as m:
         assert m.tokenize("ab") == [257] == orc.tokenize(b"ab")
         assert m.tokenize("<|a|>xab<|b") == orc.tokenize(b"<|a|>xab<|b")
         assert m.tokenize("<|a|>xab<|b")[0] == 259  # the longer special
         assert m.tokenize("<|a|>x", False) == orc.tokenize(b"<|a|>x", False)
         assert m.detokenize([259, 257]) == "ab"  # specials skipped ("<|b" is special by its prefix)
+        if ref is not None:  # the reference's loader and tokenizer on the same file
+            for text, special in ((b"ab", True), (b"<|a|>xab<|b", True), (b"<|a|>x", False)):
+                assert ref.tokenize(text, special) == (0, m.tokenize(text, special))
+            assert ref.detokenize([259, 257], True) == (0, b"ab")
 
 
 def test_sampler_restatement_pins():
