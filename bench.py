@@ -893,8 +893,9 @@ def measured_traffic(ctx_len: int):
     return int(m.group(1)) if m else None
 
 
-PHASE_NAMES = ["step start (DMA plan, clamped loads)", "QK^T + weights (with the next step's DMA pieces)", "-",
-               "reference checks + PV", "-", "DMA wait", "barrier", "merge", "steps", "prologue"]
+PHASE_NAMES = ["step start (DMA plan, clamped loads)", "QK^T + weights (with the next step's DMA pieces)",
+               "merge: to the exchange + barrier", "reference checks + PV", "merge: normalise + output stores",
+               "DMA wait", "barrier", "merge: last barrier", "steps", "prologue"]
 
 
 def phase_table() -> dict:
@@ -916,7 +917,8 @@ def phase_table() -> dict:
                          f"({B.PHASE_LIBRARY}; python -m tinymetalagent_amd.build --phases)")
     waves, nph = 8, len(PHASE_NAMES)
     out = {}
-    for (h, kv, d, L, base) in [(16, 2, 128, 4096, 0), (16, 2, 128, 2048, 0), (12, 2, 128, 2048, 131072)]:
+    for (h, kv, d, L, base) in [(16, 2, 128, 4096, 0), (16, 2, 128, 2048, 0), (16, 2, 128, 512, 0),
+                                (12, 2, 128, 2048, 131072)]:
         ctx = base + L
         g = torch.Generator(device="cuda").manual_seed(1)
         kc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
@@ -942,7 +944,7 @@ def phase_table() -> dict:
         for i, nm in enumerate(PHASE_NAMES):
             if nm in ("-", "steps"):
                 continue
-            if i in (7, 9):
+            if i in (2, 4, 7, 9):
                 case[nm + " (per wave, total)"] = round(float(x[:, :, i].mean()))
             else:
                 case[nm] = round(float(x[:, :, i].mean()) / max(steps, 1.0))

@@ -113,7 +113,7 @@ struct PrefillArgs {
 // build.py --phases and bench.py --phases): each wave sums s_memtime deltas
 // per phase of the step loop and writes them when it ends.
 #ifdef TE_PREFILL_PHASES
-constexpr int kPhases = 10;  // step start, QK^T + weights, -, checks + PV, -, DMA wait, barrier, merge, steps, prologue
+constexpr int kPhases = 10;  // step start, QK^T + weights, merge put, checks + PV, merge finish, DMA wait, barrier, merge end, steps, prologue
 #define TE_PHASE(i)                                                 \
     do {                                                            \
         const unsigned t_ = (unsigned)__builtin_amdgcn_s_memtime(); \
@@ -731,23 +731,62 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         // Wave w and wave w^4 hold the same 32 rows.  Each hands the partner
         // one 16-row block (half 0 keeps block 0, half 1 keeps block 1).  The
         // exchange uses st1, free after the last step's barrier.
+        // Per wave: the NT float4 of each lane (lane-contiguous, so one
+        // ds_write_b128 / ds_read_b128 per tile), then (m, l) per lane.
         float *xf = reinterpret_cast<float *>(st1);
         auto put = [&](const f32x4 (&ob)[NT], float m, float lsum) {
-            float *dst = xf + wave * XFER + lane;
+            f32x4 *dst = reinterpret_cast<f32x4 *>(xf + wave * XFER) + lane;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
+                dst[t * 64] = ob[t];
+            }
+            reinterpret_cast<float2 *>(xf + wave * XFER + 4 * NT * 64)[lane] = make_float2(m, lsum);
+        };
+        // The normalised rows leave through LDS: a wave writes its 16 rows
+        // row-major into the partner's slot, which only it reads and which it
+        // has just read (LDS operations of one wave stay in order), with rows
+        // padded to D + 4 floats (the 16 rows' 16-byte pieces of one write
+        // land on distinct banks), and stores them back as whole 512-byte
+        // rows, two per instruction, where the MFMA layout would give 16
+        // pieces of 64 bytes.
+        constexpr int OPITCH = D + 4;  // floats per staged output row
+        static_assert(16 * OPITCH <= XFER, "staged rows fit the exchange slot");
+        // rows = ob * w1 + po * w2 (po: the partner's block, already read)
+        auto store_rows = [&](const f32x4 (&ob)[NT], const f32x4 (&po)[NT], float w1, float w2, int nb) {
+            float *stg = xf + (wave ^ 4) * XFER;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    dst[(4 * t + r) * 64] = ob[t][r];
+            for (int t = 0; t < NT; ++t) {
+                // dims 16t + 4g + r of the lane's row
+                *reinterpret_cast<f32x4 *>(stg + c * OPITCH + 16 * t + 4 * g) = ob[t] * w1 + po[t] * w2;
+            }
+            constexpr int LPR = D / 4;  // lanes per row: 16 bytes each
+            // (the lane index is opaque here, so the row addresses are formed
+            // here rather than kept live across the step loop)
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+#pragma unroll
+            for (int i = 0; i < 16 * LPR / 64; ++i) {
+                const int r = i * (64 / LPR) + ln / LPR;
+                const int q = ln % LPR;
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(stg + r * OPITCH + 4 * q);
+                const int row = wr0 + 16 * nb + r;
+                if (row < a.tokens) {
+                    // non-temporal: the output is not read back by this launch
+                    __builtin_nontemporal_store(
+                        v, reinterpret_cast<f32x4 *>(a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D + 4 * q));
                 }
             }
-            dst[4 * NT * 64] = m;
-            dst[(4 * NT + 1) * 64] = lsum;
         };
         auto finish = [&](const f32x4 (&ob)[NT], float m, float lsum, int nb) {
-            const float *src = xf + (wave ^ 4) * XFER + lane;
-            const float m2 = src[4 * NT * 64];
-            const float l2 = src[(4 * NT + 1) * 64];
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(xf + (wave ^ 4) * XFER) + lane;
+            const float2 ml2 = reinterpret_cast<const float2 *>(xf + (wave ^ 4) * XFER + 4 * NT * 64)[lane];
+            f32x4 po[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                po[t] = src[t * 64];
+            }
+            const float m2 = ml2.x;
+            const float l2 = ml2.y;
             const float mn = fmaxf(m, m2);
             const float s1 = m == mn ? 1.0f : fast_exp2(m - mn);
             const float s2 = m2 == mn ? 1.0f : fast_exp2(m2 - mn);
@@ -760,32 +799,20 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
                     float4 v;
-                    v.x = ob[t][0] * s1 + src[(4 * t + 0) * 64] * s2;
-                    v.y = ob[t][1] * s1 + src[(4 * t + 1) * 64] * s2;
-                    v.z = ob[t][2] * s1 + src[(4 * t + 2) * 64] * s2;
-                    v.w = ob[t][3] * s1 + src[(4 * t + 3) * 64] * s2;
+                    v.x = ob[t][0] * s1 + po[t][0] * s2;
+                    v.y = ob[t][1] * s1 + po[t][1] * s2;
+                    v.z = ob[t][2] * s1 + po[t][2] * s2;
+                    v.w = ob[t][3] * s1 + po[t][3] * s2;
                     *reinterpret_cast<float4 *>(prow + 16 * t + 4 * g) = v;
                 }
                 if (g == 0) {
                     *reinterpret_cast<float2 *>(a.part_ml + 2 * pi) = make_float2(mn, ltot);
                 }
-            } else if (row < a.tokens) {
+            } else if (a.part_o == nullptr) {
                 const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
                 const float w1 = s1 * inv;
                 const float w2 = s2 * inv;
-                float *orow = a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    float4 v;
-                    v.x = ob[t][0] * w1 + src[(4 * t + 0) * 64] * w2;
-                    v.y = ob[t][1] * w1 + src[(4 * t + 1) * 64] * w2;
-                    v.z = ob[t][2] * w1 + src[(4 * t + 2) * 64] * w2;
-                    v.w = ob[t][3] * w1 + src[(4 * t + 3) * 64] * w2;
-                    // dims 16t + 4g + r; non-temporal: the output is not read
-                    // back by this launch (2-4 % faster at L = 512-2048)
-                    __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w},
-                                                reinterpret_cast<f32x4 *>(orow + 16 * t + 4 * g));
-                }
+                store_rows(ob, po, w1, w2, nb);
             }
         };
         if (half == 0) {
@@ -794,12 +821,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             put(o[0], mref[0], l[0]);
         }
         lds_barrier();
+        TE_PHASE(2);
         if (half == 0) {
             finish(o[0], mref[0], l[0], 0);
         } else {
             finish(o[1], mref[1], l[1], 1);
         }
-        lds_barrier();  // exchange reads finish before st1 is staged again
+        TE_PHASE(4);
+        lds_barrier();  // exchange and staged rows are read before st1 is staged again
         TE_PHASE(7);
         if (cnt == 0 && cnt_next > 0) {
             // Nothing of this tile was staged (an empty key range of the
