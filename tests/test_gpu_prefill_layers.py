@@ -183,3 +183,28 @@ def test_prefill_all_layers_argument_checks():
     assert call(hidden=192) == 3                   # hidden != heads * head_dim
     assert call(ggml_type=0) == 3                  # F32: not on the batched GEMM
     assert call(head_dim=32, hidden=128, kv=64) == 3
+
+
+def test_prefill_stage_profile_lines(oracle_mod, monkeypatch, capfd):
+    """TINYENGINE_METAL_PREFILL_STAGE_PROFILE (the reference's switch): one
+    stderr line per stage and layer in the reference's format, the same result
+    as without it (the stages are only synchronised)."""
+    layers = 2
+    want = _run(oracle_mod, 2, layers=layers, heads=4, kv_heads=2, head_dim=64, ffn=512, ctx=96, base=0, batch=40)
+    capfd.readouterr()
+    monkeypatch.setenv("TINYENGINE_METAL_PREFILL_STAGE_PROFILE", "1")
+    got = _run(oracle_mod, 2, layers=layers, heads=4, kv_heads=2, head_dim=64, ffn=512, ctx=96, base=0, batch=40)
+    err = capfd.readouterr().err
+    assert np.array_equal(got, want)
+    lines = [ln for ln in err.splitlines() if ln.startswith("tinyengine_metal_stage_profile: ")]
+    stages = {}
+    for ln in lines:
+        kv = dict(f.split("=", 1) for f in ln.split(": ", 1)[1].split())
+        assert kv["scope"] == "prefill_all_layers"
+        assert float(kv["gpu_ms"]) >= 0.0 and float(kv["cpu_ms"]) >= 0.0
+        stages.setdefault(int(kv["layer"]), []).append(kv["stage"])
+    assert sorted(stages) == list(range(layers))
+    assert stages[0][0] == "attn_norm_digits" and "attn_norm_digits" not in stages[1]
+    for l in range(layers):
+        assert "qkv_proj" in stages[l] and "qkv_bias_rope_flash_attention_mma_vt" in stages[l]
+        assert stages[l][-1] == ("down_proj_add_attn_norm_digits" if l + 1 < layers else "down_proj_add")

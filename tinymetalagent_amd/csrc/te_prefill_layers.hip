@@ -30,9 +30,78 @@
 // bytes in HBM at the reference's absolute tensor offsets.
 #include "te_hip_common.h"
 
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
 #include <algorithm>
+#include <chrono>
 
 namespace {
+
+// Per-stage timing of the prompt-layer flow, the reference's
+// TINYENGINE_METAL_PREFILL_STAGE_PROFILE (metal_backend_layers.mm.inc:2295-2340,
+// the switch metal_backend_runtime.mm.inc:183-186: set and not "0"): after each
+// stage the stream is synchronised and one line goes to stderr in the
+// reference's format, `tinyengine_metal_stage_profile: scope=prefill_all_layers
+// layer=L stage=S cpu_ms=C gpu_ms=G` -- G the stage's GPU time between two
+// events, C the host wait for it.  The synchronisation serialises the stages,
+// as the reference's per-stage command buffers do.
+class StageProfile {
+  public:
+    explicit StageProfile(hipStream_t st) : st_(st) {
+        const char *v = getenv("TINYENGINE_METAL_PREFILL_STAGE_PROFILE");
+        on_ = v != nullptr && strcmp(v, "0") != 0;
+        if (on_ && (hipEventCreate(&e0_) != hipSuccess || hipEventCreate(&e1_) != hipSuccess ||
+                    hipEventRecord(e0_, st_) != hipSuccess)) {
+            (void)hipGetLastError();
+            on_ = false;
+            failed_ = true;
+        }
+    }
+    ~StageProfile() {
+        if (e0_ != nullptr) {
+            (void)hipEventDestroy(e0_);
+        }
+        if (e1_ != nullptr) {
+            (void)hipEventDestroy(e1_);
+        }
+    }
+    StageProfile(const StageProfile &) = delete;
+    StageProfile &operator=(const StageProfile &) = delete;
+    bool failed() const { return failed_; }
+    // the stage that was just enqueued (no-op when off); false on a runtime error
+    bool stage(const char *name, size_t layer) {
+        if (!on_) {
+            return true;
+        }
+        using clock = std::chrono::steady_clock;
+        if (hipEventRecord(e1_, st_) != hipSuccess) {
+            return false;
+        }
+        const auto t0 = clock::now();
+        if (hipEventSynchronize(e1_) != hipSuccess) {
+            return false;
+        }
+        const double cpu_ms = std::chrono::duration<double, std::milli>(clock::now() - t0).count();
+        float gpu_ms = 0.0f;
+        if (hipEventElapsedTime(&gpu_ms, e0_, e1_) != hipSuccess) {
+            return false;
+        }
+        fprintf(stderr,
+                "tinyengine_metal_stage_profile: scope=prefill_all_layers layer=%zu stage=%s cpu_ms=%.3f "
+                "gpu_ms=%.3f\n",
+                layer, name, cpu_ms, (double)gpu_ms);
+        std::swap(e0_, e1_);  // this stage's end is the next one's start
+        return true;
+    }
+
+  private:
+    hipStream_t st_;
+    hipEvent_t e0_ = nullptr, e1_ = nullptr;
+    bool on_ = false;
+    bool failed_ = false;
+};
 
 constexpr size_t kAlign = 256;
 
@@ -140,12 +209,25 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
     const size_t ctx_kv = context_tokens * kv;
     const size_t vt_layer = te_hip_value_t_bytes(1, 1, context_tokens, kv_heads, head_dim) / sizeof(uint16_t);
     te_hip::prof_begin(st);
+    StageProfile stages(st);
+    if (stages.failed()) {
+        return TE_STATUS_RUNTIME_ERROR;
+    }
     te_status s = TE_STATUS_OK;
     for (size_t l = 0; l < layers && s == TE_STATUS_OK; ++l) {
         // each piece of the layer, then its profile mark (no-op unless profiling)
+        // and its stage line (no-op unless the stage profile is on)
+        const char *stage_name = "";
+        auto staged = [&](te_status r) {
+            if (r == TE_STATUS_OK && !stages.stage(stage_name, l)) {
+                s = TE_STATUS_RUNTIME_ERROR;
+                return false;
+            }
+            return r == TE_STATUS_OK;
+        };
         auto done = [&](te_status r, te_hip::ProfPhase p) {
             te_hip::prof_mark(st, p);
-            return r == TE_STATUS_OK;
+            return staged(r);
         };
         auto gemm = [&](const uint64_t *offs, size_t n, size_t k, float *y, const float *resid) {
             return te_hip::launch_gemm_q(m + offs[l], ggml_type, b.act, batch, n, k, y, resid, b.part, b.part_bytes,
@@ -163,6 +245,8 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
             if (glu) {
                 const te_hip::ProfShare share[2] = {{te_hip::kProfGate, 1.0}, {te_hip::kProfUp, 1.0}};
                 te_hip::prof_mark(st, share, 2);
+                stage_name = "gate_up_swiglu_pair_digits";
+                return staged(r);
             }
             return r == TE_STATUS_OK;
         };
@@ -170,32 +254,41 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
             const te_hip::ProfShare share[3] = {
                 {te_hip::kProfQ, (double)hidden}, {te_hip::kProfK, (double)kv}, {te_hip::kProfV, (double)kv}};
             te_hip::prof_mark(st, share, 3);
-            return r == TE_STATUS_OK;
+            return staged(r);
         };
         // the attention RMSNorm digits of layer l > 0 came with the previous
         // layer's down projection
-        if ((l == 0 && !done(s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights, epsilon, batch, hidden,
-                                                          b.act, st),
+        if ((l == 0 && !done((stage_name = "attn_norm_digits",
+                              s = te_hip::launch_quant_act(1, out, nullptr, attn_norm_weights, epsilon, batch, hidden,
+                                                           b.act, st)),
                              ew)) ||
-            !qkv_done(s = te_hip::launch_gemm_q_segs(ggml_type, qkv, 3, b.act, batch, hidden, b.part, b.part_bytes,
-                                                     st)) ||
-            !done(s = te_hip_attention_prefill_step_vt_f16(
-                      b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
-                      key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
-                      base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream),
+            !qkv_done((stage_name = "qkv_proj",
+                       s = te_hip::launch_gemm_q_segs(ggml_type, qkv, 3, b.act, batch, hidden, b.part, b.part_bytes,
+                                                      st))) ||
+            !done((stage_name = "qkv_bias_rope_flash_attention_mma_vt",
+                   s = te_hip_attention_prefill_step_vt_f16(
+                       b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
+                       key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
+                       base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream)),
                   te_hip::kProfAttention) ||
-            !done(s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st), ew) ||
-            !done(s = te_hip::launch_gemm_q_rms(m + output_offsets[l], ggml_type, b.act, batch, hidden, hidden, out,
-                                                out, b.part, b.part_bytes, ffn_norm_weights + l * hidden, epsilon,
-                                                b.act, st),
+            !done((stage_name = "attn_out_digits",
+                   s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st)),
+                  ew) ||
+            !done((stage_name = "output_proj_add_ffn_norm_digits",
+                   s = te_hip::launch_gemm_q_rms(m + output_offsets[l], ggml_type, b.act, batch, hidden, hidden, out,
+                                                 out, b.part, b.part_bytes, ffn_norm_weights + l * hidden, epsilon,
+                                                 b.act, st)),
                   te_hip::kProfO) ||
             !glu_done(s = te_hip::launch_gemm_glu_q(ggml_type, m + gate_offsets[l], m + up_offsets[l], b.act, batch,
                                                     ffn, hidden, b.act_ffn, st, &glu))) {
             break;
         }
-        if (!glu && (!done(s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr), te_hip::kProfGate) ||
-                     !done(s = gemm(up_offsets, ffn, hidden, b.up, nullptr), te_hip::kProfUp) ||
-                     !done(s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act_ffn, st),
+        if (!glu && (!done((stage_name = "gate_proj", s = gemm(gate_offsets, ffn, hidden, b.gate, nullptr)),
+                           te_hip::kProfGate) ||
+                     !done((stage_name = "up_proj", s = gemm(up_offsets, ffn, hidden, b.up, nullptr)),
+                           te_hip::kProfUp) ||
+                     !done((stage_name = "swiglu_digits",
+                            s = te_hip::launch_quant_act(2, b.gate, b.up, nullptr, 0.0f, batch, ffn, b.act_ffn, st)),
                            ew))) {
             break;
         }
@@ -206,6 +299,7 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
                                             b.act, st)
                 : te_hip::launch_gemm_q(m + down_offsets[l], ggml_type, b.act_ffn, batch, hidden, ffn, out, out,
                                         b.part, b.part_bytes, st);
+        stage_name = l + 1 < layers ? "down_proj_add_attn_norm_digits" : "down_proj_add";
         if (!done(s, te_hip::kProfDown)) {
             break;
         }
