@@ -442,11 +442,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
         }
     };
     // Barrier over LDS traffic only: the waves' LDS reads and writes are done
-    // and visible, while global stores (the output rows) stay in flight.
+    // and visible, while global loads and stores (the next tile's queries, the
+    // output rows) stay in flight.  A workgroup-scope fence would also wait
+    // for those (vmcnt), since the counter it must drain for the LDS DMA is
+    // the one the global accesses use; no DMA is in flight at these barriers
+    // (each step's is waited for before its step barrier).  The memory clobber
+    // keeps the compiler's LDS accesses on their side of the barrier.
     auto lds_barrier = []() __attribute__((always_inline)) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
     if (split_cnt(tile_steps(long_tile)) > 0) {
@@ -759,21 +762,42 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                 // dims 16t + 4g + r of the lane's row
                 *reinterpret_cast<f32x4 *>(stg + c * OPITCH + 16 * t + 4 * g) = ob[t] * w1 + po[t] * w2;
             }
-            constexpr int LPR = D / 4;  // lanes per row: 16 bytes each
+            constexpr int LPR = D / 4;          // lanes per row: 16 bytes each
+            constexpr int NS = 16 * LPR / 64;   // rows per lane
             // (the lane index is opaque here, so the row addresses are formed
             // here rather than kept live across the step loop)
             int ln = lane;
             asm volatile("" : "+v"(ln));
+            const int r0 = (int)((unsigned)ln / LPR);
+            const int q = (int)((unsigned)ln % LPR);
+            // every staged piece is read before the first store, so the stores
+            // wait for the LDS once
+            f32x4 v[NS];
 #pragma unroll
-            for (int i = 0; i < 16 * LPR / 64; ++i) {
-                const int r = i * (64 / LPR) + ln / LPR;
-                const int q = ln % LPR;
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(stg + r * OPITCH + 4 * q);
-                const int row = wr0 + 16 * nb + r;
-                if (row < a.tokens) {
-                    // non-temporal: the output is not read back by this launch
-                    __builtin_nontemporal_store(
-                        v, reinterpret_cast<f32x4 *>(a.out + (((size_t)sl * a.tokens + row) * a.heads + h) * D + 4 * q));
+            for (int i = 0; i < NS; ++i) {
+                v[i] = *reinterpret_cast<const f32x4 *>(stg + (i * (64 / LPR) + r0) * OPITCH + 4 * q);
+            }
+            // rows row0 + r, r = i * (64 / LPR) + r0, of this (seq*layer, head):
+            // a 32-bit float offset from the block's first row (16 rows of
+            // heads * D floats)
+            const int row0 = wr0 + 16 * nb;
+            float *orow = a.out + (((size_t)sl * a.tokens + row0) * a.heads + h) * D;
+            const unsigned rstride = (unsigned)a.heads * D;
+            // non-temporal: the output is not read back by this launch
+            if (row0 + 15 < a.tokens) {
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const unsigned off = (unsigned)(i * (64 / LPR) + r0) * rstride + 4u * (unsigned)q;
+                    __builtin_nontemporal_store(v[i], reinterpret_cast<f32x4 *>(orow + off));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const int r = i * (64 / LPR) + r0;
+                    if (row0 + r < a.tokens) {
+                        const unsigned off = (unsigned)r * rstride + 4u * (unsigned)q;
+                        __builtin_nontemporal_store(v[i], reinterpret_cast<f32x4 *>(orow + off));
+                    }
                 }
             }
         };
@@ -809,7 +833,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
                     *reinterpret_cast<float2 *>(a.part_ml + 2 * pi) = make_float2(mn, ltot);
                 }
             } else if (a.part_o == nullptr) {
-                const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+                // (v_rcp_f32: within 1 ulp; ltot >= 2^-kLazyLog2 when a key was seen)
+                const float inv = ltot > 0.0f ? __builtin_amdgcn_rcpf(ltot) : 0.0f;
                 const float w1 = s1 * inv;
                 const float w2 = s2 * inv;
                 store_rows(ob, po, w1, w2, nb);
