@@ -6,7 +6,7 @@
 // the softmax is online (base-2, exp2 of log2e-prescaled scores) per chunk and
 // merged exactly by the combine kernel; every accumulation is fp32.
 //
-// Split-K kernel, one single-wave workgroup per (chunk of positions, kv_head,
+// Split-K kernel, one single-wave workgroup per (kv_head, chunk of positions,
 // seq*layer).  The wave streams its chunk 32 positions at a time for all
 // `group` (= heads/kv_heads <= 16) query heads of its KV head at once, so every
 // K/V element is read from HBM exactly once per query token (the GQA sharing of
@@ -77,7 +77,6 @@ struct DecodeArgs {
     int chunk;
     int max_chunks;
     float qscale;    // log2(e)/sqrt(D)
-    int kv_fast;     // grid order: 1 = kv head fastest (see decode_grid)
     int positions[TE_HIP_MAX_SEQS];
 };
 
@@ -278,10 +277,12 @@ __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) 
     constexpr int NT = D / 16;  // output tiles over head_dim; also dims per lane in V loads
     constexpr int KK = D / 32;  // MFMA K-steps over head_dim for QK^T
 
-    // Grid (kv head, chunk, seq*layer) with kv_fast, else (chunk, kv head,
-    // seq*layer): see decode_grid.
-    const int kvh = a.kv_fast ? blockIdx.x : blockIdx.y;
-    const int chunk_id = a.kv_fast ? blockIdx.y : blockIdx.x;
+    // Grid (kv head, chunk, seq*layer), kv head fastest: the KV heads of one
+    // chunk are dispatched back to back, so their 256-byte halves of each
+    // cache row are read at about the same time (step at 3B / 8K / 36 layers
+    // 54.3 -> 53.4 us against chunk-fastest dispatch).
+    const int kvh = blockIdx.x;
+    const int chunk_id = blockIdx.y;
     const int sl = blockIdx.z;
     const int s = sl / a.layers;
     const int pos = a.positions[s];
@@ -698,15 +699,6 @@ DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t 
     return g;
 }
 
-// Dispatch order of the split-K grid.  With two KV heads per layer the KV
-// heads of one chunk go back to back (kv head fastest), so the two 256-byte
-// halves of each 512-byte cache row are read at about the same time: 3B at
-// 8K x 36 layers 54.3 -> 53.4 us, and faster at 2K / 32K and the 1.5B 128K
-// case.  With four, the same order puts four streams on each 1 KB row at
-// once and the 7B ragged batch ran 5 % slower (471.5 -> 495.6 us), so wider
-// KV groups keep chunk-fastest order.
-bool decode_kv_fast(size_t kv_heads) { return kv_heads <= 2; }
-
 size_t decode_workspace_bytes(const DecodeGeometry &g, size_t seqs, size_t layers, size_t heads,
                               size_t head_dim) {
     const size_t parts = seqs * layers * heads * (size_t)g.max_chunks;
@@ -857,9 +849,7 @@ te_status launch_splitk(const DecodeArgs &fused, bool is_fused, const float *que
     for (size_t s = 0; s < seqs; ++s) {
         a.positions[s] = (int)(positions != nullptr ? positions[s] : position);
     }
-    a.kv_fast = te_hip::decode_kv_fast(kv_heads) ? 1 : 0;
-    const dim3 grid = a.kv_fast ? dim3((unsigned)kv_heads, (unsigned)geo.max_chunks, (unsigned)(seqs * layers))
-                                : dim3((unsigned)geo.max_chunks, (unsigned)kv_heads, (unsigned)(seqs * layers));
+    const dim3 grid((unsigned)kv_heads, (unsigned)geo.max_chunks, (unsigned)(seqs * layers));
     hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
         if (is_fused) {
