@@ -6,7 +6,7 @@
 // the softmax is online (base-2, exp2 of log2e-prescaled scores) per chunk and
 // merged exactly by the combine kernel; every accumulation is fp32.
 //
-// Split-K kernel, one single-wave workgroup per (kv_head, chunk of positions,
+// Split-K kernel, one single-wave workgroup per (chunk of positions, kv_head,
 // seq*layer).  The wave streams its chunk 32 positions at a time for all
 // `group` (= heads/kv_heads <= 16) query heads of its KV head at once, so every
 // K/V element is read from HBM exactly once per query token (the GQA sharing of
@@ -277,12 +277,8 @@ __global__ __launch_bounds__(64, 2) void decode_splitk_f16_kernel(DecodeArgs a) 
     constexpr int NT = D / 16;  // output tiles over head_dim; also dims per lane in V loads
     constexpr int KK = D / 32;  // MFMA K-steps over head_dim for QK^T
 
-    // Grid (kv head, chunk, seq*layer), kv head fastest: the KV heads of one
-    // chunk are dispatched back to back, so their 256-byte halves of each
-    // cache row are read at about the same time (step at 3B / 8K / 36 layers
-    // 54.3 -> 53.4 us against chunk-fastest dispatch).
-    const int kvh = blockIdx.x;
-    const int chunk_id = blockIdx.y;
+    const int chunk_id = blockIdx.x;
+    const int kvh = blockIdx.y;
     const int sl = blockIdx.z;
     const int s = sl / a.layers;
     const int pos = a.positions[s];
@@ -849,7 +845,7 @@ te_status launch_splitk(const DecodeArgs &fused, bool is_fused, const float *que
     for (size_t s = 0; s < seqs; ++s) {
         a.positions[s] = (int)(positions != nullptr ? positions[s] : position);
     }
-    const dim3 grid((unsigned)kv_heads, (unsigned)geo.max_chunks, (unsigned)(seqs * layers));
+    const dim3 grid((unsigned)geo.max_chunks, (unsigned)kv_heads, (unsigned)(seqs * layers));
     hipStream_t strm = te_hip::as_stream(stream);
     if (head_dim == 128) {
         if (is_fused) {
