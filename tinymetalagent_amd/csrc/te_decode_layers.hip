@@ -82,7 +82,7 @@ extern "C" size_t te_hip_decode_all_layers_workspace_bytes(size_t position, size
     return carve(position, hidden, kv, heads, kv_heads, head_dim, ffn, vocab, nullptr, nullptr);
 }
 
-extern "C" te_status te_hip_decode_all_layers_f16(
+static te_status decode_all_layers_impl(
     const void *mapping, size_t mapping_len, const uint64_t *q_offsets, const uint64_t *k_offsets,
     const uint64_t *v_offsets, const uint64_t *output_offsets, const uint64_t *gate_offsets,
     const uint64_t *up_offsets, const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
@@ -221,4 +221,26 @@ extern "C" te_status te_hip_decode_all_layers_f16(
         }
     }
     return s;
+}
+
+extern "C" te_status te_hip_decode_all_layers_f16(
+    const void *mapping, size_t mapping_len, const uint64_t *q_offsets, const uint64_t *k_offsets,
+    const uint64_t *v_offsets, const uint64_t *output_offsets, const uint64_t *gate_offsets,
+    const uint64_t *up_offsets, const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weights, const float *ffn_norm_weights, const float *q_biases,
+    const float *k_biases, const float *v_biases, const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, size_t position, size_t context_tokens, size_t hidden, size_t kv,
+    size_t heads, size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out, uint64_t head_offset,
+    uint32_t head_ggml_type, const float *output_norm_weight, size_t vocab, uint32_t *out_token_id,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    const te_hip::BackendBucket bucket =
+        out_token_id != nullptr ? te_hip::kBucketDecodeProject : te_hip::kBucketDecodeAllLayers;
+    te_hip::BackendTimer timer(bucket, te_hip::as_stream(stream));
+    return timer.finish(decode_all_layers_impl(mapping, mapping_len, q_offsets, k_offsets, v_offsets, output_offsets,
+                                               gate_offsets, up_offsets, down_offsets, layers, ggml_type, hidden_in,
+                                               attn_norm_weights, ffn_norm_weights, q_biases, k_biases, v_biases,
+                                               rope_cos, rope_sin, key_cache, value_cache, position, context_tokens,
+                                               hidden, kv, heads, kv_heads, head_dim, ffn, epsilon, out, head_offset,
+                                               head_ggml_type, output_norm_weight, vocab, out_token_id, workspace,
+                                               workspace_bytes, stream));
 }

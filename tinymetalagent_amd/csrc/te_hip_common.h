@@ -254,4 +254,40 @@ te_status prof_flush();              // synchronise and account the recorded mar
 double prof_ms(ProfPhase phase);
 unsigned long long prof_calls(ProfPhase phase);
 
+// Backend call profile (TINYENGINE_METAL_PROFILE set and not "0", the
+// reference's switch and buckets, metal_backend_runtime.mm.inc:132-244).
+// A layer-flow entry point holds a BackendTimer over its whole call: when the
+// switch is on it records a HIP event pair around the call's launches on its
+// stream and, in finish(), waits for the second event and adds one call, the
+// host wall time and the GPU time to its bucket.  Only the outermost timer
+// of a thread records (a single-layer twin that calls the all-layers flow
+// counts as one decode_layer / prefill_layer call).  Buckets with calls are
+// printed at process exit, one line each in the reference's format.
+enum BackendBucket {
+    kBucketMatvecBatch, kBucketMatvecArgmax, kBucketQkv, kBucketQkvBatch, kBucketMlp, kBucketMlpBatch,
+    kBucketPostAttnMlp, kBucketPostAttnMlpBatch, kBucketMatvec2, kBucketMatvec, kBucketDecodeLayer,
+    kBucketDecodeAllLayers, kBucketDecodeProject, kBucketPrefillLayer, kBucketPrefillAllLayers, kBucketCount
+};
+class BackendTimer {
+  public:
+    BackendTimer(BackendBucket bucket, hipStream_t stream);
+    ~BackendTimer();
+    BackendTimer(const BackendTimer &) = delete;
+    BackendTimer &operator=(const BackendTimer &) = delete;
+    // Records the call when the switch is on and st is OK; returns st, or a
+    // runtime error when waiting for the call's launches fails.
+    te_status finish(te_status st);
+
+  private:
+    void release();
+    BackendBucket bucket_;
+    hipStream_t stream_;
+    hipEvent_t e0_ = nullptr;
+    hipEvent_t e1_ = nullptr;
+    double t0_ms_ = 0.0;
+    bool nested_ = false;
+    bool on_ = false;
+    bool done_ = false;
+};
+
 }  // namespace te_hip

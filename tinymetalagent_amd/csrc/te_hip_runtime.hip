@@ -11,8 +11,10 @@
 
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
+#include <chrono>
 #include <mutex>
 #include <vector>
 
@@ -266,6 +268,123 @@ te_status prof_flush() {
 double prof_ms(ProfPhase phase) { return t_prof.ms[phase]; }
 
 unsigned long long prof_calls(ProfPhase phase) { return t_prof.calls[phase]; }
+
+namespace {
+
+struct BackendBucketTotals {
+    const char *name;
+    unsigned long long calls;
+    double cpu_ms;
+    double gpu_ms;
+};
+
+// The reference's bucket names, in its order (metal_backend_runtime.mm.inc:
+// 134-175); this backend records the layer-flow ones.
+BackendBucketTotals g_backend_buckets[kBucketCount] = {
+    {"matvec_batch", 0, 0.0, 0.0},        {"matvec_argmax", 0, 0.0, 0.0},
+    {"qkv", 0, 0.0, 0.0},                 {"qkv_batch", 0, 0.0, 0.0},
+    {"mlp", 0, 0.0, 0.0},                 {"mlp_batch", 0, 0.0, 0.0},
+    {"post_attn_mlp", 0, 0.0, 0.0},       {"post_attn_mlp_batch", 0, 0.0, 0.0},
+    {"matvec2", 0, 0.0, 0.0},             {"matvec", 0, 0.0, 0.0},
+    {"decode_layer", 0, 0.0, 0.0},        {"decode_all_layers", 0, 0.0, 0.0},
+    {"decode_project", 0, 0.0, 0.0},      {"prefill_layer", 0, 0.0, 0.0},
+    {"prefill_all_layers", 0, 0.0, 0.0},
+};
+std::mutex g_backend_mutex;
+bool g_backend_registered = false;
+thread_local int t_backend_depth = 0;
+
+bool backend_profile_enabled() {
+    const char *v = getenv("TINYENGINE_METAL_PROFILE");
+    return v != nullptr && strcmp(v, "0") != 0;
+}
+
+double now_ms() {
+    using clock = std::chrono::steady_clock;
+    return std::chrono::duration<double, std::milli>(clock::now().time_since_epoch()).count();
+}
+
+// At exit: one line per bucket with calls, the reference's format
+// (metal_backend_runtime.mm.inc:199-217), while the switch is still set.
+void backend_profile_print() {
+    if (!backend_profile_enabled()) {
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_backend_mutex);
+    for (const BackendBucketTotals &b : g_backend_buckets) {
+        if (b.calls == 0) {
+            continue;
+        }
+        fprintf(stderr,
+                "tinyengine_metal_profile: name=%s calls=%llu cpu_ms=%.3f gpu_ms=%.3f avg_cpu_ms=%.3f "
+                "avg_gpu_ms=%.3f\n",
+                b.name, b.calls, b.cpu_ms, b.gpu_ms, b.cpu_ms / (double)b.calls, b.gpu_ms / (double)b.calls);
+    }
+}
+
+}  // namespace
+
+BackendTimer::BackendTimer(BackendBucket bucket, hipStream_t stream) : bucket_(bucket), stream_(stream) {
+    nested_ = t_backend_depth++ > 0;
+    if (nested_ || !backend_profile_enabled()) {
+        return;
+    }
+    {
+        std::lock_guard<std::mutex> lock(g_backend_mutex);
+        if (!g_backend_registered) {
+            atexit(backend_profile_print);
+            g_backend_registered = true;
+        }
+    }
+    // (the host clock starts first, so the call's GPU interval lies inside its wall time)
+    t0_ms_ = now_ms();
+    if (hipEventCreate(&e0_) != hipSuccess || hipEventCreate(&e1_) != hipSuccess ||
+        hipEventRecord(e0_, stream_) != hipSuccess) {
+        (void)hipGetLastError();  // no profile for this call; the call itself goes on
+        return;
+    }
+    on_ = true;
+}
+
+void BackendTimer::release() {
+    if (done_) {
+        return;
+    }
+    done_ = true;
+    --t_backend_depth;
+    if (e0_ != nullptr) {
+        (void)hipEventDestroy(e0_);
+    }
+    if (e1_ != nullptr) {
+        (void)hipEventDestroy(e1_);
+    }
+    e0_ = e1_ = nullptr;
+}
+
+BackendTimer::~BackendTimer() { release(); }
+
+te_status BackendTimer::finish(te_status st) {
+    if (on_ && !done_) {
+        if (hipEventRecord(e1_, stream_) != hipSuccess || hipEventSynchronize(e1_) != hipSuccess) {
+            release();
+            return st == TE_STATUS_OK ? TE_STATUS_RUNTIME_ERROR : st;
+        }
+        const double cpu_ms = now_ms() - t0_ms_;
+        float gpu_ms = 0.0f;
+        if (hipEventElapsedTime(&gpu_ms, e0_, e1_) != hipSuccess) {
+            gpu_ms = 0.0f;
+        }
+        if (st == TE_STATUS_OK) {
+            std::lock_guard<std::mutex> lock(g_backend_mutex);
+            BackendBucketTotals &b = g_backend_buckets[bucket_];
+            b.calls += 1;
+            b.cpu_ms += cpu_ms;
+            b.gpu_ms += (double)gpu_ms;
+        }
+    }
+    release();
+    return st;
+}
 
 std::mutex &library_mutex() { return g_mutex; }
 

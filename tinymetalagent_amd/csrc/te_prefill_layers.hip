@@ -149,7 +149,7 @@ extern "C" size_t te_hip_prefill_all_layers_workspace_bytes(size_t batch, size_t
     return carve(batch, hidden, kv, ffn, nullptr, nullptr);
 }
 
-extern "C" te_status te_hip_prefill_all_layers_f16(
+static te_status prefill_all_layers_impl(
     const void *mapping, size_t mapping_len, const uint64_t *q_offsets, const uint64_t *k_offsets,
     const uint64_t *v_offsets, const uint64_t *output_offsets, const uint64_t *gate_offsets,
     const uint64_t *up_offsets, const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
@@ -307,6 +307,24 @@ extern "C" te_status te_hip_prefill_all_layers_f16(
     return s;
 }
 
+extern "C" te_status te_hip_prefill_all_layers_f16(
+    const void *mapping, size_t mapping_len, const uint64_t *q_offsets, const uint64_t *k_offsets,
+    const uint64_t *v_offsets, const uint64_t *output_offsets, const uint64_t *gate_offsets,
+    const uint64_t *up_offsets, const uint64_t *down_offsets, size_t layers, uint32_t ggml_type,
+    const float *hidden_in, const float *attn_norm_weights, const float *ffn_norm_weights, const float *q_biases,
+    const float *k_biases, const float *v_biases, const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *value_cache_t, size_t base_position, size_t batch,
+    size_t context_tokens, size_t hidden, size_t kv, size_t heads, size_t kv_heads, size_t head_dim, size_t ffn,
+    float epsilon, float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    te_hip::BackendTimer timer(te_hip::kBucketPrefillAllLayers, te_hip::as_stream(stream));
+    return timer.finish(prefill_all_layers_impl(mapping, mapping_len, q_offsets, k_offsets, v_offsets, output_offsets,
+                                                gate_offsets, up_offsets, down_offsets, layers, ggml_type, hidden_in,
+                                                attn_norm_weights, ffn_norm_weights, q_biases, k_biases, v_biases,
+                                                rope_cos, rope_sin, key_cache, value_cache, value_cache_t,
+                                                base_position, batch, context_tokens, hidden, kv, heads, kv_heads,
+                                                head_dim, ffn, epsilon, out, workspace, workspace_bytes, stream));
+}
+
 // ---- single-layer twins ------------------------------------------------------
 
 extern "C" te_status te_hip_prefill_layer_f16(
@@ -317,12 +335,15 @@ extern "C" te_status te_hip_prefill_layer_f16(
     uint16_t *value_cache, uint16_t *value_cache_t, size_t base_position, size_t batch, size_t context_tokens,
     size_t hidden, size_t kv, size_t heads, size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out,
     void *workspace, size_t workspace_bytes, void *stream) {
-    return te_hip_prefill_all_layers_f16(mapping, mapping_len, &q_offset, &k_offset, &v_offset, &output_offset,
-                                         &gate_offset, &up_offset, &down_offset, 1, ggml_type, hidden_in,
-                                         attn_norm_weight, ffn_norm_weight, q_bias, k_bias, v_bias, rope_cos,
-                                         rope_sin, key_cache, value_cache, value_cache_t, base_position, batch,
-                                         context_tokens, hidden, kv, heads, kv_heads, head_dim, ffn, epsilon, out,
-                                         workspace, workspace_bytes, stream);
+    // one prefill_layer call in the backend profile (the inner flow's timer is nested)
+    te_hip::BackendTimer timer(te_hip::kBucketPrefillLayer, te_hip::as_stream(stream));
+    return timer.finish(te_hip_prefill_all_layers_f16(mapping, mapping_len, &q_offset, &k_offset, &v_offset,
+                                                      &output_offset, &gate_offset, &up_offset, &down_offset, 1,
+                                                      ggml_type, hidden_in, attn_norm_weight, ffn_norm_weight, q_bias,
+                                                      k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache,
+                                                      value_cache_t, base_position, batch, context_tokens, hidden, kv,
+                                                      heads, kv_heads, head_dim, ffn, epsilon, out, workspace,
+                                                      workspace_bytes, stream));
 }
 
 extern "C" te_status te_hip_decode_layer_f16(
@@ -333,10 +354,13 @@ extern "C" te_status te_hip_decode_layer_f16(
     uint16_t *value_cache, size_t position, size_t context_tokens, size_t hidden, size_t kv, size_t heads,
     size_t kv_heads, size_t head_dim, size_t ffn, float epsilon, float *out, void *workspace,
     size_t workspace_bytes, void *stream) {
-    return te_hip_decode_all_layers_f16(mapping, mapping_len, &q_offset, &k_offset, &v_offset, &output_offset,
-                                        &gate_offset, &up_offset, &down_offset, 1, ggml_type, hidden_in,
-                                        attn_norm_weight, ffn_norm_weight, q_bias, k_bias, v_bias, rope_cos, rope_sin,
-                                        key_cache, value_cache, position, context_tokens, hidden, kv, heads, kv_heads,
-                                        head_dim, ffn, epsilon, out, 0, 0, nullptr, 0, nullptr, workspace,
-                                        workspace_bytes, stream);
+    // one decode_layer call in the backend profile (the inner flow's timer is nested)
+    te_hip::BackendTimer timer(te_hip::kBucketDecodeLayer, te_hip::as_stream(stream));
+    return timer.finish(te_hip_decode_all_layers_f16(mapping, mapping_len, &q_offset, &k_offset, &v_offset,
+                                                     &output_offset, &gate_offset, &up_offset, &down_offset, 1,
+                                                     ggml_type, hidden_in, attn_norm_weight, ffn_norm_weight, q_bias,
+                                                     k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache,
+                                                     position, context_tokens, hidden, kv, heads, kv_heads, head_dim,
+                                                     ffn, epsilon, out, 0, 0, nullptr, 0, nullptr, workspace,
+                                                     workspace_bytes, stream));
 }
