@@ -243,30 +243,72 @@ __global__ __launch_bounds__(256) void kv_append_vt_kernel(KvAppendVtArgs a) {
     const int kv_dim = a.kv_heads * D;
     const float *kb = a.k_bias != nullptr ? a.k_bias + (size_t)layer * kv_dim + h * D : nullptr;
     const float *vb = a.v_bias != nullptr ? a.v_bias + (size_t)layer * kv_dim + h * D : nullptr;
-    // k: pairs (i, i + D/2), four per item
-    for (int idx = threadIdx.x; idx < P * (HALF / 4); idx += 256) {
+    // Every load of the workgroup is issued before the first store (the
+    // stores could alias the loads as far as the compiler knows, so loads
+    // placed after a store would wait for it): one round of memory latency.
+    // k items: pairs (i, i + D/2), four per item; v items: 8 values.  A
+    // position outside the chunk loads the chunk's first row and stores
+    // nothing (its V^T tile entry is zero).
+    constexpr int KI = P * (HALF / 4) / 256;  // k items per thread
+    constexpr int VI = P * (D / 8) / 256;     // v items per thread
+    static_assert(KI * 256 == P * (HALF / 4) && VI * 256 == P * (D / 8), "items tile the workgroup");
+    float4 k0[KI], k1[KI], c4[KI], s4[KI], kb0[KI], kb1[KI];
+    float4 v0[VI], v1[VI], vb0[VI], vb1[VI];
+#pragma unroll
+    for (int u = 0; u < KI; ++u) {
+        const int idx = threadIdx.x + 256 * u;
+        const int r = idx / (HALF / 4);
+        const int i = 4 * (idx % (HALF / 4));
+        const int p = p0 + r;
+        const int pl = p >= first && p < end ? p : first;
+        const float *krow = a.k + ((size_t)sl * a.tokens + (pl - first)) * kv_dim + h * D;
+        k0[u] = *reinterpret_cast<const float4 *>(krow + i);
+        k1[u] = *reinterpret_cast<const float4 *>(krow + i + HALF);
+        c4[u] = *reinterpret_cast<const float4 *>(a.cos_t + (size_t)pl * HALF + i);
+        s4[u] = *reinterpret_cast<const float4 *>(a.sin_t + (size_t)pl * HALF + i);
+        if (kb != nullptr) {
+            kb0[u] = *reinterpret_cast<const float4 *>(kb + i);
+            kb1[u] = *reinterpret_cast<const float4 *>(kb + i + HALF);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < VI; ++u) {
+        const int idx = threadIdx.x + 256 * u;
+        const int r = idx / (D / 8);
+        const int cq = idx % (D / 8);
+        const int p = p0 + r;
+        const int pl = p >= first && p < end ? p : first;
+        const float *vrow = a.v + ((size_t)sl * a.tokens + (pl - first)) * kv_dim + h * D + 8 * cq;
+        v0[u] = *reinterpret_cast<const float4 *>(vrow);
+        v1[u] = *reinterpret_cast<const float4 *>(vrow + 4);
+        if (vb != nullptr) {
+            vb0[u] = *reinterpret_cast<const float4 *>(vb + 8 * cq);
+            vb1[u] = *reinterpret_cast<const float4 *>(vb + 8 * cq + 4);
+        }
+    }
+    // k: bias, rotation, fp16 (rope_kv_append_kernel's operation order)
+#pragma unroll
+    for (int u = 0; u < KI; ++u) {
+        const int idx = threadIdx.x + 256 * u;
         const int r = idx / (HALF / 4);
         const int i = 4 * (idx % (HALF / 4));
         const int p = p0 + r;
         if (p < first || p >= end) {
             continue;
         }
-        const float *krow = a.k + ((size_t)sl * a.tokens + (p - first)) * kv_dim + h * D;
-        const float4 a0 = *reinterpret_cast<const float4 *>(krow + i);
-        const float4 a1 = *reinterpret_cast<const float4 *>(krow + i + HALF);
-        float x0[4] = {a0.x, a0.y, a0.z, a0.w};
-        float x1[4] = {a1.x, a1.y, a1.z, a1.w};
+        float x0[4] = {k0[u].x, k0[u].y, k0[u].z, k0[u].w};
+        float x1[4] = {k1[u].x, k1[u].y, k1[u].z, k1[u].w};
         if (kb != nullptr) {
+            const float b0[4] = {kb0[u].x, kb0[u].y, kb0[u].z, kb0[u].w};
+            const float b1[4] = {kb1[u].x, kb1[u].y, kb1[u].z, kb1[u].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                x0[j] = x0[j] + kb[i + j];
-                x1[j] = x1[j] + kb[i + j + HALF];
+                x0[j] = x0[j] + b0[j];
+                x1[j] = x1[j] + b1[j];
             }
         }
-        const float4 c4 = *reinterpret_cast<const float4 *>(a.cos_t + (size_t)p * HALF + i);
-        const float4 s4 = *reinterpret_cast<const float4 *>(a.sin_t + (size_t)p * HALF + i);
-        const float cs[4] = {c4.x, c4.y, c4.z, c4.w};
-        const float sn[4] = {s4.x, s4.y, s4.z, s4.w};
+        const float cs[4] = {c4[u].x, c4[u].y, c4[u].z, c4[u].w};
+        const float sn[4] = {s4[u].x, s4[u].y, s4[u].z, s4[u].w};
         f16x4 lo, hi;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -277,21 +319,21 @@ __global__ __launch_bounds__(256) void kv_append_vt_kernel(KvAppendVtArgs a) {
         *reinterpret_cast<f16x4 *>(dst + i) = lo;
         *reinterpret_cast<f16x4 *>(dst + i + HALF) = hi;
     }
-    // v: 8 values per item, into the cache and the LDS tile (zeros outside the chunk)
-    for (int idx = threadIdx.x; idx < P * (D / 8); idx += 256) {
+    // v: bias, fp16, into the cache and the LDS tile (zeros outside the chunk)
+#pragma unroll
+    for (int u = 0; u < VI; ++u) {
+        const int idx = threadIdx.x + 256 * u;
         const int r = idx / (D / 8);
         const int cq = idx % (D / 8);
         const int p = p0 + r;
         f16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
         if (p >= first && p < end) {
-            const float *vrow = a.v + ((size_t)sl * a.tokens + (p - first)) * kv_dim + h * D + 8 * cq;
-            const float4 b0 = *reinterpret_cast<const float4 *>(vrow);
-            const float4 b1 = *reinterpret_cast<const float4 *>(vrow + 4);
-            float x[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            float x[8] = {v0[u].x, v0[u].y, v0[u].z, v0[u].w, v1[u].x, v1[u].y, v1[u].z, v1[u].w};
             if (vb != nullptr) {
+                const float b[8] = {vb0[u].x, vb0[u].y, vb0[u].z, vb0[u].w, vb1[u].x, vb1[u].y, vb1[u].z, vb1[u].w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    x[j] = x[j] + vb[8 * cq + j];
+                    x[j] = x[j] + b[j];
                 }
             }
 #pragma unroll
