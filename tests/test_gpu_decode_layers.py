@@ -171,3 +171,43 @@ def test_decode_all_layers_q8_0_wide_down_rows(oracle_mod):
     """Q8_0 at the 3B widths: ffn_down rows of 11008 columns are 11696 bytes,
     streamed in 12 KB tiles with SwiGLU staging and the residual fused."""
     _run(oracle_mod, 8, layers=1, heads=16, kv_heads=2, head_dim=128, ffn=11008, vocab=512, ctx=32, position=9)
+
+
+@pytest.mark.parametrize("ggml_type", [2, 8])
+def test_decode_all_layers_merge_in_wo_vs_merge_launch(oracle_mod, monkeypatch, ggml_type):
+    """The attention step's merge folded into the Wo projection's staging (a
+    one-layer split of <= 12 chunks, here 12 at position 767 with 64-position
+    chunks) against TE_HIP_DECODE_MERGE_WO=0, the merge launch: both within the
+    oracle bars, and the final hidden states within 1e-4 of the largest
+    magnitude of each other (the merged attention output differs by a few ulps
+    in its rounding order)."""
+    args = dict(layers=2, heads=16, kv_heads=2, head_dim=128, ffn=512, vocab=300, ctx=800, position=767)
+    m = _run(oracle_mod, ggml_type, **args, head=False)
+    hidden = m["hidden"]
+    x = _dev(m["hidden_in"])
+    cos, sin = oracle_mod.rope_table(args["ctx"], args["head_dim"], 1.0e6)
+
+    def run_once():
+        kc, vc = _dev(m["key_cache"]), _dev(m["value_cache"])
+        got = LY.decode_all_layers(
+            _dev(m["mapping"]), m["offsets"], args["layers"], ggml_type, x, _dev(m["attn_norm"]), _dev(m["ffn_norm"]),
+            _dev(m["q_bias"]), _dev(m["k_bias"]), _dev(m["v_bias"]), _dev(cos), _dev(sin), kc, vc, args["position"],
+            args["ctx"], args["heads"], args["kv_heads"], args["head_dim"], args["ffn"], 1e-6)
+        torch.cuda.synchronize()
+        return got.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy()
+
+    fused, kc_f, vc_f = run_once()
+    monkeypatch.setenv("TE_HIP_DECODE_MERGE_WO", "0")
+    plain, kc_p, vc_p = run_once()
+    assert fused.shape == (hidden,)
+    # layer 0 appends the same k / v either way (later layers' inputs differ by the rounding)
+    assert np.array_equal(kc_f[0], kc_p[0]) and np.array_equal(vc_f[0], vc_p[0])
+    tol = 1e-4 * float(np.abs(plain).max())
+    assert float(np.abs(fused - plain).max()) <= tol
+    _run(oracle_mod, ggml_type, **args, head=False)  # the merge launch path against the oracle too
+
+
+def test_decode_all_layers_long_split_keeps_merge_launch(oracle_mod):
+    """Position 900: 15 chunks of 64 positions, past the Wo staging's 12, so
+    the step keeps its merge launch."""
+    _run(oracle_mod, 2, layers=2, heads=16, kv_heads=2, head_dim=128, ffn=512, vocab=300, ctx=960, position=900)

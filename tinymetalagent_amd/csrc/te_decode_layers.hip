@@ -28,6 +28,9 @@
 // offsets are the reference's absolute tensor offsets).
 #include "te_hip_common.h"
 
+#include <stdlib.h>
+#include <string.h>
+
 #include <algorithm>
 
 namespace {
@@ -163,6 +166,20 @@ static te_status decode_all_layers_impl(
     const te_hip::ProfShare qkv_share[3] = {
         {te_hip::kProfQ, (double)hidden}, {te_hip::kProfK, (double)kv}, {te_hip::kProfV, (double)kv}};
     const te_hip::ProfShare gu_share[2] = {{te_hip::kProfGate, 1.0}, {te_hip::kProfUp, 1.0}};
+    // The attention step's merge folds into the Wo projection's input staging
+    // (launch_gemv_merge) where the one-layer split is short: its partials,
+    // heads x chunks x (head_dim + 2) floats, are then read by every workgroup
+    // of the projection instead of by a merge launch.  TE_HIP_DECODE_MERGE_WO=0
+    // keeps the merge launch.  The workspace holds the partials as the split-K
+    // launch lays them out for one (seq, layer): o, then (m, l).
+    size_t dchunk = 0, dchunks = 0;
+    const char *merge_env = getenv("TE_HIP_DECODE_MERGE_WO");
+    const bool merge_wo = !(merge_env != nullptr && strcmp(merge_env, "0") == 0) &&
+                          te_hip_attention_decode_chunking(nullptr, position, 1, 1, kv_heads, 0, &dchunk, &dchunks) ==
+                              TE_STATUS_OK &&
+                          dchunks <= (size_t)te_hip::kGemvMergeMaxChunks;
+    const float *part_o = static_cast<const float *>(b.step_ws);
+    const float *part_ml = part_o + heads * dchunks * head_dim;
     te_status s = TE_STATUS_OK;
     for (size_t l = 0; l < layers && s == TE_STATUS_OK; ++l) {
         const te_hip::GemvSeg qkv[3] = {{m + q_offsets[l], b.q, nullptr, hidden},
@@ -175,19 +192,42 @@ static te_status decode_all_layers_impl(
         }
         prof_mark(st, qkv_share, 3);
         const size_t cache_off = l * context_tokens * kv;
-        s = te_hip_attention_decode_step_f16(b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv,
-                                             v_biases + l * kv, rope_cos, rope_sin, key_cache + cache_off,
-                                             value_cache + cache_off, nullptr, position, 1, 1, context_tokens,
-                                             heads, kv_heads, head_dim, b.attn, b.step_ws, b.step_ws_bytes, stream);
+        const te_hip::GemvSeg o = {m + output_offsets[l], out, out, hidden};
+        bool merged_in_wo = false;
+        if (merge_wo) {
+            s = te_hip_attention_decode_step_splitk_f16(b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv,
+                                                        v_biases + l * kv, rope_cos, rope_sin, key_cache + cache_off,
+                                                        value_cache + cache_off, nullptr, position, 1, 1,
+                                                        context_tokens, heads, kv_heads, head_dim, b.step_ws,
+                                                        b.step_ws_bytes, stream);
+            if (s != TE_STATUS_OK) {
+                break;
+            }
+            prof_mark(st, te_hip::kProfAttention);
+            s = te_hip::launch_gemv_merge(ggml_type, o, hidden, part_o, part_ml, dchunks, dchunks, head_dim, st,
+                                          &merged_in_wo);
+            if (s == TE_STATUS_OK && !merged_in_wo) {
+                s = te_hip_attention_decode_combine(nullptr, position, 1, 1, heads, kv_heads, head_dim, b.attn,
+                                                    b.step_ws, b.step_ws_bytes, stream);
+                prof_mark(st, te_hip::kProfAttention);
+            }
+        } else {
+            s = te_hip_attention_decode_step_f16(b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv,
+                                                 v_biases + l * kv, rope_cos, rope_sin, key_cache + cache_off,
+                                                 value_cache + cache_off, nullptr, position, 1, 1, context_tokens,
+                                                 heads, kv_heads, head_dim, b.attn, b.step_ws, b.step_ws_bytes,
+                                                 stream);
+            prof_mark(st, te_hip::kProfAttention);
+        }
         if (s != TE_STATUS_OK) {
             break;
         }
-        prof_mark(st, te_hip::kProfAttention);
-        const te_hip::GemvSeg o = {m + output_offsets[l], out, out, hidden};
-        s = te_hip::launch_gemv(ggml_type, te_hip::kGemvPlain, &o, 1, hidden, b.attn, nullptr, nullptr, 0.0f, b.xtmp,
-                                b.proj, st);
-        if (s != TE_STATUS_OK) {
-            break;
+        if (!merged_in_wo) {
+            s = te_hip::launch_gemv(ggml_type, te_hip::kGemvPlain, &o, 1, hidden, b.attn, nullptr, nullptr, 0.0f,
+                                    b.xtmp, b.proj, st);
+            if (s != TE_STATUS_OK) {
+                break;
+            }
         }
         prof_mark(st, te_hip::kProfO);
         // gate / up with the SwiGLU in their epilogue (h into b.gate) where the

@@ -190,6 +190,18 @@ te_status launch_gemv(uint32_t ggml_type, GemvPre pre, const GemvSeg *segs, int 
 te_status launch_gemv_glu(uint32_t ggml_type, const void *gate_w, const void *up_w, size_t rows, size_t cols,
                           const float *x, const float *norm_w, float eps, float *h, hipStream_t stream,
                           bool *launched);
+// One matrix against the attention output merged from one (seq, layer)'s
+// split-K partials (te_hip_attention_decode_step_splitk_f16's workspace:
+// o [heads][max_chunks][head_dim], then (m, l) [heads][max_chunks][2]) while
+// the launch stages its input: the decode step's merge launch folded into the
+// Wo projection.  *launched stays false, with OK and nothing queued, when it
+// does not apply: more than kGemvMergeMaxChunks chunks, shapes the streamed
+// kernel does not take, or an input wider than one float4 per thread; the
+// caller then runs the merge and launch_gemv.
+constexpr int kGemvMergeMaxChunks = 12;
+te_status launch_gemv_merge(uint32_t ggml_type, const GemvSeg &seg, size_t cols, const float *part_o,
+                            const float *part_ml, size_t chunks, size_t max_chunks, size_t head_dim,
+                            hipStream_t stream, bool *launched);
 
 DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t seqs, size_t layers,
                                size_t kv_heads);

@@ -34,6 +34,7 @@ constexpr int kMatvecWaves = 4;
 constexpr int kPairWaves = 12;                     // pair kernel: one 12-wave workgroup per CU (3 per SIMD)
 constexpr int kPairThreads = 64 * kPairWaves;
 constexpr int kStageBatch = 4;                      // input float4 loads in flight per thread while staging
+constexpr int kMergeChunks = te_hip::kGemvMergeMaxChunks;  // split-K partials a merge staging takes per head
 constexpr size_t kMaxPairLdsBytes = 160 * 1024;     // staged digit planes (gfx950 LDS per CU)
 constexpr size_t kPairLdsBytes = 13 * 16;           // LDS per block pair: 12 uint4 of digit planes + scales
 constexpr int kStreamChunks = 10;                   // streamed kernel: 16-byte chunk loads per lane per tile
@@ -211,14 +212,23 @@ __global__ __launch_bounds__(64 * kMatvecWaves) void matvec_kernel(const unsigne
 // it stages x * w and multiplies each row's sum by the scale, which is then
 // known, at the end (the scale is common to every element, and the staging
 // does not wait for the workgroup's reduction); kPreSwiGLU stages silu(x) * x2
-// as te_swiglu_f32 (ops.c:397-406).
-enum : int { kPreNone = 0, kPreRmsNorm = 1, kPreSwiGLU = 2 };
+// as te_swiglu_f32 (ops.c:397-406); kPreMerge stages the attention output
+// merged from its split-K partials (the decode layer's Wo projection; the sum
+// decode_merge_kernel forms, see merged_slice).
+enum : int { kPreNone = 0, kPreRmsNorm = 1, kPreSwiGLU = 2, kPreMerge = 3 };
 
 struct StageInput {
     const float *x;
     const float *x2;      // kPreSwiGLU: the up projection
     const float *norm_w;  // kPreRmsNorm: the norm weight
     float eps;            // kPreRmsNorm
+    // kPreMerge: the split-K partials of one (seq, layer), o [heads][max_chunks][head_dim]
+    // and (m, l) [heads][max_chunks][2], chunks [0, n_chunks) of each head
+    const float *part_o;
+    const float *part_ml;
+    int n_chunks;
+    int max_chunks;
+    int head_dim;
 };
 
 // The first kStageBatch float4 slices of a thread's input, loaded before the
@@ -229,10 +239,35 @@ struct StageInput {
 struct StagePrefetch {
     float4 x[kStageBatch];
     float4 y[kStageBatch];
+    // kPreMerge: the partials of the thread's one slice, chunk c of its head
+    // (m = -inf, l = 0, o = 0 past n_chunks)
+    float4 mo[kMergeChunks];
+    float2 mml[kMergeChunks];
 };
 
 template <int PRE>
 __device__ __forceinline__ void stage_prefetch(const StageInput &in, int n4, StagePrefetch &pf) {
+    if constexpr (PRE == kPreMerge) {
+        // one slice per thread (the launch checks n4 <= threads): float4 i of
+        // the attention output is dims 4 (i % (D / 4)) .. of head i / (D / 4)
+        const int i = (int)threadIdx.x;
+        const int q4 = in.head_dim / 4;
+        const int base = (i < n4 ? i / q4 : 0) * in.max_chunks;
+        const float4 *o4 = reinterpret_cast<const float4 *>(in.part_o);
+        const float2 *ml2 = reinterpret_cast<const float2 *>(in.part_ml);
+#pragma unroll
+        for (int c = 0; c < kMergeChunks; ++c) {
+            const bool live = i < n4 && c < in.n_chunks;
+            pf.mml[c] = live ? ml2[base + c] : make_float2(-__builtin_inff(), 0.0f);
+            pf.mo[c] = live ? o4[(size_t)(base + c) * q4 + i % q4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            pf.x[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            pf.y[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        return;
+    }
     const float4 *y4 = reinterpret_cast<const float4 *>(PRE == kPreRmsNorm ? in.norm_w : in.x2);
 #pragma unroll
     for (int u = 0; u < kStageBatch; ++u) {
@@ -315,6 +350,32 @@ __device__ __forceinline__ float octet_max(float m) {
 // Lane i + 4's value in lanes i with i % 16 < 12 (row shift left by 4).
 __device__ __forceinline__ uint32_t from_lane_plus4(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
+}
+
+// The thread's slice of the attention output from its head's split-K
+// partials: M = max_c m_c, then sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c
+// over the chunks in order (chunk 0 always holds position 0, so M is finite);
+// the quotient as decode_merge_kernel forms it (1 / l, 1 for l = 0).  Its
+// rounding differs from that kernel's pairwise merges by a few ulps.
+__device__ __forceinline__ float4 merged_slice(const StagePrefetch &pf) {
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int c = 0; c < kMergeChunks; ++c) {
+        mx = fmaxf(mx, pf.mml[c].x);
+    }
+    float l = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int c = 0; c < kMergeChunks; ++c) {
+        const float w = pf.mml[c].x == -__builtin_inff() ? 0.0f : fast_exp2(pf.mml[c].x - mx);
+        l += w * pf.mml[c].y;
+        o.x += w * pf.mo[c].x;
+        o.y += w * pf.mo[c].y;
+        o.z += w * pf.mo[c].z;
+        o.w += w * pf.mo[c].w;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 1.0f;
+    return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
 }
 
 // Stage the (pre-operated) input's digit planes and block scales (layout above)
@@ -426,9 +487,16 @@ __device__ __forceinline__ void stage_digit_planes(const StageInput &in, int pai
         float4 v[kStageBatch];
 #pragma unroll
         for (int u = 0; u < kStageBatch; ++u) {
-            v[u] = u * nthreads + (int)threadIdx.x < n4 ? pre_op(pf.x[u], pf.y[u]) : pf.x[u];
+            if constexpr (PRE == kPreMerge) {
+                v[u] = u == 0 && (int)threadIdx.x < n4 ? merged_slice(pf) : pf.x[u];
+            } else {
+                v[u] = u * nthreads + (int)threadIdx.x < n4 ? pre_op(pf.x[u], pf.y[u]) : pf.x[u];
+            }
         }
         digitize(0, v);
+    }
+    if constexpr (PRE == kPreMerge) {
+        return;  // one slice per thread
     }
     for (int base = kStageBatch * nthreads; base < n4; base += kStageBatch * nthreads) {
         float4 v[kStageBatch];
@@ -1077,6 +1145,10 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
         return TE_STATUS_OK;
     }
     const int wpg = waves_fit < (size_t)kPairWaves ? (int)waves_fit : kPairWaves;
+    // a merge staging takes one slice of the input per thread, with one row per tile
+    if (pre == kPreMerge && (glu || wide || nr != 1 || pairs * 16 > (size_t)(64 * wpg))) {
+        return TE_STATUS_OK;
+    }
     const size_t lds = plane_bytes + (size_t)wpg * tile_lds;
     a.row_bytes = row_bytes;
     a.tiles = 0;
@@ -1111,6 +1183,10 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
             TE_STREAM(T, L, N, C, kPreRmsNorm, false);     \
         } else if (pre == kPreSwiGLU) {                    \
             TE_STREAM(T, L, N, C, kPreSwiGLU, false);      \
+        } else if (pre == kPreMerge) {                     \
+            if constexpr (N == 1) {                        \
+                TE_STREAM(T, L, N, C, kPreMerge, false);   \
+            }                                              \
         } else {                                           \
             TE_STREAM(T, L, N, C, kPreNone, false);        \
         }                                                  \
@@ -1328,6 +1404,23 @@ te_status launch_gemv_glu(uint32_t ggml_type, const void *gate_w, const void *up
     a.cols = (int)cols;
     a.in = StageInput{x, nullptr, norm_w, eps};
     return launch_stream(ggml_type, kPreRmsNorm, a, stream, launched, true);
+}
+
+te_status launch_gemv_merge(uint32_t ggml_type, const GemvSeg &seg, size_t cols, const float *part_o,
+                            const float *part_ml, size_t chunks, size_t max_chunks, size_t head_dim,
+                            hipStream_t stream, bool *launched) {
+    *launched = false;
+    if (getenv("TE_HIP_GEMV_STRIDED") != nullptr || chunks == 0 || chunks > (size_t)kMergeChunks ||
+        chunks > max_chunks || head_dim % 4 != 0 || cols % head_dim != 0 || ((size_t)part_o & 15u) != 0 ||
+        ((size_t)part_ml & 7u) != 0 || max_chunks > 65535) {
+        return TE_STATUS_OK;
+    }
+    StreamArgs a = {};
+    a.seg[0] = StreamSeg{static_cast<const unsigned char *>(seg.w), seg.out, seg.resid, 0, (int)seg.rows, 0};
+    a.nseg = 1;
+    a.cols = (int)cols;
+    a.in = StageInput{nullptr, nullptr, nullptr, 0.0f, part_o, part_ml, (int)chunks, (int)max_chunks, (int)head_dim};
+    return launch_stream(ggml_type, kPreMerge, a, stream, launched);
 }
 
 te_status launch_dequant_row(const void *weights, uint32_t ggml_type, size_t cols, size_t row, float *out,
