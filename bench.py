@@ -87,8 +87,8 @@ def parse_args():
     p.add_argument("--phases", action="store_true",
                    help="only the prefill phase table: load the phase-instrumented library "
                         "(python -m tinymetalagent_amd.build --phases), run the causal prefill at 3B L=4096 and "
-                        "L=2048 and a 1.5B 2K chunk after 128K, print per-step shader-clock cycles per phase as "
-                        "JSON and exit")
+                        "L=2048 and a 1.5B 2K chunk after 128K, print per-step shader-clock cycles per phase, "
+                        "and the rows kernel's wall-clock marks at L=128 and L=512, as JSON and exit")
     p.add_argument("--generate", action="store_true",
                    help="only the end-to-end te_generate_raw case on a 3B-shaped GGUF (Q4_0 and Q8_0); print its "
                         "JSON and exit")
@@ -954,13 +954,76 @@ def phase_table() -> dict:
     return out
 
 
+ROWS_MARKS = ["start", "first block's weights", "block loop done", "(m, l) exchanged", "rows staged",
+              "rows stored"]
+
+
+def rows_phase_table() -> dict:
+    """Wall-clock marks of prefill_rows_f16_kernel<128> (forced on), from the
+    -DTE_PREFILL_PHASES build: each wave records s_memrealtime (100 MHz) at
+    the marks of ROWS_MARKS; reported in us from the launch's first wave start:
+    the slowest workgroup's range over its waves, and the median over
+    workgroups of each phase."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from tinymetalagent_amd import attention as A
+    from tinymetalagent_amd import runtime as R
+
+    lib = R.load_library()
+    waves, nph = 8, len(PHASE_NAMES)
+    out = {}
+    os.environ["TE_HIP_PREFILL_ROWS"] = "1"
+    try:
+        for (h, kv, d, L, base) in [(16, 2, 128, 128, 0), (16, 2, 128, 512, 0)]:
+            ctx = base + L
+            g = torch.Generator(device="cuda").manual_seed(1)
+            kc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+            vc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+            qh = torch.randn((1, 1, L, h, d), generator=g, device="cuda").half()
+            vt = A.value_t_buffer(1, 1, ctx, kv, d)
+            A.value_transpose(vc, vt)
+            o = torch.empty((1, 1, L, h, d), device="cuda")
+            nwg = (L + 31) // 32 * h
+            log = torch.zeros(nwg * waves * nph, dtype=torch.int32, device="cuda")
+            for _ in range(20):
+                A.attention_prefill_vt(qh, kc, vt, base_position=base, out=o)
+            torch.cuda.synchronize()
+            lib.te_hip_prefill_phase_log_set(ctypes.c_void_p(log.data_ptr()))
+            A.attention_prefill_vt(qh, kc, vt, base_position=base, out=o)
+            torch.cuda.synchronize()
+            lib.te_hip_prefill_phase_log_set(ctypes.c_void_p(0))
+            t = log.cpu().numpy().view(np.uint32).astype(np.int64).reshape(nwg, waves, nph)[:, :, :len(ROWS_MARKS)]
+            us = np.where(t > 0, (t - t[:, :, 0].min()) * 0.01, np.nan)  # a wave without a block has no mark 1
+            first = us[:, :, 1]
+            crit = int(np.argmax(us[:, :, 5].max(axis=1)))
+            case = {"workgroups": nwg, "span_us": round(float(us[:, :, 5].max()), 2),
+                    "slowest_workgroup_us": {nm: [round(float(np.nanmin(us[crit, :, i])), 2),
+                                                  round(float(np.nanmax(us[crit, :, i])), 2)]
+                                             for i, nm in enumerate(ROWS_MARKS)},
+                    "median_us": {
+                        "start -> first block's weights": round(float(np.nanmedian(first - us[:, :, 0])), 2),
+                        "block loop done -> rows staged": round(float(np.median(us[:, :, 4] - us[:, :, 2])), 2),
+                        "rows staged -> stored": round(float(np.median(us[:, :, 5] - us[:, :, 4])), 2)}}
+            out[f"H{h}_L{L}_base{base}"] = case
+            del kc, vc, qh, vt, o
+            torch.cuda.empty_cache()
+    finally:
+        os.environ.pop("TE_HIP_PREFILL_ROWS", None)
+    return out
+
+
 def main():
     args = parse_args()
     if args.phases:
         from tinymetalagent_amd import build as B
 
         os.environ["TINYENGINE_LIBRARY"] = str(B.PHASE_LIBRARY)
-        print(json.dumps({"prefill_phases_cycles": phase_table()}))
+        os.environ["TE_HIP_PREFILL_ROWS"] = "0"
+        tile = phase_table()
+        print(json.dumps({"prefill_phases_cycles": tile, "prefill_rows_phases_us": rows_phase_table()}))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "

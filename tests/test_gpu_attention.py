@@ -402,20 +402,27 @@ def _prefill_case(oracle_mod, h, kv, d, tokens, base, seed):
     return out.cpu().numpy().reshape(tokens, h, d), want
 
 
+@pytest.mark.parametrize("kernel", ["auto", "tile", "rows"])
 @pytest.mark.parametrize("h,kv,d,tokens,base", [
     (16, 2, 128, 300, 0),
     (16, 2, 128, 130, 200),
     (16, 2, 128, 1, 0),
     (16, 2, 128, 64, 0),
-    (16, 2, 128, 512, 0),      # BASELINE config 3 (3B) at L=512: 64 single tiles, one round
+    (16, 2, 128, 512, 0),      # BASELINE config 3 (3B) at L=512
     (14, 2, 64, 200, 37),
     (28, 4, 128, 257, 0),
     (12, 2, 128, 129, 1000),
 ])
-def test_prefill_vs_oracle(oracle_mod, h, kv, d, tokens, base):
+def test_prefill_vs_oracle(oracle_mod, monkeypatch, kernel, h, kv, d, tokens, base):
+    """Every row against the oracle, with the library's kernel choice and with
+    each kernel forced (TE_HIP_PREFILL_ROWS: the tile kernel, 128-row tiles
+    over a step loop; the rows kernel, 32-row groups with their keys split over
+    the waves)."""
+    if kernel != "auto":
+        monkeypatch.setenv("TE_HIP_PREFILL_ROWS", "1" if kernel == "rows" else "0")
     got, want = _prefill_case(oracle_mod, h, kv, d, tokens, base, 25)
     err = maxabs(got, want)
-    print(f"prefill H{h} KV{kv} d{d} L{tokens} base{base}: max abs err {err:.3e}")
+    print(f"prefill ({kernel}) H{h} KV{kv} d{d} L{tokens} base{base}: max abs err {err:.3e}")
     assert err <= TOL
 
 
@@ -909,13 +916,18 @@ def test_prefill_vt_ignores_positions_past_rounded_end(oracle_mod, tokens, base)
     assert err <= TOL and err_step <= TOL
 
 
+@pytest.mark.parametrize("kernel,tokens,base", [("tile", 300, 20), ("rows", 300, 20), ("rows", 300, 700)])
 @pytest.mark.parametrize("growth", [0.0, 0.02, 0.1, 0.2])
-def test_prefill_rising_scores_rescale(oracle_mod, growth):
+def test_prefill_rising_scores_rescale(oracle_mod, monkeypatch, growth, kernel, tokens, base):
     """Scores that keep rising along the keys (key p scaled by 1 + growth * p /
     16, q = k direction shared), so later blocks exceed an earlier reference by
     far more than 2^16 in the weights: the exact rescale path must run, with
-    and without a key split, and every row must still match the oracle."""
-    h, kv, d, tokens, base = 4, 1, 128, 300, 20
+    and without a key split, and every row must still match the oracle.  Each
+    kernel forced: the tile kernel, and the rows kernel with one block per
+    wave (320 keys: the waves' references differ and only the merge rescales)
+    and with two (1,000 keys: a wave's second block raises its reference)."""
+    monkeypatch.setenv("TE_HIP_PREFILL_ROWS", "1" if kernel == "rows" else "0")
+    h, kv, d = 4, 1, 128
     ctx = base + tokens
     g = np.random.default_rng(5)
     dirn = g.standard_normal(d).astype(np.float32)
@@ -936,5 +948,5 @@ def test_prefill_rising_scores_rescale(oracle_mod, growth):
     split = A.attention_prefill_vt(qd, kd, vt, base_position=base, workspace=ws).cpu().numpy().reshape(tokens, h, d)
     assert np.isfinite(one).all() and np.isfinite(split).all()
     err = max(maxabs(one, want), maxabs(split, want))
-    print(f"prefill rising scores (growth {growth}): max abs err {err:.3e}")
+    print(f"prefill rising scores ({kernel}, L{tokens} base{base}, growth {growth}): max abs err {err:.3e}")
     assert err <= TOL

@@ -872,6 +872,278 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
 #endif
 }
 
+// Short launches: the rows kernel.  One workgroup per RM (32) query rows of
+// one head; its 8 waves take the row group's 64-key blocks round-robin (wave
+// w: blocks w, w + 8, ...), each over all 32 rows, so a row group of at most
+// 8 blocks is one block per wave: no step loop, no per-step barrier, no LDS
+// staging.  The operands load from global
+// memory straight into registers in the MFMA layouts of the tile kernel
+// (K rows in the sigma key order, V^T rows of 8 consecutive keys), the
+// softmax is the tile kernel's (fp32, base 2, lazy reference, fp16 P), with
+// each block's row maximum taken exactly.  At the end the waves' states merge
+// once through LDS: every wave writes its rows scaled by 2^(m_w - M) / L
+// (M, L: the row's maximum and weight sum over the waves), and wave w sums
+// rows 4w .. 4w + 3 over the waves and stores them as whole rows.
+constexpr int RM = 32;
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void prefill_rows_f16_kernel(PrefillArgs a) {
+    constexpr int KK = D / 32;     // QK^T K-steps
+    constexpr int NT = D / 16;     // O^T output tiles
+    constexpr int OPITCH = D + 4;  // floats per staged row (16 rows of one write on distinct banks)
+    __shared__ __attribute__((aligned(16))) float part[kWaves][RM * OPITCH];
+    __shared__ float2 mls[kWaves][RM];
+
+    // Units: row group fastest, then head, then seq*layer; remapped so that
+    // XCD x runs units [x W/8, (x+1) W/8) (the heads of one KV group share
+    // an L2), as in the tile kernel.
+    int unit = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+    const int n_units = (int)(gridDim.x * gridDim.y * gridDim.z);
+    if (n_units % kXcds == 0) {
+        unit = (unit % kXcds) * (n_units / kXcds) + unit / kXcds;
+    }
+    const int rg = (int)((unsigned)unit % gridDim.x);
+    const unsigned hg = (unsigned)unit / gridDim.x;
+    const int h = (int)(hg % (unsigned)a.heads);
+    const int sl = (int)(hg / (unsigned)a.heads);
+    const int kvh = h / a.group;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int r0 = rg * RM;
+    const int kmax = a.base + min(r0 + RM, a.tokens) - 1;  // the row group's last key
+    const int nblk = kmax / BN + 1;
+    const float qs = a.qscale;
+    const size_t row_stride = (size_t)a.kv_heads * D;
+    const f16 *kbase = a.key_cache + (size_t)sl * a.ctx * row_stride + (size_t)kvh * D;
+    const f16 *vtbase = a.value_t + ((size_t)sl * a.kv_heads + kvh) * D * (size_t)a.ctx_pad;
+#ifdef TE_PREFILL_PHASES
+    // wall-clock marks (s_memrealtime, 100 MHz): start, first block's weights,
+    // block loop done, (m, l) exchanged, rows staged, rows stored; shader cycles
+    unsigned tr[kPhases] = {};
+    tr[0] = (unsigned)__builtin_amdgcn_s_memrealtime();
+    const unsigned cyc0 = (unsigned)__builtin_amdgcn_s_memtime();
+#endif
+
+    // Q^T operand: lane (c, g) holds row r0 + 16 nb + c, dims 32 kk + 8 g ..
+    // (rows past the end: zero operands, finite scores, never stored)
+    f16x8 qop[2][KK];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int row = r0 + 16 * nb + c;
+        const bool ok = row < a.tokens;
+        if (a.q32 != nullptr) {
+            load_q_rope<D>(a, sl, sl % a.layers, h, ok ? row : 0, g, qop[nb]);
+        } else {
+            const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                qop[nb][kk] = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
+            }
+        }
+        if (!ok) {
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                qop[nb][kk] = f16x8{};
+            }
+        }
+    }
+
+    float mref[2] = {-INFINITY, -INFINITY};  // exp reference per row, log2 units
+    float l[2] = {0.0f, 0.0f};               // per-lane partial row sums
+    f32x4 o[2][NT];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            o[nb][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    for (int j = wave; j < nblk; j += kWaves) {
+        const int kb0 = j * BN;
+        // a block reaching past kmax clamps its K keys to kmax and its V^T
+        // chunks to the chunk holding kmax (those keys are masked; the V^T
+        // writers keep that chunk's positions finite)
+        const bool tail = kb0 + BN - 1 > kmax;
+        // ---- S^T = K Q^T: tile i holds keys kb0 + sigma(i, m) ----
+        f16x8 kop[4][KK];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = tail ? min(kb0 + sigma(i, c), kmax) : kb0 + sigma(i, c);
+            const f16 *kr = kbase + (size_t)key * row_stride + 8 * g;
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                kop[i][kk] = *reinterpret_cast<const f16x8 *>(kr + 32 * kk);
+            }
+        }
+        f32x4 s[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                s[i][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    s[i][nb] = mfma16x16x32(kop[i][kk], qop[nb][kk], s[i][nb]);
+                }
+            }
+        }
+        // ---- V^T operand: tile t, k-step ks: dim 16 t + c, keys kb0 + 32 ks + 8 g .. ----
+        f16x8 vop[2][NT];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int kc = tail ? min(kb0 + 32 * ks + 8 * g, kmax & ~7) : kb0 + 32 * ks + 8 * g;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                vop[ks][t] = *reinterpret_cast<const f16x8 *>(vtbase + (size_t)(16 * t + c) * a.ctx_pad + kc);
+            }
+        }
+        // causal mask: the key of s[i][nb][r] is kb0 + 32(i/2) + 8g + 4(i%2) + r
+        if (kb0 + BN - 1 > a.base + r0) {
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const int lim = a.base + r0 + 16 * nb + c - kb0 - 8 * g;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (32 * (i >> 1) + 4 * (i & 1) + r > lim) {
+                            s[i][nb][r] = -INFINITY;
+                        }
+                    }
+                }
+            }
+        }
+        // ---- softmax: the block's row maxima, the lazy reference, fp16 weights ----
+        f16x8 pb[2][2];  // [PV k-step][row block]: keys 32 ks + 8 g + e
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    m = fmaxf(m, s[i][nb][r]);
+                }
+            }
+            const float mx = xor_max_16_32(m) * qs;  // -inf: no unmasked key in the block
+            const bool first = mref[nb] == -INFINITY;
+            const bool move = first ? mx > -INFINITY : mx - mref[nb] > kLazyLog2;
+            if (__any(move && !first)) {
+                const float alpha = move && !first ? fast_exp2(mref[nb] - mx) : 1.0f;
+                l[nb] *= alpha;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    o[nb][t] = o[nb][t] * alpha;
+                }
+            }
+            mref[nb] = move ? mx : mref[nb];
+            const float nm = -mref[nb];
+            const bool none = mref[nb] == -INFINITY;
+            float sum = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = fast_exp2(fmaf(s[2 * ks + (e >> 2)][nb][e & 3], qs, nm));
+                    pb[ks][nb][e] = none ? (f16)0.0f : (f16)x;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const f16x2 pr = {pb[ks][nb][e], pb[ks][nb][e + 1]};
+                    sum = __builtin_amdgcn_fdot2(pr, f16x2{(f16)1.0f, (f16)1.0f}, sum, false);
+                }
+            }
+            l[nb] += sum;
+        }
+#ifdef TE_PREFILL_PHASES
+        if (j == wave) {
+            tr[1] = (unsigned)__builtin_amdgcn_s_memrealtime();
+        }
+#endif
+        // ---- O^T += V^T P^T ----
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                o[0][t] = mfma16x16x32(vop[ks][t], pb[ks][0], o[0][t]);
+                o[1][t] = mfma16x16x32(vop[ks][t], pb[ks][1], o[1][t]);
+            }
+        }
+    }
+
+#ifdef TE_PREFILL_PHASES
+    tr[2] = (unsigned)__builtin_amdgcn_s_memrealtime();
+#endif
+    // ---- merge the waves' states: (m, l) per row, then the scaled rows ----
+    const int nact = min(nblk, kWaves);  // waves that took a block
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        l[nb] = xor_sum_16_32(l[nb]);
+        if (g == 0 && wave < nact) {
+            mls[wave][16 * nb + c] = make_float2(mref[nb], l[nb]);
+        }
+    }
+    __syncthreads();
+#ifdef TE_PREFILL_PHASES
+    tr[3] = (unsigned)__builtin_amdgcn_s_memrealtime();
+#endif
+    if (wave < nact) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            float mm = -INFINITY;
+            for (int p = 0; p < nact; ++p) {
+                mm = fmaxf(mm, mls[p][16 * nb + c].x);
+            }
+            float lt = 0.0f;
+            for (int p = 0; p < nact; ++p) {
+                const float2 ml = mls[p][16 * nb + c];
+                lt += ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - mm) * ml.y;
+            }
+            // (v_rcp_f32: within 1 ulp; lt >= 1 for a row that saw a key)
+            const float w = mref[nb] == -INFINITY || !(lt > 0.0f) ? 0.0f
+                                                                  : fast_exp2(mref[nb] - mm) * __builtin_amdgcn_rcpf(lt);
+            float *dst = &part[wave][(16 * nb + c) * OPITCH + 4 * g];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                *reinterpret_cast<f32x4 *>(dst + 16 * t) = o[nb][t] * w;
+            }
+        }
+    }
+    __syncthreads();
+#ifdef TE_PREFILL_PHASES
+    tr[4] = (unsigned)__builtin_amdgcn_s_memrealtime();
+#endif
+    // wave w: rows 4w .. 4w + 3 of the group, LPR lanes of 16 bytes per row
+    constexpr int LPR = D / 4;
+    constexpr int RPP = 64 / LPR;  // rows per pass
+    const int q = lane % LPR;
+#pragma unroll
+    for (int i = 0; i < 4 / RPP; ++i) {
+        const int r = 4 * wave + i * RPP + lane / LPR;
+        f32x4 acc = *reinterpret_cast<const f32x4 *>(&part[0][r * OPITCH + 4 * q]);
+        for (int p = 1; p < nact; ++p) {
+            acc += *reinterpret_cast<const f32x4 *>(&part[p][r * OPITCH + 4 * q]);
+        }
+        if (r0 + r < a.tokens) {
+            float *orow = a.out + (((size_t)sl * a.tokens + r0 + r) * a.heads + h) * D;
+            __builtin_nontemporal_store(acc, reinterpret_cast<f32x4 *>(orow + 4 * q));
+        }
+    }
+#ifdef TE_PREFILL_PHASES
+    __builtin_amdgcn_s_waitcnt(0);
+    tr[5] = (unsigned)__builtin_amdgcn_s_memrealtime();
+    tr[6] = (unsigned)__builtin_amdgcn_s_memtime() - cyc0;
+    if (a.phase_log != nullptr && lane == 0) {
+        const unsigned wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        for (int i = 0; i < kPhases; ++i) {
+            a.phase_log[(wg * kWaves + wave) * kPhases + i] = tr[i];
+        }
+    }
+#endif
+}
+
 // Key-split merge: out[row][h] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s
 // over the splits of one (seq*layer); M = max_s m_s.  A split that saw no
 // unmasked key of the row has m_s = -inf and weight 0 (split 0 always holds
@@ -1009,6 +1281,28 @@ bool prefill_paired(size_t seqs, size_t layers, size_t tokens, size_t heads, int
     return n_qtiles * heads * seqs * layers * (size_t)splits > (size_t)te_hip::device_compute_units();
 }
 
+// The rows kernel (one 32-row group per workgroup, its keys split over the
+// 8 waves) for a launch with one split over at most kRowsMaxKeys keys.  Its
+// last row group reads every key's K and V^T through one CU, in the MFMA
+// operand order (16 rows x 64 bytes per load instruction), with no compute
+// to hide it: measured on MI355X (3B shapes, graph-replayed), it is faster
+// than the tile kernel up to 256 keys (L = 128: 6.97 against 8.54 us, L = 256:
+// 9.44 against 9.98) and slower from 512 (13.8 against 13.2 us; 36.8 against
+// 19.4 at 1,024).  TE_HIP_PREFILL_ROWS=1 takes it for every launch with one
+// split, =0 never.
+constexpr size_t kRowsMaxKeys = 256;
+
+bool prefill_rows(size_t tokens, size_t base_position, int splits) {
+    if (splits != 1) {
+        return false;
+    }
+    const char *env = getenv("TE_HIP_PREFILL_ROWS");
+    if (env != nullptr && (env[0] == '0' || env[0] == '1') && env[1] == '\0') {
+        return env[0] == '1';
+    }
+    return base_position + tokens <= kRowsMaxKeys;
+}
+
 #ifdef TE_PREFILL_PHASES
 unsigned *g_phase_log = nullptr;
 #endif
@@ -1027,6 +1321,18 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
     a.qscale = TE_LOG2E / sqrtf((float)head_dim);
     if (a.splits < 1) {
         a.splits = 1;
+    }
+#ifdef TE_PREFILL_PHASES
+    a.phase_log = g_phase_log;
+#endif
+    if (prefill_rows(tokens, base_position, a.splits)) {
+        const dim3 grid((unsigned)((tokens + RM - 1) / RM), (unsigned)heads, (unsigned)(seqs * layers));
+        if (head_dim == 128) {
+            prefill_rows_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
+        } else {
+            prefill_rows_f16_kernel<64><<<grid, kThreads, 0, strm>>>(a);
+        }
+        return te_hip::launch_status();
     }
     a.paired = prefill_paired(seqs, layers, tokens, heads, a.splits) ? 1 : 0;
 #ifdef TE_PREFILL_PHASES
