@@ -596,6 +596,34 @@ def prefill_case(torch, A, timer, *, heads, kv, d, tokens, base=0, chunks=1, rep
     return res
 
 
+def prefill_graph_us(torch, A, *, heads, kv, d, tokens, base=0, kernel=None, launches=20, reps=20) -> float:
+    """te_hip_attention_prefill_vt_f16 (one split, V^T resident) per launch,
+    `launches` launches captured in one HIP graph and replayed: the kernel
+    time without the host's launch cost.  kernel "rows" / "tile" forces that
+    kernel (TE_HIP_PREFILL_ROWS), None takes the library's choice."""
+    ctx = base + tokens
+    g = torch.Generator(device="cuda").manual_seed(44)
+    kc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+    vc = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+    qh = torch.randn((1, 1, tokens, heads, d), generator=g, device="cuda").half()
+    vt = A.value_t_buffer(1, 1, ctx, kv, d)
+    A.value_transpose(vc, vt)
+    out = torch.empty((1, 1, tokens, heads, d), device="cuda")
+    old = os.environ.pop("TE_HIP_PREFILL_ROWS", None)
+    if kernel is not None:
+        os.environ["TE_HIP_PREFILL_ROWS"] = "1" if kernel == "rows" else "0"
+    try:
+        us = graph_time_us(torch, [lambda s: A.attention_prefill_vt(qh, kc, vt, base_position=base, out=out,
+                                                                    stream=s)] * launches, reps)
+    finally:
+        os.environ.pop("TE_HIP_PREFILL_ROWS", None)
+        if old is not None:
+            os.environ["TE_HIP_PREFILL_ROWS"] = old
+    del kc, vc, qh, vt, out
+    torch.cuda.empty_cache()
+    return us
+
+
 def graph_time_us(torch, launches, reps: int) -> float:
     """Mean microseconds per launch of `launches` (a list of callables taking a
     stream), captured once into a HIP graph and replayed: no host launch cost."""
@@ -1162,10 +1190,20 @@ def main():
         cfgs["0p5b_decode_pos512_1layer"] = dict(step_us=r(c["step_ms"] * 1e3, 2), splitk_us=r(c["splitk_ms"] * 1e3, 2))
         for L in (512, 2048):
             p = prefill_case(torch, A, timer, heads=16, kv=2, d=128, tokens=L, reps=20, split=True)
+            gus = prefill_graph_us(torch, A, heads=16, kv=2, d=128, tokens=L)
             cfgs[f"3b_prefill_L{L}"] = dict(attention_us=r(p["attention_ms"] * 1e3, 2), tflops=round(p["tflops"], 1),
                                             frac=r(p["tflops"] / FP16_MFMA_PEAK_TFLOPS),
+                                            attention_graph_us=r(gus, 2),
                                             step_fused_us=r(p["step_ms"] * 1e3, 2),
                                             split_entry=split_fields(p))
+        # prompts of at most 256 keys take the rows kernel; both kernels timed
+        for L in (128, 256):
+            rows_us = prefill_graph_us(torch, A, heads=16, kv=2, d=128, tokens=L)
+            tile_us = prefill_graph_us(torch, A, heads=16, kv=2, d=128, tokens=L, kernel="tile")
+            fl = prefill_flops(16, 128, L, 0)
+            cfgs[f"3b_prefill_L{L}"] = dict(kernel="prefill_rows_f16_kernel", attention_graph_us=r(rows_us, 2),
+                                            tflops=round(fl / rows_us / 1e6, 1),
+                                            tile_kernel_graph_us=r(tile_us, 2))
         p = prefill_case(torch, A, timer, heads=12, kv=2, d=128, tokens=2048, base=0, chunks=8, reps=3, split=True)
         cfgs["1p5b_chunked_prefill_16k_from0"] = dict(chunks=8, chunk_tokens=2048, attention_ms=r(p["attention_ms"], 3),
                                                      step_fused_ms=r(p["step_ms"], 3),
