@@ -875,12 +875,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
 // Short launches: the rows kernel.  One workgroup per RM (32) query rows of
 // one head; its 8 waves take the row group's 64-key blocks round-robin (wave
 // w: blocks w, w + 8, ...), each over all 32 rows, so a row group of at most
-// 8 blocks is one block per wave: no step loop, no per-step barrier, no LDS
-// staging.  The operands load from global
-// memory straight into registers in the MFMA layouts of the tile kernel
-// (K rows in the sigma key order, V^T rows of 8 consecutive keys), the
-// softmax is the tile kernel's (fp32, base 2, lazy reference, fp16 P), with
-// each block's row maximum taken exactly.  At the end the waves' states merge
+// 8 blocks is one block per wave: no step loop, no per-step barrier, no K /
+// V^T staging.  The group's queries go to LDS once; the K and V^T operands
+// load from global memory straight into registers in the MFMA layouts of the
+// tile kernel (K rows in the sigma key order, V^T rows of 8 consecutive
+// keys), and only waves that have a block load anything.  The softmax is the
+// tile kernel's (fp32, base 2, lazy reference, fp16 P), with each block's row
+// maximum taken exactly.  At the end the waves' states merge
 // once through LDS: every wave writes its rows scaled by 2^(m_w - M) / L
 // (M, L: the row's maximum and weight sum over the waves), and wave w sums
 // rows 4w .. 4w + 3 over the waves and stores them as whole rows.
@@ -893,6 +894,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_rows_f16_kernel(PrefillAr
     constexpr int OPITCH = D + 4;  // floats per staged row (16 rows of one write on distinct banks)
     __shared__ __attribute__((aligned(16))) float part[kWaves][RM * OPITCH];
     __shared__ float2 mls[kWaves][RM];
+    __shared__ __attribute__((aligned(16))) f16 qlds[RM][D + 8];  // rows padded: conflict-free operand reads
 
     // Units: row group fastest, then head, then seq*layer; remapped so that
     // XCD x runs units [x W/8, (x+1) W/8) (the heads of one KV group share
@@ -926,27 +928,61 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_rows_f16_kernel(PrefillAr
     const unsigned cyc0 = (unsigned)__builtin_amdgcn_s_memtime();
 #endif
 
-    // Q^T operand: lane (c, g) holds row r0 + 16 nb + c, dims 32 kk + 8 g ..
-    // (rows past the end: zero operands, finite scores, never stored)
+    // The group's fp16 queries, loaded once into LDS by the whole workgroup
+    // (the loads into one CU bound this kernel): thread t takes row t / (D/8),
+    // dims 8 (t % (D/8)) ..; rows past the end are zero (finite scores, never
+    // stored).  The fused step adds the bias and rotates here, with the
+    // operation order of rope_kv_append_kernel (FP contraction off), so the
+    // bits equal the fp16 queries the unfused path stores.
+    {
+#pragma clang fp contract(off)
+        constexpr int CPR = D / 8;     // 16-byte chunks per row
+        constexpr int HCH = CPR / 2;   // chunks per rotation half
+        const int t = threadIdx.x;
+        if (t < RM * CPR) {
+            const int rr = t / CPR;
+            const int ch = t % CPR;
+            const int row = r0 + rr;
+            f16x8 v = f16x8{};
+            if (row < a.tokens && a.q32 == nullptr) {
+                v = *reinterpret_cast<const f16x8 *>(a.q + (((size_t)sl * a.tokens + row) * a.heads + h) * D + 8 * ch);
+            } else if (row < a.tokens) {
+                // own chunk and its rotation partner (dims +-D/2), bias first
+                const float *qrow = a.q32 + (((size_t)sl * a.tokens + row) * a.heads + h) * D;
+                const int pc = ch ^ HCH;
+                float x[8], y[8];
+                *reinterpret_cast<float4 *>(x) = *reinterpret_cast<const float4 *>(qrow + 8 * ch);
+                *reinterpret_cast<float4 *>(x + 4) = *reinterpret_cast<const float4 *>(qrow + 8 * ch + 4);
+                *reinterpret_cast<float4 *>(y) = *reinterpret_cast<const float4 *>(qrow + 8 * pc);
+                *reinterpret_cast<float4 *>(y + 4) = *reinterpret_cast<const float4 *>(qrow + 8 * pc + 4);
+                if (a.q_bias != nullptr) {
+                    const float *qb = a.q_bias + ((size_t)(sl % a.layers) * a.heads + h) * D;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        x[j] = x[j] + qb[8 * ch + j];
+                        y[j] = y[j] + qb[8 * pc + j];
+                    }
+                }
+                const int pos = a.base + row;
+                const float *cr = a.rope_cos + (size_t)pos * (D / 2) + 8 * (ch % HCH);
+                const float *sr = a.rope_sin + (size_t)pos * (D / 2) + 8 * (ch % HCH);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    // first half: x0 c - x1 s; second half: x1 c + x0 s (x0 = dim d, x1 = dim d + D/2)
+                    v[j] = ch < HCH ? (f16)(x[j] * cr[j] - y[j] * sr[j]) : (f16)(x[j] * cr[j] + y[j] * sr[j]);
+                }
+            }
+            *reinterpret_cast<f16x8 *>(&qlds[rr][8 * ch]) = v;
+        }
+    }
+    __syncthreads();
+    // Q^T operand: lane (c, g) holds row 16 nb + c of the group, dims 32 kk + 8 g ..
     f16x8 qop[2][KK];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        const int row = r0 + 16 * nb + c;
-        const bool ok = row < a.tokens;
-        if (a.q32 != nullptr) {
-            load_q_rope<D>(a, sl, sl % a.layers, h, ok ? row : 0, g, qop[nb]);
-        } else {
-            const f16 *qrow = a.q + (((size_t)sl * a.tokens + (ok ? row : 0)) * a.heads + h) * D;
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                qop[nb][kk] = *reinterpret_cast<const f16x8 *>(qrow + 8 * g + 32 * kk);
-            }
-        }
-        if (!ok) {
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                qop[nb][kk] = f16x8{};
-            }
+        for (int kk = 0; kk < KK; ++kk) {
+            qop[nb][kk] = *reinterpret_cast<const f16x8 *>(&qlds[16 * nb + c][32 * kk + 8 * g]);
         }
     }
 
@@ -1285,11 +1321,13 @@ bool prefill_paired(size_t seqs, size_t layers, size_t tokens, size_t heads, int
 // 8 waves) for a launch with one split over at most kRowsMaxKeys keys.  Its
 // last row group reads every key's K and V^T through one CU, in the MFMA
 // operand order (16 rows x 64 bytes per load instruction), with no compute
-// to hide it: measured on MI355X (3B shapes, graph-replayed), it is faster
-// than the tile kernel up to 256 keys (L = 128: 6.97 against 8.54 us, L = 256:
-// 9.44 against 9.98) and slower from 512 (13.8 against 13.2 us; 36.8 against
-// 19.4 at 1,024).  TE_HIP_PREFILL_ROWS=1 takes it for every launch with one
-// split, =0 never.
+// to hide it.  Measured on MI355X (3B shapes, graph-replayed) against the
+// tile kernel: L = 128 6.00 against 8.55 us, 256 8.53 against 9.99, 384
+// 11.24 against 11.73, 512 12.92 against 13.17, 1,024 about twice as long.
+// At 512 keys its 256 workgroups of 146 KB LDS need every CU at once (one
+// measured launch started a workgroup 6.6 us late, in a second round), so
+// the choice stops at 256.  TE_HIP_PREFILL_ROWS=1 takes it for every launch
+// with one split, =0 never.
 constexpr size_t kRowsMaxKeys = 256;
 
 bool prefill_rows(size_t tokens, size_t base_position, int splits) {
