@@ -237,6 +237,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     constexpr int VB = VH::BYTES;
     constexpr int XFER = (4 * NT + 2) * 64;         // floats per wave in the merge exchange
     constexpr int STAGE = std::max(2 * KB + 2 * VB, kWaves * XFER * 4);
+    static_assert(kWaves * KK * 64 * 16 <= STAGE, "the fused step's query exchange fits st1");
     constexpr int GROUPS = 2 * KH::LOADS + 2 * VH::LOADS;  // 1 KB loads per step
     constexpr int LOADS = GROUPS / kWaves;          // per wave per step
     static_assert(LOADS * kWaves == GROUPS, "staging loads must tile the step");
@@ -424,23 +425,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             }
         }
     };
-    auto prep_q = [&](int qt) __attribute__((always_inline)) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const int row = qt * BM + 32 * (wave & 3) + 16 * nb + c;
-            const bool ok = row < a.tokens;
-            if (a.q32 != nullptr) {
-                load_q_rope<D>(a, sl, sl % a.layers, h, ok ? row : 0, g, qop[nb]);
-            }
-            // rows past the end: zero operands (finite scores, never stored)
-            if (!ok) {
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    qop[nb][kk] = f16x8{};
-                }
-            }
-        }
-    };
     // Barrier over LDS traffic only: the waves' LDS reads and writes are done
     // and visible, while global loads and stores (the next tile's queries, the
     // output rows) stay in flight.  A workgroup-scope fence would also wait
@@ -450,6 +434,55 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     // keeps the compiler's LDS accesses on their side of the barrier.
     auto lds_barrier = []() __attribute__((always_inline)) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    // The fused step's queries: waves w and w ^ 4 hold the same 32 rows, so
+    // each loads, biases and rotates one 16-row block (half h: block h) and
+    // they hand each other their blocks through st1, which is free at a
+    // tile's start (the tile's first step is staged in st0): half the fp32
+    // query and rotation-table loads, which arrive with nothing to hide them.
+    // Two LDS barriers: the blocks are written before they are read, and read
+    // before the first step stages into st1.
+    auto prep_q = [&](int qt) __attribute__((always_inline)) {
+        if (a.q32 != nullptr) {
+            const int row = qt * BM + 32 * (wave & 3) + 16 * half + c;
+            f16x8 mine[KK];
+            if (row < a.tokens) {
+                load_q_rope<D>(a, sl, sl % a.layers, h, row, g, mine);
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    mine[kk] = f16x8{};  // rows past the end: zero operands (finite scores, never stored)
+                }
+            }
+            f16x8 *xq = reinterpret_cast<f16x8 *>(st1);
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                xq[(wave * KK + kk) * 64 + lane] = mine[kk];
+            }
+            lds_barrier();
+            f16x8 other[KK];
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                other[kk] = xq[((wave ^ 4) * KK + kk) * 64 + lane];
+            }
+            lds_barrier();
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                qop[0][kk] = half == 0 ? mine[kk] : other[kk];
+                qop[1][kk] = half == 0 ? other[kk] : mine[kk];
+            }
+            return;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            // rows past the end: zero operands (finite scores, never stored)
+            if (qt * BM + 32 * (wave & 3) + 16 * nb + c >= a.tokens) {
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    qop[nb][kk] = f16x8{};
+                }
+            }
+        }
     };
 
     if (split_cnt(tile_steps(long_tile)) > 0) {
