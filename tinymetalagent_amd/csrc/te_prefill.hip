@@ -227,7 +227,10 @@ struct DmaPlan {
     int vsoff;
 };
 
-template <int D>
+// Q32: the fused step's fp32 queries (bias + RoPE on load), else fp16
+// queries; one instantiation per query kind keeps each kind's registers to
+// its own path.
+template <int D, bool Q32>
 __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(PrefillArgs a) {
     typedef KHalf<D> KH;
     typedef VtHalf<D> VH;
@@ -443,7 +446,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     // Two LDS barriers: the blocks are written before they are read, and read
     // before the first step stages into st1.
     auto prep_q = [&](int qt) __attribute__((always_inline)) {
-        if (a.q32 != nullptr) {
+        if constexpr (Q32) {
             const int row = qt * BM + 32 * (wave & 3) + 16 * half + c;
             f16x8 mine[KK];
             if (row < a.tokens) {
@@ -488,7 +491,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
     if (split_cnt(tile_steps(long_tile)) > 0) {
         stage_load(split_lo(tile_steps(long_tile)), tile_kmax(long_tile), st0);
     }
-    if (a.q32 == nullptr) {
+    if constexpr (!Q32) {
         load_q16(long_tile);
     }
     bool first_staged = true;  // the tile's first step is in LDS (waited for) when it starts
@@ -759,7 +762,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             body(std::integral_constant<int, 1>(), j + 1);
         }
         first_staged = cnt > 0;
-        if (ti + 1 < n_tiles_wg && a.q32 == nullptr) {
+        if (!Q32 && ti + 1 < n_tiles_wg) {
             load_q16(pair);  // qop is dead after the last step: the next tile's queries load across the merge
         }
 
@@ -1412,9 +1415,15 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
     const int n_units_x = a.paired ? (a.n_qtiles + 1) / 2 : a.n_qtiles;
     const dim3 grid((unsigned)n_units_x, (unsigned)heads, (unsigned)(seqs * layers * a.splits));
     if (head_dim == 128) {
-        prefill_causal_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
+        if (a.q32 != nullptr) {
+            prefill_causal_f16_kernel<128, true><<<grid, kThreads, 0, strm>>>(a);
+        } else {
+            prefill_causal_f16_kernel<128, false><<<grid, kThreads, 0, strm>>>(a);
+        }
+    } else if (a.q32 != nullptr) {
+        prefill_causal_f16_kernel<64, true><<<grid, kThreads, 0, strm>>>(a);
     } else {
-        prefill_causal_f16_kernel<64><<<grid, kThreads, 0, strm>>>(a);
+        prefill_causal_f16_kernel<64, false><<<grid, kThreads, 0, strm>>>(a);
     }
     return te_hip::launch_status();
 }
