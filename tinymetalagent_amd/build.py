@@ -51,8 +51,12 @@ HIP_FLAGS = [
 # accumulation registers (its blocks' integer sums are shifted and scaled by
 # VALU code; the accumulation-register form moved every one through v_accvgpr
 # reads and writes: gate GEMM at 512 rows 103 -> 92 us).
+# te_vecops.hip: the max-ilp scheduling strategy (the 3B Q4_0 decode token
+# 1,420 -> 1,394 us, Q8_0 unchanged, same box, alternating builds; the
+# prefill, decode and GEMM sources measured no better with it).
 HIP_SOURCE_FLAGS = {
     "te_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "te_vecops.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
 
 
