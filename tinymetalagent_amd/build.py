@@ -51,12 +51,13 @@ HIP_FLAGS = [
 # accumulation registers (its blocks' integer sums are shifted and scaled by
 # VALU code; the accumulation-register form moved every one through v_accvgpr
 # reads and writes: gate GEMM at 512 rows 103 -> 92 us).
-# te_vecops.hip: the iterative-ilp scheduling strategy (the 3B decode token
-# Q4_0 1,431 -> 1,404 us, Q8_0 1,646 -> 1,627 us, same box, alternating
-# builds; the prefill, decode, append and GEMM sources measured no better
-# with the other strategies).
+# te_vecops.hip and te_gemm.hip: the iterative-ilp scheduling strategy (the
+# 3B decode token Q4_0 1,431 -> 1,404 us, Q8_0 1,646 -> 1,627 us; the prompt
+# GEMM at 512 rows, gate 87.1 -> 84.7 us, down 91.0 -> 90.3 us; same box,
+# alternating builds).  The prefill, decode and append sources measured no
+# better with it or the other strategies.
 HIP_SOURCE_FLAGS = {
-    "te_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "te_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "te_vecops.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 
