@@ -1113,9 +1113,13 @@ te_status launch_stream(uint32_t ggml_type, int pre, StreamArgs a, hipStream_t s
     // a GLU tile's rows of one matrix fill half its buffer
     const size_t hgroups = glu ? groups / 2 : groups;
     const size_t cus = (size_t)device_compute_units();
-    const size_t want = cus * 8;
     // tiles of at most 10 KB (larger tiles measured faster at lm_head, 4 / 8 / 12 KB: more bytes
-    // in flight per wave), as many rows as keep every CU at 8 waves
+    // in flight per wave), as many rows as keep 16 tiles per CU for Q4_0 and 24 for Q8_0 (3B
+    // decode token against 8 per CU, same box: Q4_0 1,396 -> 1,371 us, mostly the 11008-row
+    // projections at one row per lane group instead of two and the paired gate / up at two
+    // instead of four; Q8_0 1,633 -> 1,611 us, its paired gate / up at one row instead of two;
+    // the lm_head keeps its rows per group)
+    const size_t want = cus * (ggml_type == kGgmlQ8_0 ? 24 : 16);
     size_t tile_cap = kStreamTileBytes;
     if (const char *env = getenv("TE_HIP_GEMV_TILE")) {  // tuning override: bytes per row-group tile
         tile_cap = (size_t)atoi(env) >= 1024 && (size_t)atoi(env) <= kStreamTileBytes ? (size_t)atoi(env) : tile_cap;
