@@ -167,10 +167,14 @@ def test_decode_all_layers_argument_checks():
     assert call(head_dim=32, hidden=128, kv=64) == 3   # head_dim not 64 / 128: nothing launched
 
 
-def test_decode_all_layers_q8_0_wide_down_rows(oracle_mod):
-    """Q8_0 at the 3B widths: ffn_down rows of 11008 columns are 11696 bytes,
-    streamed in 12 KB tiles with SwiGLU staging and the residual fused."""
-    _run(oracle_mod, 8, layers=1, heads=16, kv_heads=2, head_dim=128, ffn=11008, vocab=512, ctx=32, position=9)
+@pytest.mark.parametrize("ggml_type", [2, 8])
+def test_decode_all_layers_3b_widths(oracle_mod, ggml_type):
+    """One layer at the 3B widths (hidden 2048, ffn 11008): the paired gate /
+    up GEMV at two rows per lane group (Q4_0) and one (Q8_0), the ffn_down
+    rows of 11008 columns (Q8_0: 11696 bytes, streamed in 12 KB tiles) with
+    SwiGLU staging and the residual fused."""
+    _run(oracle_mod, ggml_type, layers=1, heads=16, kv_heads=2, head_dim=128, ffn=11008, vocab=512, ctx=32,
+         position=9)
 
 
 @pytest.mark.parametrize("ggml_type", [2, 8])

@@ -47,8 +47,9 @@ def _matvec_bound(oracle_mod, data, ggml_type, x, cols, rows):
 
 @pytest.mark.parametrize("ggml_type,rows,cols", [
     (V.GGML_Q4_0, 1, 32), (V.GGML_Q4_0, 7, 96), (V.GGML_Q4_0, 2048, 2048), (V.GGML_Q4_0, 256, 11008),
-    (V.GGML_Q4_0, 16387, 256),                         # four rows per wave, ragged last wave
-    (V.GGML_Q8_0, 3, 64), (V.GGML_Q8_0, 8195, 160),    # two rows per wave, ragged
+    (V.GGML_Q4_0, 16387, 256),                         # one row per lane group, ragged last wave
+    (V.GGML_Q8_0, 3, 64), (V.GGML_Q8_0, 8195, 160),    # ragged
+    (V.GGML_Q4_0, 40003, 256), (V.GGML_Q8_0, 60001, 256),  # two rows per lane group, ragged last tile
     (V.GGML_Q8_0, 512, 2048), (V.GGML_F32, 5, 4), (V.GGML_F32, 300, 2052), (V.GGML_F32, 9000, 64),
     (V.GGML_Q4_0, 200003, 128),                        # several row tiles per wave, ragged last tile
     (V.GGML_Q8_0, 1000, 2560),                         # two pair steps per tile, the second partial
