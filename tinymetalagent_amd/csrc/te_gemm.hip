@@ -83,91 +83,157 @@ __device__ __forceinline__ void quant_block(float v, size_t row, int K, int b, i
     }
 }
 
-// One workgroup per row: x' = pre(x), then digits and block scales.
+// One 32-value block of digits held as eight consecutive values by each of
+// four adjacent lanes (g = lane & 3 holds values 8g .. 8g + 7): the same
+// digits and scale as quant_block (the block maximum does not depend on the
+// order it is taken in), stored as 8-byte pieces where `vec`.
+__device__ __forceinline__ void quant_block8(const float (&v)[8], size_t row, int K, int b, int g,
+                                             int8_t *__restrict__ hi, int8_t *__restrict__ lo,
+                                             float *__restrict__ scales, bool vec) {
+    float m = fabsf(v[0]);
+#pragma unroll
+    for (int j = 1; j < 8; ++j) {
+        m = fmaxf(m, fabsf(v[j]));
+    }
+    m = fmaxf(m, __shfl_xor(m, 1, 4));
+    m = fmaxf(m, __shfl_xor(m, 2, 4));
+    int q[8] = {};
+    float s;
+    if (!(m <= FLT_MAX)) {  // inf or NaN in the block: its products are NaN
+        s = __builtin_nanf("");
+    } else if (m == 0.0f) {
+        s = 0.0f;
+    } else {
+        int E;
+        (void)frexpf(m, &E);
+        const int e = min(14 - E, 126);  // blocks below 2^-112 round towards 0
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            q[j] = (int)rintf(ldexpf(v[j], e));
+        }
+        s = ldexpf(1.0f, -e);
+    }
+    uint32_t h[2] = {0, 0}, l[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int l8 = ((q[j] + 128) & 255) - 128;
+        h[j >> 2] |= (uint32_t)(((q[j] - l8) >> 8) & 255) << (8 * (j & 3));
+        l[j >> 2] |= (uint32_t)(l8 & 255) << (8 * (j & 3));
+    }
+    const size_t t = (((row >> 5) * (size_t)(K >> 5) + b) << 10) + ((row & 31) << 5) + 8 * g;
+    if (vec) {
+        *reinterpret_cast<uint2 *>(hi + t) = make_uint2(h[0], h[1]);
+        *reinterpret_cast<uint2 *>(lo + t) = make_uint2(l[0], l[1]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            hi[t + j] = (int8_t)(h[j >> 2] >> (8 * (j & 3)));
+            lo[t + j] = (int8_t)(l[j >> 2] >> (8 * (j & 3)));
+        }
+    }
+    if (g == 0) {
+        scales[row * (size_t)(K / 32) + b] = s;
+    }
+}
+
+// Eight consecutive floats: two 16-byte loads where `vec`.
+__device__ __forceinline__ void load8(const float *p, bool vec, float (&v)[8]) {
+    if (vec) {
+        const float4 a = *reinterpret_cast<const float4 *>(p);
+        const float4 c = *reinterpret_cast<const float4 *>(p + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = c.x, v[5] = c.y, v[6] = c.z, v[7] = c.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = p[j];
+        }
+    }
+}
+
+__device__ __forceinline__ void store8(float *p, bool vec, const float (&v)[8]) {
+    if (vec) {
+        *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[j] = v[j];
+        }
+    }
+}
+
+// The fp64 sum of squares of a row whose thread t holds columns
+// 8t + 2048i .. +7 (i = 0, 1, ...): each thread adds its values in column
+// order, the wave's lanes are added by an xor butterfly and the workgroup's
+// four waves in wave order.  quant_act_kernel<kActRmsNorm> and
+// gemm_reduce_rms_kernel both sum this way, so their RMSNorm factors agree
+// bit for bit.  (te_rmsnorm_f32, ops.c:272-293, sums in fp64 in index order.)
+__device__ __forceinline__ double row_sum_squares(double ss) {
+    __shared__ double part[kActThreads / 64];
+    for (int off = 32; off > 0; off >>= 1) {
+        ss += __shfl_xor(ss, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < kActThreads / 64; ++w) {
+        t += part[w];
+    }
+    return t;
+}
+
+// x' = pre(x), then digits and block scales.  Thread t of a workgroup holds
+// eight consecutive values of block t / 4 of a pass of 64 blocks; without a
+// row-wide norm the gridDim.y workgroups of a row take every gridDim.y-th
+// pass, else one workgroup takes the row (the norm's sum first, then the
+// digits from a second read of the row).
 // planes: hi and lo, int8 in 32 x 32 tiles [M/32][K/32][32][32]; scales [M][K/32] fp32.
-// The kernel is bound by load latency, not bandwidth: loads are issued
-// together ahead of their use.
+// `vec`: every pointer 16-byte aligned (16-byte loads, 8-byte digit stores).
+constexpr int kActPass = kActThreads * 8;
 template <int PRE>
 __global__ __launch_bounds__(kActThreads) void quant_act_kernel(const float *__restrict__ x,
                                                                 const float *__restrict__ x2,
                                                                 const float *__restrict__ norm_w, float eps,
                                                                 int K, int8_t *__restrict__ hi,
                                                                 int8_t *__restrict__ lo,
-                                                                float *__restrict__ scales) {
+                                                                float *__restrict__ scales, bool vec) {
     const size_t row = blockIdx.x;
     const float *xr = x + row * (size_t)K;
+    const int c0 = 8 * (int)threadIdx.x;
     float rms = 1.0f;
     if (PRE == kActRmsNorm) {
-        // te_rmsnorm_f32 (ops.c:272-293): fp64 sum of squares, 1 / sqrtf(mean + eps);
-        // each thread sums its values in index order, eight loads in flight
-        __shared__ double part[kActThreads / 64];
         double ss = 0.0;
-        int i = threadIdx.x;
-        for (; i + 7 * kActThreads < K; i += 8 * kActThreads) {
+        for (int c = c0; c < K; c += kActPass) {
             float v[8];
+            load8(xr + c, vec, v);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                v[u] = xr[i + u * kActThreads];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const double d = (double)v[u];
+            for (int j = 0; j < 8; ++j) {
+                const double d = (double)v[j];
                 ss += d * d;
             }
         }
-        for (; i < K; i += kActThreads) {
-            const double d = (double)xr[i];
-            ss += d * d;
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            ss += __shfl_xor(ss, off);
-        }
-        if ((threadIdx.x & 63) == 0) {
-            part[threadIdx.x >> 6] = ss;
-        }
-        __syncthreads();
-        double t = 0.0;
-        for (int w = 0; w < kActThreads / 64; ++w) {
-            t += part[w];
-        }
-        rms = 1.0f / sqrtf((float)(t / (double)K) + eps);
+        rms = 1.0f / sqrtf((float)(row_sum_squares(ss) / (double)K) + eps);
     }
-    // one 32-value block per half wave: lane j of the half takes value j;
-    // workgroup blockIdx.y of gridDim.y takes every gridDim.y-th group of
-    // blocks, four blocks' loads at a time
-    const int lane = threadIdx.x & 31;
-    const int halves = kActThreads / 32 * gridDim.y;
-    const int nblk = K / 32;
-    for (int b = (threadIdx.x >> 5) + blockIdx.y * (kActThreads / 32); b < nblk; b += 4 * halves) {
-        float v[4], w2[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int bb = b + u * halves;
-            v[u] = 0.0f;
-            w2[u] = 0.0f;
-            if (bb < nblk) {  // uniform per half wave
-                const int i = bb * 32 + lane;
-                v[u] = xr[i];
-                if (PRE == kActRmsNorm) {
-                    w2[u] = norm_w[i];
-                } else if (PRE == kActSwiGLU) {
-                    w2[u] = x2[row * (size_t)K + i];
-                }
-            }
+    for (int c = c0 + blockIdx.y * kActPass; c < K; c += kActPass * gridDim.y) {
+        float v[8], w2[8];
+        load8(xr + c, vec, v);
+        if (PRE == kActRmsNorm) {
+            load8(norm_w + c, vec, w2);
+        } else if (PRE == kActSwiGLU) {
+            load8(x2 + row * (size_t)K + c, vec, w2);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int bb = b + u * halves;
-            if (bb < nblk) {
-                float y = v[u];
-                if (PRE == kActRmsNorm) {
-                    y = y * rms * w2[u];
-                } else if (PRE == kActSwiGLU) {
-                    y = y / (1.0f + expf(-y)) * w2[u];  // te_swiglu_f32 (ops.c:397-405)
-                }
-                quant_block(y, row, K, bb, lane, hi, lo, scales);
+        for (int j = 0; j < 8; ++j) {
+            if (PRE == kActRmsNorm) {
+                v[j] = v[j] * rms * w2[j];
+            } else if (PRE == kActSwiGLU) {
+                v[j] = v[j] / (1.0f + expf(-v[j])) * w2[j];  // te_swiglu_f32 (ops.c:397-405)
             }
         }
+        quant_block8(v, row, K, c >> 5, threadIdx.x & 3, hi, lo, scales, vec);
     }
 }
 
@@ -580,117 +646,170 @@ __global__ __launch_bounds__(256) void gemm_q2_kernel(GemmSegsArg sg, size_t row
     }
 }
 
+// part[0][i] + part[1][i] + ... + part[splits-1][i], added in split order,
+// for W consecutive elements at i (W = 4: 16-byte loads); the splits' loads
+// are issued eight at a time.
+template <int W>
+struct Vals {
+    float v[W];
+};
+template <int W>
+__device__ __forceinline__ Vals<W> load_vals(const float *p) {
+    Vals<W> r;
+    if constexpr (W == 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(p);
+        r.v[0] = a.x, r.v[1] = a.y, r.v[2] = a.z, r.v[3] = a.w;
+    } else {
+        r.v[0] = *p;
+    }
+    return r;
+}
+template <int W>
+__device__ __forceinline__ void store_vals(float *p, const Vals<W> &r) {
+    if constexpr (W == 4) {
+        *reinterpret_cast<float4 *>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+    } else {
+        *p = r.v[0];
+    }
+}
+template <int W>
+__device__ __forceinline__ Vals<W> sum_splits(const float *__restrict__ part, int splits, size_t count, size_t i) {
+    Vals<W> a = load_vals<W>(part + i);
+    for (int z0 = 1; z0 < splits; z0 += 8) {
+        Vals<W> b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (z0 + u < splits) {
+                b[u] = load_vals<W>(part + (size_t)(z0 + u) * count + i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (z0 + u < splits) {
+#pragma unroll
+                for (int j = 0; j < W; ++j) {
+                    a.v[j] += b[u].v[j];
+                }
+            }
+        }
+    }
+    return a;
+}
+
 // out = (resid +) the splits' partial sums, added in split order, for every
-// segment of a segmented launch (element i of the [segment][M][n] order).
+// segment of a segmented launch (element i of the [segment][M][n] order),
+// W elements per thread (W = 4: every pointer 16-byte aligned and every
+// segment boundary M * n_off a multiple of 4, so four elements never straddle
+// one).
+template <int W>
 __global__ __launch_bounds__(256) void gemm_reduce_segs_kernel(const float *__restrict__ part, int splits, int M,
                                                                GemmSegsArg sg) {
     const size_t count = (size_t)M * sg.n_off[sg.nseg];
-    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
+    for (size_t i = (blockIdx.x * (size_t)256 + threadIdx.x) * W; i < count; i += (size_t)gridDim.x * 256 * W) {
         int seg = 0;
 #pragma unroll
         for (int t = 1; t < kMaxGemmSegs; ++t) {
             seg += (t < sg.nseg && i >= (size_t)M * sg.n_off[t]) ? 1 : 0;
         }
-        float a = part[i];
-        for (int z = 1; z < splits; ++z) {
-            a += part[(size_t)z * count + i];
-        }
+        Vals<W> a = sum_splits<W>(part, splits, count, i);
         const size_t j = i - (size_t)M * sg.n_off[seg];
-        sg.out[seg][j] = sg.resid[seg] != nullptr ? sg.resid[seg][j] + a : a;
+        if (sg.resid[seg] != nullptr) {
+            const Vals<W> r = load_vals<W>(sg.resid[seg] + j);
+#pragma unroll
+            for (int k = 0; k < W; ++k) {
+                a.v[k] = r.v[k] + a.v[k];
+            }
+        }
+        store_vals<W>(sg.out[seg] + j, a);
     }
 }
 
 // gemm_reduce_kernel's sums for one row (resid + the splits' partial sums in
 // split order -> out), then that row's RMSNorm digits into hi / lo / scales,
 // exactly as quant_act_kernel<kActRmsNorm> computes them from out: thread t
-// holds columns t + 256 u, summed into the fp64 sum of squares in that order,
-// which are the values lane t % 32 of half wave t / 32 quantizes for blocks
-// t / 32 + 8 u.  One workgroup per row, N <= kRmsCache * 256, N % 32 == 0,
-// splits <= kRmsSplits.  Every load is issued before the first store (out may
-// be resid), so all of a thread's loads are in flight together.
-constexpr int kRmsCache = 8;
+// holds columns 8t .. 8t + 7, summed into the fp64 sum of squares in
+// row_sum_squares's order, and quantizes them as quant_act_kernel's thread t
+// does.  One workgroup per row, N <= kActPass, N % 32 == 0,
+// splits <= kRmsSplits.  Every load, the norm weights' included, is issued
+// before the first store (out may be resid), so all of a thread's loads are
+// in flight together.
 constexpr int kRmsSplits = 8;
 __global__ __launch_bounds__(kActThreads) void gemm_reduce_rms_kernel(const float *__restrict__ part, int splits,
                                                                       size_t count, const float *resid, float *out,
                                                                       int N, const float *__restrict__ norm_w,
                                                                       float eps, int8_t *__restrict__ hi,
                                                                       int8_t *__restrict__ lo,
-                                                                      float *__restrict__ scales) {
+                                                                      float *__restrict__ scales, bool vec) {
     const size_t row = blockIdx.x;
-    const int tid = threadIdx.x;
-    float pv[kRmsCache][kRmsSplits];
-    float rv[kRmsCache];
+    const int c = 8 * (int)threadIdx.x;
+    const bool mine = c < N;
+    const int cl = mine ? c : 0;  // threads past the row load column 0 and store nothing
+    const size_t o = row * (size_t)N + cl;
+    float pv[kRmsSplits][8], rv[8] = {}, wv[8];
 #pragma unroll
-    for (int u = 0; u < kRmsCache; ++u) {
-        const int i = tid + kActThreads * u;
-        const size_t o = row * (size_t)N + i;
-        rv[u] = 0.0f;
-#pragma unroll
-        for (int z = 0; z < kRmsSplits; ++z) {
-            pv[u][z] = i < N && z < splits ? part[(size_t)z * count + o] : 0.0f;
-        }
-        if (i < N && resid != nullptr) {
-            rv[u] = resid[o];
+    for (int z = 0; z < kRmsSplits; ++z) {
+        if (z < splits) {
+            load8(part + (size_t)z * count + o, vec, pv[z]);
         }
     }
-    float xv[kRmsCache];
+    if (resid != nullptr) {
+        load8(resid + o, vec, rv);
+    }
+    load8(norm_w + cl, vec, wv);
+    float xv[8];
     double ss = 0.0;
 #pragma unroll
-    for (int u = 0; u < kRmsCache; ++u) {
-        const int i = tid + kActThreads * u;
-        float a = pv[u][0];
+    for (int j = 0; j < 8; ++j) {
+        float a = pv[0][j];
 #pragma unroll
         for (int z = 1; z < kRmsSplits; ++z) {
             if (z < splits) {
-                a += pv[u][z];
+                a += pv[z][j];
             }
         }
-        const float x = resid != nullptr ? rv[u] + a : a;
-        xv[u] = x;
-        if (i < N) {
-            out[row * (size_t)N + i] = x;
-            const double d = (double)x;
-            ss += d * d;
-        }
+        xv[j] = resid != nullptr ? rv[j] + a : a;
+        const double d = (double)xv[j];
+        ss += mine ? d * d : 0.0;
     }
-    __shared__ double sum_part[kActThreads / 64];
-    for (int off = 32; off > 0; off >>= 1) {
-        ss += __shfl_xor(ss, off);
+    if (mine) {
+        store8(out + o, vec, xv);
     }
-    if ((tid & 63) == 0) {
-        sum_part[tid >> 6] = ss;
-    }
-    __syncthreads();
-    double t = 0.0;
-    for (int w = 0; w < kActThreads / 64; ++w) {
-        t += sum_part[w];
-    }
-    const float rms = 1.0f / sqrtf((float)(t / (double)N) + eps);
-    const int lane = tid & 31;
+    const float rms = 1.0f / sqrtf((float)(row_sum_squares(ss) / (double)N) + eps);
+    if (mine) {
 #pragma unroll
-    for (int u = 0; u < kRmsCache; ++u) {
-        const int bb = (tid >> 5) + (kActThreads / 32) * u;
-        if (bb < N / 32) {  // uniform per half wave
-            quant_block(xv[u] * rms * norm_w[bb * 32 + lane], row, N, bb, lane, hi, lo, scales);
+        for (int j = 0; j < 8; ++j) {
+            xv[j] = xv[j] * rms * wv[j];
         }
+        quant_block8(xv, row, N, c >> 5, threadIdx.x & 3, hi, lo, scales, vec);
     }
 }
 
-// out = (resid +) the splits' partial sums, added in split order.
+// out = (resid +) the splits' partial sums, added in split order, W
+// elements per thread (W = 4: count % 4 == 0 and every pointer 16-byte
+// aligned).
+template <int W>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int splits, size_t count,
                                                           const float *resid, float *out) {
-    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
-        float a = part[i];
-        for (int z = 1; z < splits; ++z) {
-            a += part[(size_t)z * count + i];
+    for (size_t i = (blockIdx.x * (size_t)256 + threadIdx.x) * W; i < count; i += (size_t)gridDim.x * 256 * W) {
+        Vals<W> a = sum_splits<W>(part, splits, count, i);
+        if (resid != nullptr) {
+            const Vals<W> r = load_vals<W>(resid + i);
+#pragma unroll
+            for (int k = 0; k < W; ++k) {
+                a.v[k] = r.v[k] + a.v[k];
+            }
         }
-        out[i] = resid != nullptr ? resid[i] + a : a;
+        store_vals<W>(out + i, a);
     }
 }
 
 }  // namespace
 
 namespace te_hip {
+
+static bool aligned16(const void *p) {
+    return ((uintptr_t)p & 15u) == 0;
+}
 
 // digit planes padded to whole 32-row tiles
 static size_t plane_bytes(size_t rows, size_t cols) {
@@ -710,14 +829,17 @@ te_status launch_quant_act(int pre, const float *x, const float *x2, const float
     int8_t *hi = static_cast<int8_t *>(act);
     int8_t *lo = hi + planes;
     float *scales = reinterpret_cast<float *>(lo + planes);
-    // without a row-wide norm, several workgroups share a long row
-    const dim3 grid((unsigned)rows, pre == kActRmsNorm ? 1u : (unsigned)std::max<size_t>(1, cols / 32 / 64));
+    const bool vec = aligned16(x) && aligned16(act) && (pre != kActSwiGLU || aligned16(x2)) &&
+                     (pre != kActRmsNorm || aligned16(norm_w));
+    // without a row-wide norm, the row's passes of kActPass values are spread over workgroups
+    const dim3 grid((unsigned)rows, pre == kActRmsNorm ? 1u : (unsigned)std::max<size_t>(1, cols / kActPass));
     if (pre == kActRmsNorm) {
-        quant_act_kernel<kActRmsNorm><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
+        quant_act_kernel<kActRmsNorm>
+            <<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales, vec);
     } else if (pre == kActSwiGLU) {
-        quant_act_kernel<kActSwiGLU><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
+        quant_act_kernel<kActSwiGLU><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales, vec);
     } else {
-        quant_act_kernel<kActPlain><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales);
+        quant_act_kernel<kActPlain><<<grid, kActThreads, 0, stream>>>(x, x2, norm_w, eps, (int)cols, hi, lo, scales, vec);
     }
     return launch_status();
 }
@@ -832,21 +954,32 @@ te_status launch_gemm_q_segs(uint32_t ggml_type, const GemmSeg *segs, int nseg, 
     bool digits_done = false;
     if (splits > 1) {
         const size_t count = rows * n_total;
-        const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
+        bool vec = aligned16(partials) && count % 4 == 0;
+        for (int i = 0; i < nseg; ++i) {
+            vec = vec && aligned16(sg.out[i]) && aligned16(sg.resid[i]) && (rows * (size_t)sg.n_off[i + 1]) % 4 == 0;
+        }
+        const int width = vec ? 4 : 1;
+        const unsigned blocks = (unsigned)std::min<size_t>((count / width + 255) / 256, 4096);
         const char *env = getenv("TE_HIP_GEMM_REDUCE_RMS");
-        if (rms && n <= (size_t)kRmsCache * kActThreads && splits <= (size_t)kRmsSplits &&
-            !(env != nullptr && env[0] == '0')) {
+        if (rms && n <= (size_t)kActPass && splits <= (size_t)kRmsSplits && !(env != nullptr && env[0] == '0')) {
             const size_t planes_out = plane_bytes(rows, n);
             int8_t *ohi = static_cast<int8_t *>(post->act_out);
             int8_t *olo = ohi + planes_out;
             float *osc = reinterpret_cast<float *>(olo + planes_out);
             gemm_reduce_rms_kernel<<<(unsigned)rows, kActThreads, 0, stream>>>(
-                partials, (int)splits, count, res, out, (int)n, post->norm_w, post->eps, ohi, olo, osc);
+                partials, (int)splits, count, res, out, (int)n, post->norm_w, post->eps, ohi, olo, osc,
+                vec && aligned16(post->norm_w) && aligned16(post->act_out));
             digits_done = true;
         } else if (nseg == 1) {
-            gemm_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, count, res, out);
+            if (vec) {
+                gemm_reduce_kernel<4><<<blocks, 256, 0, stream>>>(partials, (int)splits, count, res, out);
+            } else {
+                gemm_reduce_kernel<1><<<blocks, 256, 0, stream>>>(partials, (int)splits, count, res, out);
+            }
+        } else if (vec) {
+            gemm_reduce_segs_kernel<4><<<blocks, 256, 0, stream>>>(partials, (int)splits, (int)rows, sg);
         } else {
-            gemm_reduce_segs_kernel<<<blocks, 256, 0, stream>>>(partials, (int)splits, (int)rows, sg);
+            gemm_reduce_segs_kernel<1><<<blocks, 256, 0, stream>>>(partials, (int)splits, (int)rows, sg);
         }
     }
     te_status st = launch_status();
