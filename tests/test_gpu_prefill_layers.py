@@ -151,6 +151,38 @@ def test_prefill_paired_gate_up_gemm_bits(ggml_type, monkeypatch):
     assert np.isfinite(outs[0]).all() and np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
+@pytest.mark.parametrize("batch,base", [(300, 3), (512, 0), (70, 5)])
+def test_prefill_attention_digits_in_kernel_bits(batch, base, monkeypatch):
+    """The attention kernel's own digits of its output rows (the default)
+    against fp32 rows and the separate digits launch (TE_HIP_PREFILL_DIGITS=0):
+    the same output bits.  300 and 512 rows after 3 / 0 cached positions take
+    the 128-row tile kernel (300: a ragged last tile), 70 after 5 the rows
+    kernel (at most 256 keys)."""
+    layers, heads, kv_heads, head_dim, ffn = 2, 4, 2, 128, 512
+    ctx = base + batch
+    m = S.synthetic_model(94, 2, layers, heads, kv_heads, head_dim, ffn, 64, ctx, base)
+    hidden = m["hidden"]
+    cos, sin = A.rope_table(ctx, head_dim, 1.0e6)
+    x_in = _dev(S.normal(94, "rows", (batch, hidden)))
+    outs = []
+    for mode in ("1", "0"):
+        monkeypatch.setenv("TE_HIP_PREFILL_DIGITS", mode)
+        kc, vc = _dev(m["key_cache"]), _dev(m["value_cache"])
+        vt = A.value_t_buffer(1, layers, ctx, kv_heads, head_dim)
+        A.value_transpose(vc.view(torch.float16).reshape(1, layers, ctx, kv_heads, head_dim), vt,
+                          first_position=0, count=base)
+        got = LY.prefill_all_layers(_dev(m["mapping"]), m["offsets"], layers, 2, x_in.clone(),
+                                    _dev(m["attn_norm"]), _dev(m["ffn_norm"]), _dev(m["q_bias"]), _dev(m["k_bias"]),
+                                    _dev(m["v_bias"]), cos.contiguous(), sin.contiguous(), kc, vc, vt, base, ctx,
+                                    heads, kv_heads, head_dim, ffn, 1e-6)
+        torch.cuda.synchronize()
+        outs.append((got.cpu().numpy(), kc.cpu().numpy()))
+    print(f"rows {batch} after {base}: in-kernel vs separate digits max |diff| "
+          f"{np.abs(outs[0][0] - outs[1][0]).max():.3g}")
+    assert np.isfinite(outs[0][0]).all()
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
 def test_prefill_layer_by_layer(oracle_mod):
     """te_hip_prefill_layer_f16 once per layer: the same result as the all-layers flow."""
     _run(oracle_mod, 8, layers=2, heads=4, kv_heads=2, head_dim=64, ffn=256, ctx=48, base=5, batch=17,

@@ -95,8 +95,9 @@ __device__ __forceinline__ void quant_block8(const float (&v)[8], size_t row, in
     for (int j = 1; j < 8; ++j) {
         m = fmaxf(m, fabsf(v[j]));
     }
-    m = fmaxf(m, __shfl_xor(m, 1, 4));
-    m = fmaxf(m, __shfl_xor(m, 2, 4));
+    // the quad's maximum by DPP moves (lanes xor 1, then xor 2)
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
     int q[8] = {};
     float s;
     if (!(m <= FLT_MAX)) {  // inf or NaN in the block: its products are NaN
@@ -114,11 +115,12 @@ __device__ __forceinline__ void quant_block8(const float (&v)[8], size_t row, in
         s = ldexpf(1.0f, -e);
     }
     uint32_t h[2] = {0, 0}, l[2] = {0, 0};
+    // q = 256 * hi + lo with lo in [-128, 127]: hi = (q + 128) >> 8, and lo's
+    // byte is q's low byte
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int l8 = ((q[j] + 128) & 255) - 128;
-        h[j >> 2] |= (uint32_t)(((q[j] - l8) >> 8) & 255) << (8 * (j & 3));
-        l[j >> 2] |= (uint32_t)(l8 & 255) << (8 * (j & 3));
+        h[j >> 2] |= (uint32_t)(((q[j] + 128) >> 8) & 255) << (8 * (j & 3));
+        l[j >> 2] |= (uint32_t)(q[j] & 255) << (8 * (j & 3));
     }
     const size_t t = (((row >> 5) * (size_t)(K >> 5) + b) << 10) + ((row & 31) << 5) + 8 * g;
     if (vec) {
@@ -814,6 +816,10 @@ static bool aligned16(const void *p) {
 // digit planes padded to whole 32-row tiles
 static size_t plane_bytes(size_t rows, size_t cols) {
     return (rows + 31) / 32 * 32 * cols;
+}
+
+size_t act_plane_bytes(size_t rows, size_t cols) {
+    return plane_bytes(rows, cols);
 }
 
 size_t act_buffer_bytes(size_t rows, size_t cols) {

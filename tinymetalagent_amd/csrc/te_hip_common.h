@@ -122,6 +122,9 @@ te_status launch_dequant_rows(const void *weights, uint32_t ggml_type, size_t co
 // out[m][n] = sum_k act[m][k] W[n][k] (+ resid[m][n]) for a Q4_0 / Q8_0
 // weight tensor W [n][k] at a 2-byte aligned address.
 size_t act_buffer_bytes(size_t rows, size_t cols);
+// The layout inside `act`: the hi plane at act, the lo plane at
+// act + act_plane_bytes(rows, cols), the fp32 block scales after the lo plane.
+size_t act_plane_bytes(size_t rows, size_t cols);
 te_status launch_quant_act(int pre, const float *x, const float *x2, const float *norm_w, float eps, size_t rows,
                            size_t cols, void *act, hipStream_t stream);
 // `partials` (partial_bytes, may be NULL) lets small output grids split K.
@@ -164,6 +167,20 @@ te_status launch_gemm_q_rms(const void *weights, uint32_t ggml_type, const void 
 // any size.
 te_status launch_gemm_glu_q(uint32_t ggml_type, const void *gate_w, const void *up_w, const void *act, size_t rows,
                             size_t n, size_t k, void *act_out, hipStream_t stream, bool *launched);
+
+// te_hip_attention_prefill_step_vt_f16 (te_prefill.hip; arguments as there)
+// with the attention output as the next GEMM's digits: with act_out set, the
+// launch_quant_act(0) digits of the output rows [seqs*layers*tokens][heads *
+// head_dim] go to act_out (act_buffer_bytes of that shape), formed by the
+// attention kernel from the rows it holds, and `out` is not written.  Only
+// without a key split (workspace NULL or one split): else UNSUPPORTED.
+te_status launch_prefill_step_vt(const float *query, const float *k_new, const float *v_new, const float *q_bias,
+                                 const float *k_bias, const float *v_bias, const float *rope_cos,
+                                 const float *rope_sin, uint16_t *key_cache, uint16_t *value_cache,
+                                 uint16_t *value_cache_t, size_t seqs, size_t layers, size_t tokens,
+                                 size_t base_position, size_t context_tokens, size_t heads, size_t kv_heads,
+                                 size_t head_dim, float *out, void *act_out, void *workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
 
 // One weight matrix of a fused GEMV launch: out[r] = W[r] . x' (+ resid[r] when
 // resid is set; resid may equal out), r < rows.

@@ -104,10 +104,68 @@ struct PrefillArgs {
     int splits;      // key splits: blockIdx.z = (seq*layers + layer) * splits + split
     float *part_o;   // splits > 1: unnormalised O per (split, seq*layer, row, head), else null
     float *part_ml;  // splits > 1: (m, l) per (split, seq*layer, row, head)
+    // one split only: the output rows as the next GEMM's digits (hi / lo
+    // planes in 32 x 32 tiles, fp32 block scales; te_gemm.hip's layout)
+    // instead of fp32 rows; null: fp32 rows to `out`
+    int8_t *dhi;
+    int8_t *dlo;
+    float *dscales;
 #ifdef TE_PREFILL_PHASES
     unsigned *phase_log;  // [workgroup][wave][kPhases]: shader-clock cycles per phase, summed
 #endif
 };
+
+// Four consecutive output values (columns col .. col + 3 of `row`, col % 4
+// == 0) as digits: the eight lanes holding one 32-value block (lanes 8j ..
+// 8j + 7, every lane of the wave taking part) share its largest magnitude,
+// then each value becomes v = 256 * hi + lo at the block's scale -- the
+// arithmetic of te_gemm.hip's quant_act_kernel<kActPlain>, so the digits are
+// the ones that kernel makes from the fp32 rows.  K = the row length (heads *
+// D); only `store` lanes write.
+__device__ __forceinline__ void store_digits4(const f32x4 &v, size_t row, int K, int col, int8_t *__restrict__ hi,
+                                              int8_t *__restrict__ lo, float *__restrict__ scales, bool store) {
+    // the eight lanes' maximum by DPP moves (no LDS round trip): lanes xor 1
+    // and xor 2 within each quad, then the half-row mirror (lane i <-> 7 - i)
+    // joins the two quads
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+    if (!store) {
+        return;
+    }
+    int q[4] = {0, 0, 0, 0};
+    float s;
+    if (!(m <= __FLT_MAX__)) {  // inf or NaN in the block: its products are NaN
+        s = __builtin_nanf("");
+    } else if (m == 0.0f) {
+        s = 0.0f;
+    } else {
+        int E;
+        (void)frexpf(m, &E);
+        const int e = min(14 - E, 126);  // blocks below 2^-112 round towards 0
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            q[j] = (int)rintf(ldexpf(v[j], e));
+        }
+        s = ldexpf(1.0f, -e);
+    }
+    // q = 256 * hi + lo with lo in [-128, 127]: hi = (q + 128) >> 8, and lo's
+    // byte is q's low byte
+    uint32_t h = 0, l = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h |= (uint32_t)(((q[j] + 128) >> 8) & 255) << (8 * j);
+        l |= (uint32_t)(q[j] & 255) << (8 * j);
+    }
+    const int b = col >> 5;
+    const size_t t = (((row >> 5) * (size_t)(K >> 5) + b) << 10) + ((row & 31) << 5) + (col & 31);
+    *reinterpret_cast<uint32_t *>(hi + t) = h;
+    *reinterpret_cast<uint32_t *>(lo + t) = l;
+    if ((col & 31) == 0) {
+        scales[row * (size_t)(K >> 5) + b] = s;
+    }
+}
 
 // Phase instrumentation (a build with -DTE_PREFILL_PHASES only, see
 // build.py --phases and bench.py --phases): each wave sums s_memtime deltas
@@ -817,6 +875,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_causal_f16_kernel(Prefill
             // a 32-bit float offset from the block's first row (16 rows of
             // heads * D floats)
             const int row0 = wr0 + 16 * nb;
+            if constexpr (Q32) {
+                if (a.dhi != nullptr) {  // the fused step's rows as digits (uniform)
+#pragma unroll
+                    for (int i = 0; i < NS; ++i) {
+                        const int r = i * (64 / LPR) + r0;
+                        store_digits4(v[i], (size_t)sl * a.tokens + row0 + r, a.heads * D, h * D + 4 * q, a.dhi,
+                                      a.dlo, a.dscales, row0 + r < a.tokens);
+                    }
+                    return;
+                }
+            }
             float *orow = a.out + (((size_t)sl * a.tokens + row0) * a.heads + h) * D;
             const unsigned rstride = (unsigned)a.heads * D;
             // non-temporal: the output is not read back by this launch
@@ -1198,7 +1267,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_rows_f16_kernel(PrefillAr
         for (int p = 1; p < nact; ++p) {
             acc += *reinterpret_cast<const f32x4 *>(&part[p][r * OPITCH + 4 * q]);
         }
-        if (r0 + r < a.tokens) {
+        if (a.dhi != nullptr) {  // uniform
+            store_digits4(acc, (size_t)sl * a.tokens + r0 + r, a.heads * D, h * D + 4 * q, a.dhi, a.dlo, a.dscales,
+                          r0 + r < a.tokens);
+        } else if (r0 + r < a.tokens) {
             float *orow = a.out + (((size_t)sl * a.tokens + r0 + r) * a.heads + h) * D;
             __builtin_nontemporal_store(acc, reinterpret_cast<f32x4 *>(orow + 4 * q));
         }
@@ -1500,16 +1572,22 @@ te_status check_prefill_args(size_t seqs, size_t layers, size_t tokens, size_t b
 }
 
 // The attention over V^T with `splits` key splits (workspace = the partials),
-// then the merge launch when splits > 1.
+// then the merge launch when splits > 1.  With act_out (the fused step, one
+// split only): the output rows as digits, formed in the attention kernel.
 te_status run_prefill(PrefillArgs a, int splits, void *partials, size_t seqs, size_t layers, size_t tokens,
                       size_t base_position, size_t context_tokens, size_t heads, size_t kv_heads, size_t head_dim,
-                      float *out, hipStream_t strm) {
+                      float *out, hipStream_t strm, void *act_out = nullptr) {
     a.out = out;
     a.splits = splits;
     if (splits > 1) {
         const size_t parts = (size_t)splits * seqs * layers * tokens * heads;
         a.part_o = static_cast<float *>(partials);
         a.part_ml = a.part_o + parts * head_dim;
+    } else if (act_out != nullptr) {
+        const size_t planes = te_hip::act_plane_bytes(seqs * layers * tokens, heads * head_dim);
+        a.dhi = static_cast<int8_t *>(act_out);
+        a.dlo = a.dhi + planes;
+        a.dscales = reinterpret_cast<float *>(a.dlo + planes);
     }
     te_status st = launch_prefill(a, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads, head_dim,
                                   strm);
@@ -1618,14 +1696,13 @@ extern "C" te_status te_hip_attention_prefill_vt_f16(
                        head_dim, out, te_hip::as_stream(stream));
 }
 
-extern "C" te_status te_hip_attention_prefill_step_vt_f16(
-    const float *query, const float *k_new, const float *v_new,
-    const float *q_bias, const float *k_bias, const float *v_bias,
-    const float *rope_cos, const float *rope_sin,
-    uint16_t *key_cache, uint16_t *value_cache, uint16_t *value_cache_t,
-    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
-    size_t heads, size_t kv_heads, size_t head_dim,
-    float *out, void *workspace, size_t workspace_bytes, void *stream) {
+te_status te_hip::launch_prefill_step_vt(const float *query, const float *k_new, const float *v_new,
+                                         const float *q_bias, const float *k_bias, const float *v_bias,
+                                         const float *rope_cos, const float *rope_sin, uint16_t *key_cache,
+                                         uint16_t *value_cache, uint16_t *value_cache_t, size_t seqs, size_t layers,
+                                         size_t tokens, size_t base_position, size_t context_tokens, size_t heads,
+                                         size_t kv_heads, size_t head_dim, float *out, void *act_out,
+                                         void *workspace, size_t workspace_bytes, hipStream_t strm) {
     if (query == nullptr || k_new == nullptr || v_new == nullptr || rope_cos == nullptr || rope_sin == nullptr ||
         key_cache == nullptr || value_cache == nullptr || value_cache_t == nullptr || out == nullptr) {
         return TE_STATUS_INVALID_ARGUMENT;
@@ -1638,7 +1715,7 @@ extern "C" te_status te_hip_attention_prefill_step_vt_f16(
         return TE_STATUS_UNSUPPORTED;
     }
     if (!al16(query) || !al16(q_bias) || !al16(rope_cos) || !al16(rope_sin) || !al16(key_cache) ||
-        !al16(value_cache) || !al16(value_cache_t) || !al16(out) || !al16(workspace)) {
+        !al16(value_cache) || !al16(value_cache_t) || !al16(out) || !al16(workspace) || !al16(act_out)) {
         return TE_STATUS_UNSUPPORTED;
     }
     const int splits = splits_for(workspace, workspace_bytes, seqs, layers, tokens, base_position, heads, head_dim,
@@ -1646,7 +1723,9 @@ extern "C" te_status te_hip_attention_prefill_step_vt_f16(
     if (st != TE_STATUS_OK) {
         return st;
     }
-    hipStream_t strm = te_hip::as_stream(stream);
+    if (act_out != nullptr && splits != 1) {
+        return TE_STATUS_UNSUPPORTED;  // the digits come from the one-split kernels only
+    }
     if (al16(k_new) && al16(v_new)) {
         // bias + RoPE + fp16 append of k / v and the chunk's V^T rows: one launch
         st = te_hip::launch_kv_append_vt(k_new, v_new, k_bias, v_bias, rope_cos, rope_sin, key_cache, value_cache,
@@ -1674,7 +1753,21 @@ extern "C" te_status te_hip_attention_prefill_step_vt_f16(
     a.key_cache = reinterpret_cast<const f16 *>(key_cache);
     a.value_t = reinterpret_cast<const f16 *>(value_cache_t);
     return run_prefill(a, splits, workspace, seqs, layers, tokens, base_position, context_tokens, heads, kv_heads,
-                       head_dim, out, strm);
+                       head_dim, out, strm, act_out);
+}
+
+extern "C" te_status te_hip_attention_prefill_step_vt_f16(
+    const float *query, const float *k_new, const float *v_new,
+    const float *q_bias, const float *k_bias, const float *v_bias,
+    const float *rope_cos, const float *rope_sin,
+    uint16_t *key_cache, uint16_t *value_cache, uint16_t *value_cache_t,
+    size_t seqs, size_t layers, size_t tokens, size_t base_position, size_t context_tokens,
+    size_t heads, size_t kv_heads, size_t head_dim,
+    float *out, void *workspace, size_t workspace_bytes, void *stream) {
+    return te_hip::launch_prefill_step_vt(query, k_new, v_new, q_bias, k_bias, v_bias, rope_cos, rope_sin, key_cache,
+                                          value_cache, value_cache_t, seqs, layers, tokens, base_position,
+                                          context_tokens, heads, kv_heads, head_dim, out, nullptr, workspace,
+                                          workspace_bytes, te_hip::as_stream(stream));
 }
 
 // ---- entry points over the plain value cache: V^T is built per call --------

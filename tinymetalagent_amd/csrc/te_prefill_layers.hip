@@ -202,6 +202,8 @@ static te_status prefill_all_layers_impl(
         return TE_STATUS_INVALID_ARGUMENT;
     }
     const hipStream_t st = te_hip::as_stream(stream);
+    const char *digits_env = getenv("TE_HIP_PREFILL_DIGITS");
+    const bool attn_digits = !(digits_env != nullptr && digits_env[0] == '0');
     if (out != hidden_in &&
         hipMemcpyAsync(out, hidden_in, batch * hidden * sizeof(float), hipMemcpyDeviceToDevice, st) != hipSuccess) {
         return TE_STATUS_RUNTIME_ERROR;
@@ -265,15 +267,20 @@ static te_status prefill_all_layers_impl(
             !qkv_done((stage_name = "qkv_proj",
                        s = te_hip::launch_gemm_q_segs(ggml_type, qkv, 3, b.act, batch, hidden, b.part, b.part_bytes,
                                                       st))) ||
+            // the attention output leaves the attention kernel as the output
+            // projection's digits (TE_HIP_PREFILL_DIGITS=0: fp32 rows and a
+            // digits launch, the same bits)
             !done((stage_name = "qkv_bias_rope_flash_attention_mma_vt",
-                   s = te_hip_attention_prefill_step_vt_f16(
+                   s = te_hip::launch_prefill_step_vt(
                        b.q, b.k, b.v, q_biases + l * hidden, k_biases + l * kv, v_biases + l * kv, rope_cos, rope_sin,
                        key_cache + l * ctx_kv, value_cache + l * ctx_kv, value_cache_t + l * vt_layer, 1, 1, batch,
-                       base_position, context_tokens, heads, kv_heads, head_dim, b.attn, nullptr, 0, stream)),
+                       base_position, context_tokens, heads, kv_heads, head_dim, b.attn, attn_digits ? b.act : nullptr,
+                       nullptr, 0, st)),
                   te_hip::kProfAttention) ||
-            !done((stage_name = "attn_out_digits",
-                   s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st)),
-                  ew) ||
+            (!attn_digits &&
+             !done((stage_name = "attn_out_digits",
+                    s = te_hip::launch_quant_act(0, b.attn, nullptr, nullptr, 0.0f, batch, hidden, b.act, st)),
+                   ew)) ||
             !done((stage_name = "output_proj_add_ffn_norm_digits",
                    s = te_hip::launch_gemm_q_rms(m + output_offsets[l], ggml_type, b.act, batch, hidden, hidden, out,
                                                  out, b.part, b.part_bytes, ffn_norm_weights + l * hidden, epsilon,
