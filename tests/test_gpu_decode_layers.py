@@ -212,6 +212,13 @@ def test_decode_all_layers_merge_in_wo_vs_merge_launch(oracle_mod, monkeypatch, 
 
 
 def test_decode_all_layers_long_split_keeps_merge_launch(oracle_mod):
-    """Position 900: 15 chunks of 64 positions, past the Wo staging's 12, so
-    the step keeps its merge launch."""
+    """Position 900: past the Wo staging's 12 chunks, so the step keeps its
+    merge launch (29 one-tile chunks of 32 positions: the two layers' 116
+    tiles are within 3/4 of the CUs)."""
     _run(oracle_mod, 2, layers=2, heads=16, kv_heads=2, head_dim=128, ffn=512, vocab=300, ctx=960, position=900)
+
+
+def test_decode_all_layers_one_tile_chunks_3b_2k(oracle_mod):
+    """One 3B-shaped layer at position 2047: 64 one-tile chunks per KV head
+    (128 single-wave workgroups) and the merge launch."""
+    _run(oracle_mod, 2, layers=1, heads=16, kv_heads=2, head_dim=128, ffn=512, vocab=300, ctx=2048, position=2047)

@@ -660,6 +660,13 @@ DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t 
     // 8 resident waves per CU the registers allow run 4-8 % slower -- and a
     // short last chunk per stream costs a partly idle tail.  Balancing on the
     // total rather than the longest sequence keeps ragged batches even.
+    // A launch too small to fill the GPU (one layer's decode step) takes
+    // one-tile chunks instead where those stay within 3/4 of a workgroup per
+    // CU and two-tile chunks would exceed the kGemvMergeMaxChunks partials the
+    // decode-layer flow merges in its Wo projection (so that flow runs the
+    // merge launch either way): 3B Q4_0 decode token at 1K / 2K / 3K 1,309 ->
+    // 1,279 / ~1,318 -> ~1,293 / 1,332 -> 1,316 us; at 4K (one workgroup per
+    // CU) 1,327 against 1,344, so it stops below.
     // TE_HIP_DECODE_CHUNK (a multiple of 32) overrides the choice.
     DecodeGeometry g;
     size_t max_n = 0, total_tiles = 0;
@@ -669,15 +676,18 @@ DecodeGeometry decode_geometry(const size_t *positions, size_t position, size_t 
         total_tiles += layers * kv_heads * ((n + kTile - 1) / kTile);
     }
     const size_t target = (size_t)device_compute_units() * kTargetWaves2PerCU / 2;
-    size_t tiles = (total_tiles + target - 1) / target;
-    if (tiles < 2) {
-        tiles = 2;
-    }
     const size_t max_tiles = (max_n + kTile - 1) / kTile;
+    const bool one_tile = total_tiles * 4 <= (size_t)device_compute_units() * 3 &&
+                          (max_tiles + 1) / 2 > (size_t)kGemvMergeMaxChunks;
+    const size_t min_tiles = one_tile ? 1 : 2;
+    size_t tiles = (total_tiles + target - 1) / target;
+    if (tiles < min_tiles) {
+        tiles = min_tiles;
+    }
     const size_t n_longest = (max_tiles + tiles - 1) / tiles;  // chunks of the longest stream
     tiles = (max_tiles + n_longest - 1) / n_longest;           // equal chunks for it
-    if (tiles < 2) {
-        tiles = 2;
+    if (tiles < min_tiles) {
+        tiles = min_tiles;
     }
     size_t chunk = tiles * kTile;
     const char *env = getenv("TE_HIP_DECODE_CHUNK");
@@ -706,8 +716,11 @@ size_t decode_chunks_bound(size_t max_position, size_t layers, size_t kv_heads) 
     // M = its 32-position tiles, t0 = max(2, ceil(T / target)) and T >= layers *
     // kv_heads * M the total tiles; the later steps only lengthen the chunk.  So
     // n_longest <= ceil(M / 2) and n_longest <= ceil(target / (layers * kv_heads)),
-    // both non-decreasing in M.  With TE_HIP_DECODE_CHUNK the count is
-    // ceil(n / chunk) before the doubling that keeps it <= kMaxCombineChunks.
+    // both non-decreasing in M.  One-tile chunks give n_longest = M where
+    // layers * kv_heads * M <= T <= 3/4 of the CUs: at most
+    // min(M, 3/4 CUs / (layers * kv_heads)), also non-decreasing in M.  With
+    // TE_HIP_DECODE_CHUNK the count is ceil(n / chunk) before the doubling
+    // that keeps it <= kMaxCombineChunks.
     const size_t max_n = max_position + 1;
     const size_t m_tiles = (max_n + kTile - 1) / kTile;
     const char *env = getenv("TE_HIP_DECODE_CHUNK");
@@ -719,7 +732,8 @@ size_t decode_chunks_bound(size_t max_position, size_t layers, size_t kv_heads) 
     }
     const size_t target = (size_t)device_compute_units() * kTargetWaves2PerCU / 2;
     const size_t streams = layers * kv_heads;
-    const size_t b = std::min((m_tiles + 1) / 2, (target + streams - 1) / streams);
+    const size_t b = std::max(std::min((m_tiles + 1) / 2, (target + streams - 1) / streams),
+                              std::min(m_tiles, (size_t)device_compute_units() * 3 / 4 / streams));
     return std::min(std::max(b, (size_t)1), (size_t)kMaxCombineChunks);
 }
 
