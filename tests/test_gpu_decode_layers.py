@@ -213,8 +213,8 @@ def test_decode_all_layers_merge_in_wo_vs_merge_launch(oracle_mod, monkeypatch, 
 
 def test_decode_all_layers_long_split_keeps_merge_launch(oracle_mod):
     """Position 900: past the Wo staging's 12 chunks, so the step keeps its
-    merge launch (29 one-tile chunks of 32 positions: the two layers' 116
-    tiles are within 3/4 of the CUs)."""
+    merge launch (29 one-tile chunks of 32 positions: a layer's 58 tiles are
+    within 3/4 of the CUs)."""
     _run(oracle_mod, 2, layers=2, heads=16, kv_heads=2, head_dim=128, ffn=512, vocab=300, ctx=960, position=900)
 
 
