@@ -992,21 +992,17 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *values, uint3
             bi = i;
         }
     };
-    // ten 16-byte loads per thread and round, all issued before the compares:
-    // four rounds of memory latency for a 151936-entry vocabulary (four loads
-    // per round took ten rounds: 10.75 us)
-    constexpr int kBatch = 10;
     const uint32_t n4 = ((size_t)values & 15u) == 0 ? len / 4 : 0;
     const float4 *v4 = reinterpret_cast<const float4 *>(values);
-    for (uint32_t base = 0; base < n4; base += kBatch * 1024) {
-        float4 q[kBatch];
+    for (uint32_t base = 0; base < n4; base += 4 * 1024) {
+        float4 q[4];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int u = 0; u < 4; ++u) {  // all loads issued before the compares
             const uint32_t j = base + u * 1024 + threadIdx.x;
             q[u] = j < n4 ? v4[j] : make_float4(-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX);
         }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int u = 0; u < 4; ++u) {
             const uint32_t i = 4 * (base + u * 1024 + threadIdx.x);
             take(q[u].x, i);
             take(q[u].y, i + 1);
