@@ -495,10 +495,12 @@ def test_prefill_several_sequences_and_layers(oracle_mod):
     (2, 2, 14, 2, 64, 130, 37, True),
     (1, 2, 12, 2, 128, 200, 500, False),
 ])
-def test_prefill_step_fused_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens, base, bias):
+def test_prefill_step_fused_vs_oracle(oracle_mod, monkeypatch, seqs, layers, h, kv, d, tokens, base, bias):
     """te_hip_attention_prefill_step_f16 == rope_kv_append (with q_half) +
     prefill, per the oracle: cache slots bit-exact, outputs within the bar,
-    query/k/v untouched."""
+    query/k/v untouched.  The unfused launch it is compared with bit for bit
+    is forced to the kernel the fused step chooses (the rows kernel up to 512
+    keys for fp32 queries, 256 for fp16 ones)."""
     ctx = base + tokens + 3
     tag = f"pfs{h}{kv}{d}{tokens}{base}"
     q = S.normal(28, tag + "q", (seqs, layers, tokens, h, d), 1 / math.sqrt(d))
@@ -525,6 +527,7 @@ def test_prefill_step_fused_vs_oracle(oracle_mod, seqs, layers, h, kv, d, tokens
     assert np.array_equal(tq.cpu().numpy(), q) and np.array_equal(tk.cpu().numpy(), k)
     assert np.array_equal(tv.cpu().numpy(), v)
     # same output bits as the unfused kernel on the stored fp16 queries
+    monkeypatch.setenv("TE_HIP_PREFILL_ROWS", "1" if base + tokens <= 512 else "0")
     ref = A.attention_prefill(f16_dev(q_half), kc, vc, base_position=base)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)

@@ -151,13 +151,13 @@ def test_prefill_paired_gate_up_gemm_bits(ggml_type, monkeypatch):
     assert np.isfinite(outs[0]).all() and np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
-@pytest.mark.parametrize("batch,base", [(300, 3), (512, 0), (70, 5)])
+@pytest.mark.parametrize("batch,base", [(300, 300), (512, 0), (70, 5)])
 def test_prefill_attention_digits_in_kernel_bits(batch, base, monkeypatch):
     """The attention kernel's own digits of its output rows (the default)
     against fp32 rows and the separate digits launch (TE_HIP_PREFILL_DIGITS=0):
-    the same output bits.  300 and 512 rows after 3 / 0 cached positions take
-    the 128-row tile kernel (300: a ragged last tile), 70 after 5 the rows
-    kernel (at most 256 keys)."""
+    the same output bits.  300 rows after 300 cached positions take the
+    128-row tile kernel (600 keys; a ragged last tile), 512 after 0 and 70
+    after 5 the rows kernel (the fused step's choice up to 512 keys)."""
     layers, heads, kv_heads, head_dim, ffn = 2, 4, 2, 128, 512
     ctx = base + batch
     m = S.synthetic_model(94, 2, layers, heads, kv_heads, head_dim, ffn, 64, ctx, base)

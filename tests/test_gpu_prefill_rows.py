@@ -96,6 +96,38 @@ def test_rows_kernel_is_the_default_up_to_256_keys(monkeypatch, tokens, base, ro
     assert torch.equal(auto, rows if rows_default else tile)
 
 
+@pytest.mark.parametrize("tokens,base,rows_default", [(512, 0, True), (300, 213, False), (300, 212, True)])
+def test_rows_kernel_is_the_fused_step_default_up_to_512_keys(monkeypatch, tokens, base, rows_default):
+    """The fused step (fp32 queries, bias and RoPE on load) takes the rows
+    kernel by default up to base + tokens <= 512 keys: its output bits equal
+    the forced rows kernel's there, the forced tile kernel's past it."""
+    h, kv, d = 16, 2, 128
+    ctx = base + tokens
+    g = torch.Generator(device="cuda").manual_seed(tokens + base)
+    q = torch.randn((1, 1, tokens, h, d), generator=g, device="cuda") / math.sqrt(d)
+    k = torch.randn((1, 1, tokens, kv, d), generator=g, device="cuda")
+    v = torch.randn((1, 1, tokens, kv, d), generator=g, device="cuda")
+    kc0 = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+    vc0 = torch.randn((1, 1, ctx, kv, d), generator=g, device="cuda").half()
+    cos, sin = A.rope_table(ctx, d, 1e6)
+
+    def step(mode):
+        if mode is None:
+            monkeypatch.delenv("TE_HIP_PREFILL_ROWS", raising=False)
+        else:
+            monkeypatch.setenv("TE_HIP_PREFILL_ROWS", mode)
+        kc, vc = kc0.clone(), vc0.clone()
+        vt = A.value_t_buffer(1, 1, ctx, kv, d)
+        A.value_transpose(vc, vt, first_position=0, count=base)
+        out = A.prefill_step_vt(q, k, v, cos, sin, kc, vc, vt, base_position=base)
+        torch.cuda.synchronize()
+        return out
+
+    auto, rows, tile = step(None), step("1"), step("0")
+    assert not torch.equal(rows, tile)  # the two kernels round differently on these inputs
+    assert torch.equal(auto, rows if rows_default else tile)
+
+
 @pytest.mark.parametrize("seqs,layers,h,kv,d,tokens,base,bias", [
     (1, 1, 16, 2, 128, 512, 0, True),
     (2, 2, 14, 2, 64, 130, 37, True),

@@ -1434,11 +1434,17 @@ bool prefill_paired(size_t seqs, size_t layers, size_t tokens, size_t heads, int
 // 11.24 against 11.73, 512 12.92 against 13.17, 1,024 about twice as long.
 // At 512 keys its 256 workgroups of 146 KB LDS need every CU at once (one
 // measured launch started a workgroup 6.6 us late, in a second round), so
-// the choice stops at 256.  TE_HIP_PREFILL_ROWS=1 takes it for every launch
-// with one split, =0 never.
+// for fp16 queries the choice stops at 256.  With fp32 queries (the fused
+// step: bias and RoPE on load) the tile kernel's query preparation costs
+// more than the rows kernel's (which loads a group's queries once, into
+// LDS), so the fused step takes the rows kernel up to kRowsMaxKeysQ32:
+// its attention at 3B L = 512 15.3 against 23.5 us, the 3B Q4_0 512-token
+// prompt 12.81 -> 12.43-12.67 ms.  TE_HIP_PREFILL_ROWS=1 takes it for every
+// launch with one split, =0 never.
 constexpr size_t kRowsMaxKeys = 256;
+constexpr size_t kRowsMaxKeysQ32 = 512;
 
-bool prefill_rows(size_t tokens, size_t base_position, int splits) {
+bool prefill_rows(size_t tokens, size_t base_position, int splits, bool q32) {
     if (splits != 1) {
         return false;
     }
@@ -1446,7 +1452,7 @@ bool prefill_rows(size_t tokens, size_t base_position, int splits) {
     if (env != nullptr && (env[0] == '0' || env[0] == '1') && env[1] == '\0') {
         return env[0] == '1';
     }
-    return base_position + tokens <= kRowsMaxKeys;
+    return base_position + tokens <= (q32 ? kRowsMaxKeysQ32 : kRowsMaxKeys);
 }
 
 #ifdef TE_PREFILL_PHASES
@@ -1471,7 +1477,7 @@ te_status launch_prefill(PrefillArgs a, size_t seqs, size_t layers, size_t token
 #ifdef TE_PREFILL_PHASES
     a.phase_log = g_phase_log;
 #endif
-    if (prefill_rows(tokens, base_position, a.splits)) {
+    if (prefill_rows(tokens, base_position, a.splits, a.q32 != nullptr)) {
         const dim3 grid((unsigned)((tokens + RM - 1) / RM), (unsigned)heads, (unsigned)(seqs * layers));
         if (head_dim == 128) {
             prefill_rows_f16_kernel<128><<<grid, kThreads, 0, strm>>>(a);
